@@ -1,0 +1,93 @@
+// dfx_device.h — device-side helpers shared by the gfx950 kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dfx.h"
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+#define WAVE 64
+
+// Device super-block sizes (256 elements) of each storage type.
+#define SB_Q4_K 144
+#define SB_Q6_K 224
+#define SB_Q8_0 272
+#define SB_F16  512
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    half_t v = __builtin_bit_cast(half_t, h);
+    return (float)v;
+}
+__device__ __forceinline__ uint16_t f2h(float f) {
+    half_t v = (half_t)f;   // v_cvt_f16_f32: round to nearest even
+    return __builtin_bit_cast(uint16_t, v);
+}
+
+// 6-bit scale / min of sub-block j (0..7) of a Q4_K block (GGML get_scale_min_k4).
+__device__ __forceinline__ void q4k_scale_min(int j, const uint8_t * s, int & sc, int & m) {
+    if (j < 4) {
+        sc = s[j] & 63;
+        m  = s[j + 4] & 63;
+    } else {
+        sc = (s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4);
+        m  = (s[j + 4] >> 4)   | ((s[j]     >> 6) << 4);
+    }
+}
+
+// ---- wave reductions (64 lanes) ----
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
+// ---- converted activations (the GEMM input) ----
+// GGML's mul_mat converts activations to the weight's vec_dot_type; the buffer holds
+// that conversion so the GEMM can reproduce GGML's integer block dot products:
+//   q   f16 [M][K]        Q8_K / Q8_0: the int8 quants (exact in f16); F16: the values
+//   d   f32 [M][K/blk]    block scale (Q8_K: blk 256, f32; Q8_0: blk 32, the f16 scale)
+//   bs  f16 [M][K/16]     Q8_K only: sums of q over 16-element groups (GGML bsums)
+enum { CONV_Q8_K = 0, CONV_Q8_0 = 1, CONV_F16 = 2 };
+
+__host__ __device__ inline int conv_mode(int wtype) {
+    return (wtype == DFX_TYPE_Q4_K || wtype == DFX_TYPE_Q6_K) ? CONV_Q8_K
+         : (wtype == DFX_TYPE_Q8_0) ? CONV_Q8_0 : CONV_F16;
+}
+
+struct act_layout {
+    size_t q, d, bs, bytes;
+};
+__host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+__host__ __device__ inline act_layout act_layout_of(int mode, int64_t M, int64_t K) {
+    act_layout L;
+    L.q = 0;
+    L.d = align256((size_t)M * K * 2);
+    const size_t nd = mode == CONV_Q8_K ? (size_t)M * (K / 256) : mode == CONV_Q8_0 ? (size_t)M * (K / 32) : 0;
+    L.bs = align256(L.d + nd * 4);
+    const size_t nbs = mode == CONV_Q8_K ? (size_t)M * (K / 16) : 0;
+    L.bytes = align256(L.bs + nbs * 2);
+    return L;
+}
+
+// Error plumbing shared by the host-side launch wrappers.
+extern "C" void dfx_set_error(const char * fmt, ...);
+#define DFX_CHECK_LAUNCH(name)                                                     \
+    do {                                                                           \
+        hipError_t e_ = hipGetLastError();                                         \
+        if (e_ != hipSuccess) {                                                    \
+            dfx_set_error("%s: launch failed: %s", name, hipGetErrorString(e_));   \
+            return DFX_ERR_HIP;                                                    \
+        }                                                                          \
+    } while (0)

@@ -1,0 +1,304 @@
+// k_quant.hip — dequantisation, embedding gather and the activation-side
+// conversions that feed the MFMA GEMMs (RMSNorm, SwiGLU, plain convert).
+//
+// Activation conversion restates what GGML's mul_mat does to src1 before the
+// dot products: rows are converted to the weight's vec_dot_type (Q8_K blocks of
+// 256 for Q4_K/Q6_K, Q8_0 blocks of 32 for Q8_0, F16 for F16).  The GEMM then
+// consumes f16(d*q), so the activation rounding of the reference is reproduced
+// value for value (up to the final f16 rounding of d*q).
+#include "dfx_device.h"
+
+// ---------------------------------------------------------------------------
+// Dequantisation of one element of a device-layout row (bit-exact with GGML
+// dequantize_row_q4_K / _q6_K / _q8_0 / fp16_to_fp32: no FMA contraction, same
+// association order).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float dequant_elem(int type, const uint8_t * row, int64_t e) {
+#pragma clang fp contract(off)
+    const int64_t sb = e >> 8;
+    const int i = (int)(e & 255);
+    if (type == DFX_TYPE_Q4_K) {
+        const uint8_t * b = row + sb * SB_Q4_K;
+        const float d = h2f(*(const uint16_t *)(b + 0));
+        const float dmin = h2f(*(const uint16_t *)(b + 2));
+        const int g = i >> 6, r = i & 63, sub = 2 * g + (r >> 5), l = r & 31;
+        const uint8_t byte = b[16 + 32 * g + l];
+        const int q = (r < 32) ? (byte & 0x0F) : (byte >> 4);
+        int sc, m;
+        q4k_scale_min(sub, b + 4, sc, m);
+        const float d1 = d * (float)sc;
+        const float m1 = dmin * (float)m;
+        return d1 * (float)q - m1;
+    } else if (type == DFX_TYPE_Q6_K) {
+        const uint8_t * b = row + sb * SB_Q6_K;
+        const float d = h2f(*(const uint16_t *)(b + 208));
+        const int half = i >> 7, r = i & 127, quarter = r >> 5, l = r & 31;
+        const uint8_t lo = b[64 * half + l + 32 * (quarter & 1)];
+        const int low4 = (quarter < 2) ? (lo & 0x0F) : (lo >> 4);
+        const int hi2 = (b[128 + 32 * half + l] >> (2 * quarter)) & 3;
+        const int q = (low4 | (hi2 << 4)) - 32;
+        const float sc = (float)(int8_t)b[192 + (i >> 4)];
+        return (d * sc) * (float)q;
+    } else if (type == DFX_TYPE_Q8_0) {
+        const uint8_t * b = row + sb * SB_Q8_0;
+        const float d = h2f(*(const uint16_t *)(b + 2 * (i >> 5)));
+        return (float)(int8_t)b[16 + i] * d;
+    } else if (type == DFX_TYPE_F32) {
+        return *(const float *)(row + e * 4);
+    } else {  // F16
+        return h2f(*(const uint16_t *)(row + e * 2));
+    }
+}
+
+__device__ __forceinline__ int64_t dev_row_bytes(int type, int64_t n) {
+    const int64_t nsb = n >> 8;
+    switch (type) {
+        case DFX_TYPE_Q4_K: return nsb * SB_Q4_K;
+        case DFX_TYPE_Q6_K: return nsb * SB_Q6_K;
+        case DFX_TYPE_Q8_0: return nsb * SB_Q8_0;
+        case DFX_TYPE_F32: return n * 4;
+        default: return n * 2;
+    }
+}
+
+__global__ void k_dequant(int type, const uint8_t * w, int64_t n_rows, int64_t n_cols, float * out) {
+    const int64_t total = n_rows * n_cols;
+    const int64_t rb = dev_row_bytes(type, n_cols);
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = idx / n_cols, e = idx - r * n_cols;
+        out[idx] = dequant_elem(type, w + r * rb, e);
+    }
+}
+
+__global__ void k_embed(int type, const uint8_t * table, int64_t n_embd, const int32_t * tokens,
+                        int64_t M, float * x) {
+    const int64_t total = M * n_embd;
+    const int64_t rb = dev_row_bytes(type, n_embd);
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t m = idx / n_embd, e = idx - m * n_embd;
+        x[idx] = dequant_elem(type, table + (int64_t)tokens[m] * rb, e);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Conversion of one 256-element block held by a wave (lane owns elements
+// 4*lane .. 4*lane+3) into the activation buffer (layout in dfx_device.h).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void store_q4(uint16_t * dst, const uint16_t o[4]) {
+    const uint64_t packed = (uint64_t)o[0] | ((uint64_t)o[1] << 16) | ((uint64_t)o[2] << 32) | ((uint64_t)o[3] << 48);
+    *(uint64_t *)dst = packed;
+}
+
+// row m, block b (256 elements) of a [M][K] activation
+__device__ __forceinline__ void convert_block256(const float v[4], int lane, int mode, uint8_t * act,
+                                                 const act_layout & Lay, int64_t m, int64_t K, int64_t b) {
+#pragma clang fp contract(off)
+    uint16_t * q = (uint16_t *)(act + Lay.q) + m * K + b * 256 + 4 * lane;
+    uint16_t o[4];
+    if (mode == CONV_Q8_K) {
+        // GGML quantize_row_q8_K_ref: max = the signed value of the first element
+        // with the largest |x|; iscale = -127/max; q = min(127, nearest_int(iscale*x));
+        // d = 1/iscale; bsums over 16.  All-zero block -> d = 0, q = 0.
+        float amax = 0.0f, mx = 0.0f;
+        int idx = 0x7fffffff;
+        for (int j = 0; j < 4; j++) {
+            const float ax = fabsf(v[j]);
+            if (ax > amax) { amax = ax; mx = v[j]; idx = 4 * lane + j; }
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            const float oa = __shfl_xor(amax, off, WAVE);
+            const float om = __shfl_xor(mx, off, WAVE);
+            const int oi = __shfl_xor(idx, off, WAVE);
+            if (oa > amax || (oa == amax && oi < idx)) { amax = oa; mx = om; idx = oi; }
+        }
+        int qi[4] = {0, 0, 0, 0};
+        float d = 0.0f;
+        if (amax != 0.0f) {
+            // divisions through double round exactly once, whatever the fp32 divide lowering
+            const float iscale = (float)(-127.0 / (double)mx);
+            d = (float)(1.0 / (double)iscale);
+            for (int j = 0; j < 4; j++) qi[j] = min((int)__builtin_rintf(iscale * v[j]), 127);
+        }
+        for (int j = 0; j < 4; j++) o[j] = f2h((float)qi[j]);
+        store_q4(q, o);
+        int s = qi[0] + qi[1] + qi[2] + qi[3];
+        s += __shfl_xor(s, 1, WAVE);
+        s += __shfl_xor(s, 2, WAVE);
+        if ((lane & 3) == 0) ((uint16_t *)(act + Lay.bs))[m * (K / 16) + b * 16 + (lane >> 2)] = f2h((float)s);
+        if (lane == 0) ((float *)(act + Lay.d))[m * (K / 256) + b] = d;
+    } else if (mode == CONV_Q8_0) {
+        // GGML quantize_row_q8_0_ref over 32-element blocks (8 lanes each):
+        // d = amax/127, q = roundf(x * (1/d)), stored d rounded to f16.
+        float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        for (int off = 4; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, WAVE));
+        const float d = (float)((double)amax / 127.0);
+        const float id = d != 0.0f ? (float)(1.0 / (double)d) : 0.0f;
+        for (int j = 0; j < 4; j++) o[j] = f2h((float)(int)roundf(v[j] * id));
+        store_q4(q, o);
+        if ((lane & 7) == 0) ((float *)(act + Lay.d))[m * (K / 32) + b * 8 + (lane >> 3)] = h2f(f2h(d));
+    } else {
+        for (int j = 0; j < 4; j++) o[j] = f2h(v[j]);
+        store_q4(q, o);
+    }
+}
+
+// One wave per (row, 256-block).
+__global__ void k_act_convert(int mode, const float * x, int64_t M, int64_t K, uint8_t * act) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int64_t nb = K >> 8;
+    if (wid >= M * nb) return;
+    const int64_t m = wid / nb, b = wid - m * nb;
+    const act_layout Lay = act_layout_of(mode, M, K);
+    const float4 t = *(const float4 *)(x + m * K + b * 256 + 4 * lane);
+    const float v[4] = {t.x, t.y, t.z, t.w};
+    convert_block256(v, lane, mode, act, Lay, m, K, b);
+}
+
+// RMSNorm + weight + conversion; one 256-thread workgroup per row.
+// GGML ggml_compute_forward_rms_norm_f32: sum += (double)(x*x); mean = (float)(sum/K);
+// scale = 1.0f/sqrtf(mean + eps); y = x*scale; then ggml_mul by w.
+// Output row m normalises input row xmap[m] (or m).
+__global__ void __launch_bounds__(256) k_rmsnorm_convert(int mode, const float * x, const int32_t * xmap,
+                                                         const float * w, int64_t M, int64_t K, float eps,
+                                                         uint8_t * act) {
+#pragma clang fp contract(off)
+    __shared__ double red[4];
+    const int64_t m = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const float * xr = x + (int64_t)(xmap ? xmap[m] : m) * K;
+    double s = 0.0;
+    for (int64_t k = 4 * tid; k < K; k += 1024) {
+        const float4 t = *(const float4 *)(xr + k);
+        s += (double)(t.x * t.x);
+        s += (double)(t.y * t.y);
+        s += (double)(t.z * t.z);
+        s += (double)(t.w * t.w);
+    }
+    s = wave_sum_d(s);
+    if (lane == 0) red[wv] = s;
+    __syncthreads();
+    const double tot = red[0] + red[1] + red[2] + red[3];
+    const float mean = (float)(tot / (double)K);
+    // correctly rounded sqrtf and division (double rounding is exact for these ops)
+    const float root = (float)sqrt((double)(mean + eps));
+    const float scale = (float)(1.0 / (double)root);
+    const act_layout Lay = act_layout_of(mode, M, K);
+    const int64_t nb = K >> 8;
+    for (int64_t b = wv; b < nb; b += 4) {
+        const int64_t k = b * 256 + 4 * lane;
+        const float4 t = *(const float4 *)(xr + k);
+        const float4 g = *(const float4 *)(w + k);
+        const float v[4] = {(t.x * scale) * g.x, (t.y * scale) * g.y, (t.z * scale) * g.z, (t.w * scale) * g.w};
+        convert_block256(v, lane, mode, act, Lay, m, K, b);
+    }
+}
+
+// exp inside GGML ops (silu, soft_max) is taken correctly rounded: (float)exp((double)x).
+__device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
+
+// silu(gate) * up, then conversion.  gu row m = [gate F | up F]; one wave per (row, block).
+// GGML ggml_silu_f32: x / (1 + exp(-x)).
+__global__ void k_swiglu_convert(int mode, const float * gu, int64_t M, int64_t F, uint8_t * act) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int64_t nb = F >> 8;
+    if (wid >= M * nb) return;
+    const int64_t m = wid / nb, b = wid - m * nb;
+    const int64_t k = b * 256 + 4 * lane;
+    const float4 g = *(const float4 *)(gu + m * 2 * F + k);
+    const float4 u = *(const float4 *)(gu + m * 2 * F + F + k);
+    auto silu = [](float a) { return (float)((double)a / (double)(1.0f + exp_cr(-a))); };
+    const float v[4] = {silu(g.x) * u.x, silu(g.y) * u.y, silu(g.z) * u.z, silu(g.w) * u.w};
+    const act_layout Lay = act_layout_of(mode, M, F);
+    convert_block256(v, lane, mode, act, Lay, m, F, b);
+}
+
+// ---------------------------------------------------------------------------
+// C ABI launch wrappers
+// ---------------------------------------------------------------------------
+// Weight storage types the GEMMs read (activation conversion follows them).
+static bool dev_type_ok(int t) {
+    return t == DFX_TYPE_Q4_K || t == DFX_TYPE_Q6_K || t == DFX_TYPE_Q8_0 || t == DFX_TYPE_F16;
+}
+// Tables that are only gathered / dequantised may also stay F32.
+static bool table_type_ok(int t) { return dev_type_ok(t) || t == DFX_TYPE_F32; }
+
+extern "C" int dfx_dequant(int type, const void * w, int64_t n_rows, int64_t n_cols, float * out, void * stream) {
+    if (!table_type_ok(type) || n_cols <= 0 || n_rows <= 0 || (n_cols & 255)) {
+        dfx_set_error("dfx_dequant: unsupported type %d or shape %lldx%lld", type, (long long)n_rows, (long long)n_cols);
+        return DFX_ERR_UNSUPPORTED;
+    }
+    const int64_t total = n_rows * n_cols;
+    const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
+    hipLaunchKernelGGL(k_dequant, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, type,
+                       (const uint8_t *)w, n_rows, n_cols, out);
+    DFX_CHECK_LAUNCH("dfx_dequant");
+    return DFX_OK;
+}
+
+extern "C" int dfx_embed(int type, const void * table, int64_t n_embd, const int32_t * tokens, int64_t M,
+                         float * x, void * stream) {
+    if (!table_type_ok(type) || n_embd <= 0 || (n_embd & 255) || M < 0) {
+        dfx_set_error("dfx_embed: unsupported type %d or n_embd %lld", type, (long long)n_embd);
+        return DFX_ERR_UNSUPPORTED;
+    }
+    if (M == 0) return DFX_OK;
+    const int64_t total = M * n_embd;
+    const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
+    hipLaunchKernelGGL(k_embed, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, type,
+                       (const uint8_t *)table, n_embd, tokens, M, x);
+    DFX_CHECK_LAUNCH("dfx_embed");
+    return DFX_OK;
+}
+
+extern "C" size_t dfx_act_bytes(int wtype, int64_t M, int64_t K) {
+    return act_layout_of(conv_mode(wtype), M, K).bytes;
+}
+
+extern "C" int dfx_act_convert(int wtype, const float * x, int64_t M, int64_t K, void * act, void * stream) {
+    if (!dev_type_ok(wtype) || K <= 0 || (K & 255) || M < 0) {
+        dfx_set_error("dfx_act_convert: unsupported type %d or K %lld", wtype, (long long)K);
+        return DFX_ERR_UNSUPPORTED;
+    }
+    if (M == 0) return DFX_OK;
+    const int64_t waves = M * (K >> 8);
+    hipLaunchKernelGGL(k_act_convert, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
+                       conv_mode(wtype), x, M, K, (uint8_t *)act);
+    DFX_CHECK_LAUNCH("dfx_act_convert");
+    return DFX_OK;
+}
+
+int dfx_rmsnorm_convert_ex(int wtype, const float * x, const int32_t * xmap, const float * w, int64_t M, int64_t K,
+                           float eps, void * act, void * stream) {
+    if (!dev_type_ok(wtype) || K <= 0 || (K & 255) || M < 0) {
+        dfx_set_error("dfx_rmsnorm_convert: unsupported type %d or K %lld", wtype, (long long)K);
+        return DFX_ERR_UNSUPPORTED;
+    }
+    if (M == 0) return DFX_OK;
+    hipLaunchKernelGGL(k_rmsnorm_convert, dim3((unsigned)M), dim3(256), 0, (hipStream_t)stream,
+                       conv_mode(wtype), x, xmap, w, M, K, eps, (uint8_t *)act);
+    DFX_CHECK_LAUNCH("dfx_rmsnorm_convert");
+    return DFX_OK;
+}
+
+extern "C" int dfx_rmsnorm_convert(int wtype, const float * x, const float * w, int64_t M, int64_t K, float eps,
+                                   void * act, void * stream) {
+    return dfx_rmsnorm_convert_ex(wtype, x, nullptr, w, M, K, eps, act, stream);
+}
+
+extern "C" int dfx_swiglu_convert(int wtype, const float * gu, int64_t M, int64_t F, void * act, void * stream) {
+    if (!dev_type_ok(wtype) || F <= 0 || (F & 255) || M < 0) {
+        dfx_set_error("dfx_swiglu_convert: unsupported type %d or F %lld", wtype, (long long)F);
+        return DFX_ERR_UNSUPPORTED;
+    }
+    if (M == 0) return DFX_OK;
+    const int64_t waves = M * (F >> 8);
+    hipLaunchKernelGGL(k_swiglu_convert, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
+                       conv_mode(wtype), gu, M, F, (uint8_t *)act);
+    DFX_CHECK_LAUNCH("dfx_swiglu_convert");
+    return DFX_OK;
+}

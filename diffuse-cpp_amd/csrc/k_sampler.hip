@@ -1,0 +1,223 @@
+// k_sampler.hip — per-row vocab statistics and remask selection.
+//
+// Row statistics restate the reference's per-masked-position scan
+// (src/diffuse-sampler.cpp:34-57 compute_entropy, 241-252 top-1/top-2) as
+// workgroup reductions over a logits row:
+//   pass 1  argmax (strict >, lowest index on ties) and top-2
+//   pass 2  sum of expf(x - max)
+//   pass 3  entropy = -sum p*log_p over p = expf((x - max) - logf(sum)) > 1e-10
+// Rows are read three times; passes 2 and 3 hit the caches behind HBM.
+#include "dfx_device.h"
+
+#include <algorithm>
+
+#define RS_THREADS 1024
+
+struct top2_t { float best; int idx; float second; };
+
+__device__ __forceinline__ top2_t top2_merge(top2_t a, top2_t b) {
+    // second = max over every element except the argmax
+    if (b.best > a.best || (b.best == a.best && b.idx < a.idx)) {
+        top2_t r = {b.best, b.idx, fmaxf(b.second, a.best)};
+        return r;
+    }
+    top2_t r = {a.best, a.idx, fmaxf(a.second, b.best)};
+    return r;
+}
+
+__device__ __forceinline__ top2_t top2_shfl(top2_t v, int off) {
+    top2_t o;
+    o.best = __shfl_xor(v.best, off, WAVE);
+    o.idx = __shfl_xor(v.idx, off, WAVE);
+    o.second = __shfl_xor(v.second, off, WAVE);
+    return o;
+}
+
+__global__ void __launch_bounds__(RS_THREADS) k_row_stats(const float * __restrict__ logits, int64_t ld,
+                                                          const int32_t * __restrict__ rows, int V,
+                                                          dfx_row_stat * __restrict__ out) {
+#pragma clang fp contract(off)
+    __shared__ top2_t red_t[RS_THREADS / 64];
+    __shared__ double red_d[RS_THREADS / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int nw = RS_THREADS / 64;
+    const float * x = logits + (int64_t)rows[blockIdx.x] * ld;
+
+    // pass 1: per thread, elements in increasing index order
+    top2_t t = {-INFINITY, 0x7fffffff, -INFINITY};
+    const bool vec = ((V & 3) == 0) && ((((uintptr_t)x) & 15) == 0);
+    if (vec) {
+        for (int i = 4 * tid; i < V; i += 4 * RS_THREADS) {
+            const float4 v = *(const float4 *)(x + i);
+            const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (e[j] > t.best) { t.second = fmaxf(t.second, t.best); t.best = e[j]; t.idx = i + j; }
+                else t.second = fmaxf(t.second, e[j]);
+            }
+        }
+    } else {
+        for (int i = tid; i < V; i += RS_THREADS) {
+            const float e = x[i];
+            if (e > t.best) { t.second = fmaxf(t.second, t.best); t.best = e; t.idx = i; }
+            else t.second = fmaxf(t.second, e);
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) t = top2_merge(t, top2_shfl(t, off));
+    if (lane == 0) red_t[wv] = t;
+    __syncthreads();
+    t = red_t[0];
+    for (int w = 1; w < nw; w++) t = top2_merge(t, red_t[w]);
+    const float mx = t.best;
+    // The reference's running second starts at -1e30 and is replaced by the old best
+    // whenever a new best appears, so the sentinel survives only if index 0 is the argmax.
+    float second = t.second;
+    if (t.idx == 0) second = fmaxf(second, -1e30f);
+
+    // pass 2: sum of exp
+    double s = 0.0;
+    for (int i = tid; i < V; i += RS_THREADS) s += (double)(float)exp((double)(x[i] - mx));
+    s = wave_sum_d(s);
+    __syncthreads();
+    if (lane == 0) red_d[wv] = s;
+    __syncthreads();
+    double tot = 0.0;
+    for (int w = 0; w < nw; w++) tot += red_d[w];
+    const float log_sum = logf((float)tot);
+
+    // pass 3: entropy
+    double ent = 0.0;
+    for (int i = tid; i < V; i += RS_THREADS) {
+        const float lp = (x[i] - mx) - log_sum;
+        const float p = (float)exp((double)lp);
+        if (p > 1e-10f) ent -= (double)(p * lp);
+    }
+    ent = wave_sum_d(ent);
+    __syncthreads();
+    if (lane == 0) red_d[wv] = ent;
+    __syncthreads();
+    if (tid == 0) {
+        double e = 0.0;
+        for (int w = 0; w < nw; w++) e += red_d[w];
+        dfx_row_stat r;
+        r.token = t.idx;
+        r.best = mx;
+        r.second = second;
+        r.entropy = (float)e;
+        out[blockIdx.x] = r;
+    }
+}
+
+extern "C" int dfx_row_stats(const float * logits, int64_t ld, const int32_t * rows, int64_t n_rows, int64_t V,
+                             dfx_row_stat * out, void * stream) {
+    if (n_rows < 0 || V <= 0 || V > INT32_MAX || ld < V) {
+        dfx_set_error("dfx_row_stats: bad shape rows=%lld V=%lld ld=%lld", (long long)n_rows, (long long)V,
+                      (long long)ld);
+        return DFX_ERR_ARG;
+    }
+    if (n_rows == 0) return DFX_OK;
+    hipLaunchKernelGGL(k_row_stats, dim3((unsigned)n_rows), dim3(RS_THREADS), 0, (hipStream_t)stream, logits, ld,
+                       rows, (int)V, out);
+    DFX_CHECK_LAUNCH("dfx_row_stats");
+    return DFX_OK;
+}
+
+// Candidate records for the masked positions (src/diffuse-sampler.cpp:253-255):
+// confidence = top-1 logit, or top1 - top2 for TOPK_MARGIN.
+__global__ void k_make_candidates(const dfx_row_stat * __restrict__ st, const int32_t * __restrict__ pos, int n,
+                                  int margin, dfx_candidate * __restrict__ out) {
+#pragma clang fp contract(off)
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const dfx_row_stat s = st[i];
+    dfx_candidate c;
+    c.pos = pos[i];
+    c.token = s.token;
+    c.confidence = margin ? (s.best - s.second) : s.best;
+    c.entropy = s.entropy;
+    out[i] = c;
+}
+
+int dfx_make_candidates(const dfx_row_stat * stats, const int32_t * pos, int n, int margin, dfx_candidate * out,
+                        void * stream) {
+    if (n <= 0) return DFX_OK;
+    hipLaunchKernelGGL(k_make_candidates, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, stats,
+                       pos, n, margin, out);
+    DFX_CHECK_LAUNCH("dfx_make_candidates");
+    return DFX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Selection: bitonic sort of candidate indices by the policy key in one workgroup.
+// ---------------------------------------------------------------------------
+#define SEL_MAX 2048
+#define SEL_THREADS 1024
+
+// true if candidate a goes before candidate b
+__device__ __forceinline__ bool sel_before(const dfx_candidate & a, const dfx_candidate & b, bool by_entropy) {
+    if (by_entropy) {
+        if (a.entropy != b.entropy) return a.entropy < b.entropy;
+    } else {
+        if (a.confidence != b.confidence) return a.confidence > b.confidence;
+    }
+    return a.pos < b.pos;
+}
+
+__global__ void __launch_bounds__(SEL_THREADS) k_select(const dfx_candidate * __restrict__ cand, int n, int P,
+                                                        int by_entropy, float tau, int n_sched,
+                                                        int32_t * __restrict__ order, int32_t * __restrict__ n_unmask) {
+    __shared__ dfx_candidate c[SEL_MAX];
+    __shared__ int32_t ix[SEL_MAX];
+    __shared__ int n_easy;
+    const int tid = threadIdx.x;
+    if (tid == 0) n_easy = 0;
+    for (int i = tid; i < P; i += SEL_THREADS) {
+        if (i < n) c[i] = cand[i];
+        ix[i] = i;
+    }
+    __syncthreads();
+    // padding indices (>= n) always sort last
+    for (int k = 2; k <= P; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = tid; i < P; i += SEL_THREADS) {
+                const int l = i ^ j;
+                if (l > i) {
+                    const int a = ix[i], b = ix[l];
+                    bool b_first;
+                    if (a >= n) b_first = b < n || b < a;
+                    else if (b >= n) b_first = false;
+                    else b_first = sel_before(c[b], c[a], by_entropy != 0);
+                    const bool up = (i & k) == 0;
+                    if (up ? b_first : !b_first) { ix[i] = b; ix[l] = a; }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    int cnt = 0;
+    for (int i = tid; i < n; i += SEL_THREADS) {
+        order[i] = ix[i];
+        if (by_entropy && c[i].entropy < tau) cnt++;
+    }
+    if (cnt) atomicAdd(&n_easy, cnt);
+    __syncthreads();
+    if (tid == 0) {
+        int u = by_entropy ? max(n_sched, n_easy) : n_sched;
+        *n_unmask = min(u, n);
+    }
+}
+
+extern "C" int dfx_select(const dfx_candidate * cand, int n, int remasking, float tau, int n_sched, int32_t * order,
+                          int32_t * n_unmask, void * stream) {
+    // remasking ids: include/diffuse.h:37-43 (LOW_CONFIDENCE, RANDOM, ENTROPY_EXIT, MASKGIT_PLUS, TOPK_MARGIN)
+    if (n < 0 || n > SEL_MAX || remasking < 0 || remasking > 4 || remasking == 1) {
+        dfx_set_error("dfx_select: unsupported n=%d or remasking=%d", n, remasking);
+        return DFX_ERR_ARG;
+    }
+    int P = 1;
+    while (P < n) P <<= 1;
+    hipLaunchKernelGGL(k_select, dim3(1), dim3(SEL_THREADS), 0, (hipStream_t)stream, cand, n, P, remasking == 2 ? 1 : 0,
+                       tau, n_sched, order, n_unmask);
+    DFX_CHECK_LAUNCH("dfx_select");
+    return DFX_OK;
+}

@@ -1,0 +1,312 @@
+"""ctypes binding of the C ABI in include/dfx.h (libdiffuse.so).
+
+The Python-side binding a caller of the denoising path uses: device buffers,
+kernel entry points, and the model / context / generate API that mirrors
+diffuse-cpp's include/diffuse.h:71-91.  It loads the in-tree build
+(diffuse-cpp_amd/lib/libdiffuse.so) and raises if that library is missing:
+there is no CPU fallback.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libdiffuse.so")
+
+TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_K = 0, 1, 8, 12, 14, 15
+SCHED_COSINE, SCHED_LINEAR = 0, 1
+LOW_CONFIDENCE, RANDOM, ENTROPY_EXIT, MASKGIT_PLUS, TOPK_MARGIN = 0, 1, 2, 3, 4
+
+
+class DfxError(RuntimeError):
+    pass
+
+
+class Hparams(C.Structure):
+    _fields_ = [("n_vocab", C.c_uint32), ("n_embd", C.c_uint32), ("n_head", C.c_uint32),
+                ("n_head_kv", C.c_uint32), ("n_layer", C.c_uint32), ("n_ff", C.c_uint32),
+                ("n_ctx_max", C.c_uint32), ("rope_theta", C.c_float), ("rms_norm_eps", C.c_float),
+                ("mask_token_id", C.c_uint32), ("is_dream", C.c_int32)]
+
+
+class SamplerParams(C.Structure):
+    _fields_ = [("n_steps", C.c_int), ("temperature", C.c_float), ("schedule", C.c_int),
+                ("remasking", C.c_int), ("seed", C.c_uint32), ("entropy_threshold", C.c_float),
+                ("use_cache", C.c_int), ("cache_refresh", C.c_int), ("cache_keep_active", C.c_int)]
+
+    @classmethod
+    def make(cls, n_steps=32, temperature=0.0, schedule=SCHED_COSINE, remasking=LOW_CONFIDENCE,
+             seed=42, entropy_threshold=1.5, use_cache=True, cache_refresh=0, cache_keep_active=0):
+        # defaults of include/diffuse.h:45-55
+        return cls(n_steps, temperature, schedule, remasking, seed, entropy_threshold,
+                   1 if use_cache else 0, cache_refresh, cache_keep_active)
+
+
+class GenStats(C.Structure):
+    _fields_ = [("actual_steps", C.c_int), ("total_ms", C.c_double), ("forward_ms", C.c_double),
+                ("sample_ms", C.c_double), ("rows_per_step", C.c_int * 256),
+                ("unmasked_per_step", C.c_int * 256), ("step_ms", C.c_float * 256)]
+
+
+class SynthSpec(C.Structure):
+    _fields_ = [("n_vocab", C.c_uint32), ("n_embd", C.c_uint32), ("n_head", C.c_uint32),
+                ("n_head_kv", C.c_uint32), ("n_layer", C.c_uint32), ("n_ff", C.c_uint32),
+                ("n_ctx_max", C.c_uint32), ("rope_theta", C.c_float), ("rms_norm_eps", C.c_float),
+                ("mask_token_id", C.c_uint32), ("is_dream", C.c_int32), ("tied_output", C.c_int32),
+                ("seed", C.c_uint64), ("sigma", C.c_float), ("scheme", C.c_char_p),
+                ("n_threads", C.c_int32)]
+
+
+ROW_STAT = np.dtype([("token", "<i4"), ("best", "<f4"), ("second", "<f4"), ("entropy", "<f4")])
+CANDIDATE = np.dtype([("pos", "<i4"), ("token", "<i4"), ("confidence", "<f4"), ("entropy", "<f4")])
+
+# Architectures of the benchmark configurations (hparams as the converters write them).
+LLADA_8B = dict(n_vocab=126464, n_embd=4096, n_head=32, n_head_kv=32, n_layer=32, n_ff=12288,
+                rope_theta=500000.0, rms_norm_eps=1e-5, mask_token_id=126336, is_dream=0)
+DREAM_7B = dict(n_vocab=152064, n_embd=3584, n_head=28, n_head_kv=4, n_layer=28, n_ff=18944,
+                rope_theta=1000000.0, rms_norm_eps=1e-6, mask_token_id=151666, is_dream=1)
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise DfxError(f"{LIB_PATH} is not built (run `make -C diffuse-cpp_amd`)")
+        _lib = C.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+def _declare(L):
+    P, I64, I32, F, S = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_size_t
+    sig = {
+        "dfx_last_error": (C.c_char_p, []),
+        "dfx_device_count": (I32, [C.POINTER(C.c_int)]),
+        "dfx_malloc": (I32, [C.POINTER(C.c_void_p), S]),
+        "dfx_free": (I32, [P]),
+        "dfx_memcpy_h2d": (I32, [P, P, S, P]),
+        "dfx_memcpy_d2h": (I32, [P, P, S, P]),
+        "dfx_memcpy_d2d": (I32, [P, P, S, P]),
+        "dfx_memset": (I32, [P, I32, S, P]),
+        "dfx_stream_create": (I32, [C.POINTER(C.c_void_p)]),
+        "dfx_stream_destroy": (I32, [P]),
+        "dfx_stream_sync": (I32, [P]),
+        "dfx_timer_start": (I32, [C.POINTER(C.c_void_p), P]),
+        "dfx_timer_stop": (I32, [P, P, C.POINTER(C.c_float)]),
+        "dfx_device_row_bytes": (I64, [I32, I64]),
+        "dfx_device_type": (I32, [I32]),
+        "dfx_repack_rows": (I32, [I32, P, I64, I64, P]),
+        "dfx_dequant": (I32, [I32, P, I64, I64, P, P]),
+        "dfx_embed": (I32, [I32, P, I64, P, I64, P, P]),
+        "dfx_act_bytes": (S, [I32, I64, I64]),
+        "dfx_act_convert": (I32, [I32, P, I64, I64, P, P]),
+        "dfx_rmsnorm_convert": (I32, [I32, P, P, I64, I64, F, P, P]),
+        "dfx_swiglu_convert": (I32, [I32, P, I64, I64, P, P]),
+        "dfx_gemm_ws_bytes": (S, [I64, I64]),
+        "dfx_gemm": (I32, [I32, P, I64, I64, P, I64, P, P, P, P, P]),
+        "dfx_rope_store": (I32, [P, P, I64, I32, I32, I32, P, P, P, P, P]),
+        "dfx_attention": (I32, [P, P, P, I64, I64, I32, I32, I32, P, P]),
+        "dfx_row_stats": (I32, [P, I64, P, I64, I64, P, P]),
+        "dfx_select": (I32, [P, I32, I32, F, I32, P, P, P]),
+        "dfx_quantize_rows": (I32, [I32, P, I64, I64, P]),
+        "dfx_quantize_file": (I32, [C.c_char_p, C.c_char_p, C.c_char_p, I32]),
+        "dfx_synth_model": (I32, [C.c_char_p, C.POINTER(SynthSpec)]),
+        "dfx_model_load": (I32, [C.c_char_p, C.POINTER(C.c_void_p)]),
+        "dfx_model_free": (None, [P]),
+        "dfx_model_hparams": (I32, [P, C.POINTER(Hparams)]),
+        "dfx_context_new": (I32, [P, I32, C.POINTER(C.c_void_p)]),
+        "dfx_context_free": (None, [P]),
+        "dfx_forward": (I32, [P, P, I32, P]),
+        "dfx_generate": (I32, [P, P, I32, I32, C.POINTER(SamplerParams), P, C.POINTER(GenStats)]),
+        "dfx_generate_trace": (I32, [P, P, I32, I32, C.POINTER(SamplerParams), P, C.POINTER(GenStats), P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def check(rc, what=""):
+    if rc != 0:
+        raise DfxError(f"{what} failed ({rc}): {lib().dfx_last_error().decode()}")
+
+
+def _ptr(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class Buf:
+    """A device allocation; upload/download through numpy arrays."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        check(lib().dfx_malloc(C.byref(p), max(self.nbytes, 1)), "dfx_malloc")
+        self.ptr = p
+
+    @classmethod
+    def of(cls, arr):
+        arr = np.ascontiguousarray(arr)
+        b = cls(arr.nbytes)
+        b.upload(arr)
+        return b
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        check(lib().dfx_memcpy_h2d(self.ptr, _ptr(arr), arr.nbytes, None), "h2d")
+
+    def download(self, dtype, count=None, shape=None):
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = self.nbytes // dtype.itemsize
+        out = np.empty(count, dtype=dtype)
+        check(lib().dfx_memcpy_d2h(_ptr(out), self.ptr, out.nbytes, None), "d2h")
+        return out.reshape(shape) if shape is not None else out
+
+    def zero(self):
+        check(lib().dfx_memset(self.ptr, 0, self.nbytes, None), "memset")
+        sync()
+
+    def free(self):
+        if self.ptr:
+            lib().dfx_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def sync(stream=None):
+    check(lib().dfx_stream_sync(stream), "sync")
+
+
+def device_count():
+    n = C.c_int(0)
+    rc = lib().dfx_device_count(C.byref(n))
+    return n.value if rc == 0 else 0
+
+
+def act_parts(act_buf, wtype, M, K):
+    """Split a downloaded activation buffer (layout of dfx_act_bytes) into (q, d, bs)."""
+    raw = act_buf.download(np.uint8)
+
+    def a256(x):
+        return (x + 255) // 256 * 256
+    q = raw[:M * K * 2].view(np.float16).reshape(M, K)
+    d_off = a256(M * K * 2)
+    if wtype in (TYPE_Q4_K, TYPE_Q6_K):
+        nd, nbs = M * (K // 256), M * (K // 16)
+    elif wtype == TYPE_Q8_0:
+        nd, nbs = M * (K // 32), 0
+    else:
+        return q, None, None
+    d = raw[d_off:d_off + nd * 4].view(np.float32).reshape(M, -1)
+    bs_off = a256(d_off + nd * 4)
+    bs = raw[bs_off:bs_off + nbs * 2].view(np.float16).reshape(M, -1) if nbs else None
+    return q, d, bs
+
+
+def repack(gguf_type, raw, n_rows, n_cols):
+    """GGUF row bytes -> device layout bytes (host side)."""
+    rb = lib().dfx_device_row_bytes(gguf_type, n_cols)
+    if rb < 0:
+        raise DfxError(f"no device layout for type {gguf_type} with {n_cols} columns")
+    out = np.empty(rb * n_rows, dtype=np.uint8)
+    raw = np.ascontiguousarray(raw)
+    check(lib().dfx_repack_rows(gguf_type, _ptr(raw), n_rows, n_cols, _ptr(out)), "repack")
+    return out
+
+
+def quantize_rows(gguf_type, x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n_rows, n_cols = x.shape
+    from_block = {TYPE_F32: (1, 4), TYPE_F16: (1, 2), TYPE_Q8_0: (32, 34), TYPE_Q4_K: (256, 144),
+                  TYPE_Q6_K: (256, 210)}[gguf_type]
+    out = np.empty(n_rows * (n_cols // from_block[0]) * from_block[1], dtype=np.uint8)
+    check(lib().dfx_quantize_rows(gguf_type, _ptr(x), n_rows, n_cols, _ptr(out)), "quantize_rows")
+    return out
+
+
+def synth_model(path, arch, scheme="q4_k_m", seed=0, sigma=0.02, n_threads=0, tied_output=False,
+                n_ctx_max=4096):
+    spec = SynthSpec(arch["n_vocab"], arch["n_embd"], arch["n_head"], arch["n_head_kv"],
+                     arch["n_layer"], arch["n_ff"], n_ctx_max, arch["rope_theta"],
+                     arch["rms_norm_eps"], arch["mask_token_id"], arch.get("is_dream", 0),
+                     1 if tied_output else 0, seed, sigma, scheme.encode(), n_threads)
+    check(lib().dfx_synth_model(str(path).encode(), C.byref(spec)), "dfx_synth_model")
+
+
+def quantize_file(src, dst, scheme, n_threads=0):
+    check(lib().dfx_quantize_file(str(src).encode(), str(dst).encode(), scheme.encode(), n_threads),
+          "dfx_quantize_file")
+
+
+class Model:
+    def __init__(self, path):
+        h = C.c_void_p()
+        check(lib().dfx_model_load(str(path).encode(), C.byref(h)), "dfx_model_load")
+        self.h = h
+        hp = Hparams()
+        check(lib().dfx_model_hparams(h, C.byref(hp)), "hparams")
+        self.hparams = hp
+
+    def close(self):
+        if self.h:
+            lib().dfx_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Context:
+    def __init__(self, model, n_ctx):
+        h = C.c_void_p()
+        check(lib().dfx_context_new(model.h, n_ctx, C.byref(h)), "dfx_context_new")
+        self.h, self.model = h, model
+
+    def forward(self, tokens):
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        V = self.model.hparams.n_vocab
+        out = np.empty((len(tokens), V), dtype=np.float32)
+        check(lib().dfx_forward(self.h, _ptr(tokens), len(tokens), _ptr(out)), "dfx_forward")
+        return out
+
+    def generate(self, prompt, n_generate, params, stats=None):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.empty(n_generate, dtype=np.int32)
+        st = stats if stats is not None else GenStats()
+        check(lib().dfx_generate(self.h, _ptr(prompt), len(prompt), n_generate, C.byref(params),
+                                 _ptr(out), C.byref(st)), "dfx_generate")
+        return out
+
+    def generate_trace(self, prompt, n_generate, params, stats=None):
+        """(tokens, unmask_step): step at which each generated position was unmasked."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.empty(n_generate, dtype=np.int32)
+        steps = np.empty(n_generate, dtype=np.int32)
+        st = stats if stats is not None else GenStats()
+        check(lib().dfx_generate_trace(self.h, _ptr(prompt), len(prompt), n_generate, C.byref(params),
+                                       _ptr(out), C.byref(st), _ptr(steps)), "dfx_generate_trace")
+        return out, steps
+
+    def close(self):
+        if self.h:
+            lib().dfx_context_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,141 @@
+// api.cpp — the C form (dfx.h) and the C++ form (diffuse.h) of the public API.
+//
+// C++ entry points keep the reference's error behaviour: load failures are fatal
+// (DIFFUSE_DIE, src/diffuse-common.h:17-21 and src/diffuse-model.cpp:4-10, 74-80,
+// 92-95), diffuse_forward returns false after logging (src/diffuse-graph.cpp:331-345),
+// and a failed forward inside diffuse_generate is fatal (src/diffuse-sampler.cpp:152,
+// 169, 192).
+#include <cstdlib>
+#include <cstring>
+
+#include "engine.h"
+
+#define DIFFUSE_DIE(fmt, ...)                                              \
+    do {                                                                   \
+        fprintf(stderr, "[diffuse] FATAL: " fmt "\n", ##__VA_ARGS__);      \
+        exit(1);                                                           \
+    } while (0)
+
+// ---- C ABI ----
+extern "C" int dfx_model_load(const char * path, dfx_model ** out) {
+    if (!path || !out) {
+        dfx_set_error("dfx_model_load: null argument");
+        return DFX_ERR_ARG;
+    }
+    return engine_model_load(path, out);
+}
+
+extern "C" void dfx_model_free(dfx_model * m) { engine_model_free(m); }
+
+extern "C" int dfx_model_hparams(const dfx_model * m, dfx_hparams * o) {
+    if (!m || !o) return DFX_ERR_ARG;
+    const diffuse_hparams & h = m->hparams;
+    o->n_vocab = h.n_vocab;
+    o->n_embd = h.n_embd;
+    o->n_head = h.n_head;
+    o->n_head_kv = h.n_head_kv;
+    o->n_layer = h.n_layer;
+    o->n_ff = h.n_ff;
+    o->n_ctx_max = h.n_ctx_max;
+    o->rope_theta = h.rope_theta;
+    o->rms_norm_eps = h.rms_norm_eps;
+    o->mask_token_id = h.mask_token_id;
+    o->is_dream = m->is_dream ? 1 : 0;
+    return DFX_OK;
+}
+
+extern "C" int dfx_context_new(const dfx_model * m, int n_ctx, dfx_context ** out) {
+    if (!m || !out || n_ctx < 0) {
+        dfx_set_error("dfx_context_new: bad argument");
+        return DFX_ERR_ARG;
+    }
+    return engine_context_new(m, n_ctx, 1, out);
+}
+
+extern "C" void dfx_context_free(dfx_context * c) { engine_context_free(c); }
+
+extern "C" int dfx_forward(dfx_context * c, const int32_t * tokens, int n, float * logits_out) {
+    if (!c) return DFX_ERR_ARG;
+    return engine_forward(c, tokens, n, logits_out);
+}
+
+extern "C" int dfx_generate(dfx_context * c, const int32_t * prompt, int n_prompt, int n_generate,
+                            const dfx_sampler_params * p, int32_t * out, dfx_gen_stats * stats) {
+    if (!c || !p || (!prompt && n_prompt) || (!out && n_generate)) {
+        dfx_set_error("dfx_generate: null argument");
+        return DFX_ERR_ARG;
+    }
+    return engine_generate(c, prompt, n_prompt, n_generate, *p, out, stats, nullptr);
+}
+
+extern "C" int dfx_generate_trace(dfx_context * c, const int32_t * prompt, int n_prompt, int n_generate,
+                                  const dfx_sampler_params * p, int32_t * out, dfx_gen_stats * stats,
+                                  int32_t * unmask_step) {
+    if (!c || !p || (!prompt && n_prompt) || (!out && n_generate)) {
+        dfx_set_error("dfx_generate_trace: null argument");
+        return DFX_ERR_ARG;
+    }
+    return engine_generate(c, prompt, n_prompt, n_generate, *p, out, stats, nullptr, unmask_step);
+}
+
+// ---- C++ API (include/diffuse.h) ----
+diffuse_model * diffuse_model_load(const std::string & path, int /*n_threads*/) {
+    diffuse_model * m = nullptr;
+    if (engine_model_load(path, &m) != DFX_OK) DIFFUSE_DIE("%s", dfx_last_error());
+    return m;
+}
+
+void diffuse_model_free(diffuse_model * model) { engine_model_free(model); }
+
+const diffuse_hparams & diffuse_model_hparams(const diffuse_model * model) { return model->hparams; }
+
+diffuse_context * diffuse_context_new(const diffuse_model * model, int n_ctx, int n_threads) {
+    diffuse_context * c = nullptr;
+    if (engine_context_new(model, n_ctx, n_threads, &c) != DFX_OK)
+        DIFFUSE_DIE("failed to create context: %s", dfx_last_error());
+    return c;
+}
+
+void diffuse_context_free(diffuse_context * ctx) { engine_context_free(ctx); }
+
+bool diffuse_forward(diffuse_context * ctx, const int32_t * tokens, int n_tokens, float * logits_out) {
+    if (engine_forward(ctx, tokens, n_tokens, logits_out) != DFX_OK) {
+        DIFFUSE_LOG("forward failed: %s", dfx_last_error());
+        return false;
+    }
+    return true;
+}
+
+std::vector<int32_t> diffuse_generate(diffuse_context * ctx, const std::vector<int32_t> & prompt_tokens,
+                                      int n_generate, const diffuse_sampler_params & params,
+                                      diffuse_step_callback callback) {
+    dfx_sampler_params p;
+    p.n_steps = params.n_steps;
+    p.temperature = params.temperature;
+    p.schedule = (int)params.schedule;
+    p.remasking = (int)params.remasking;
+    p.seed = params.seed;
+    p.entropy_threshold = params.entropy_threshold;
+    p.use_cache = params.use_cache ? 1 : 0;
+    p.cache_refresh = params.cache_refresh;
+    p.cache_keep_active = params.cache_keep_active;
+    std::vector<int32_t> out((size_t)std::max(n_generate, 0));
+    const int rc = engine_generate(ctx, prompt_tokens.data(), (int)prompt_tokens.size(), n_generate, p, out.data(),
+                                   nullptr, callback ? &callback : nullptr);
+    if (rc != DFX_OK) DIFFUSE_DIE("generation failed: %s", dfx_last_error());
+    return out;
+}
+
+// The autoregressive path (src/ar-*.cpp) is not part of the denoising hot path;
+// the symbols exist so programs written against diffuse.h link.
+std::vector<int32_t> ar_generate(diffuse_context *, const std::vector<int32_t> &, int, const ar_sampler_params &,
+                                 ar_token_callback) {
+    DIFFUSE_LOG("ar_generate: the autoregressive path is not available in this build");
+    return {};
+}
+
+std::vector<int32_t> ar_speculative_generate(diffuse_context *, diffuse_context *, const std::vector<int32_t> &, int,
+                                             const ar_spec_params &, ar_token_callback, ar_spec_stats *) {
+    DIFFUSE_LOG("ar_speculative_generate: the autoregressive path is not available in this build");
+    return {};
+}

@@ -1,0 +1,486 @@
+// engine.cpp — forward pass and denoising loop on one gfx950 GPU.
+//
+// Forward (src/diffuse-graph.cpp:11-160 full, 395-593 cached): one HIP stream,
+// per layer
+//   rmsnorm+convert -> Q|K|V GEMM (+bias) -> RoPE + cache store -> attention over
+//   the cache -> convert -> O GEMM (+residual) -> rmsnorm+convert -> gate|up GEMM
+//   -> SwiGLU+convert -> down GEMM (+residual)
+// then the final norm and the vocab head for the rows whose logits are read.
+// The cached step runs the same sequence on the active rows only: their K/V are
+// scattered into the HBM-resident cache before attention, which then reads all
+// positions (src/diffuse-cache.h:124-140 update_kv + the [cached ‖ active] concat).
+//
+// Denoising loop (src/diffuse-sampler.cpp:60-370): host bookkeeping of seq /
+// is_masked / the active set, device row statistics + selection, and only the
+// per-candidate records come back to the host each step.
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <numeric>
+#include <random>
+
+#include "engine.h"
+
+namespace {
+
+#define TRY(x)                         \
+    do {                               \
+        const int rc_ = (x);           \
+        if (rc_ != DFX_OK) return rc_; \
+    } while (0)
+
+int hip_ok(hipError_t e, const char * what) {
+    if (e == hipSuccess) return DFX_OK;
+    dfx_set_error("%s: %s", what, hipGetErrorString(e));
+    return e == hipErrorOutOfMemory ? DFX_ERR_OOM : DFX_ERR_HIP;
+}
+
+struct dims {
+    int64_t d, F, V, L, H, Hkv, hd, dkv, nqkv;
+    explicit dims(const diffuse_hparams & hp) {
+        d = hp.n_embd; F = hp.n_ff; V = hp.n_vocab; L = hp.n_layer; H = hp.n_head; Hkv = hp.n_head_kv;
+        hd = d / H; dkv = hd * Hkv; nqkv = d + 2 * dkv;
+    }
+};
+
+void free_buffers(diffuse_context * c) {
+    void * bufs[] = {c->x, c->act, c->qkv, c->qr, c->att, c->gu, c->logits, c->kc, c->vc, c->rope_tab,
+                     c->d_tok, c->d_pos, c->d_hrows, c->d_hmap, c->d_srows, c->d_spos, c->ws, c->d_stats,
+                     c->d_cand, c->d_order, c->d_nun};
+    for (void * p : bufs)
+        if (p) hipFree(p);
+    if (c->h_pin) hipHostFree(c->h_pin);
+    c->x = c->qkv = c->qr = c->att = c->gu = c->logits = c->kc = c->vc = c->rope_tab = nullptr;
+    c->act = nullptr;
+    c->d_tok = c->d_pos = c->d_hrows = c->d_hmap = c->d_srows = c->d_spos = c->d_order = c->d_nun = nullptr;
+    c->ws = nullptr;
+    c->d_stats = nullptr;
+    c->d_cand = nullptr;
+    c->h_pin = nullptr;
+    c->cap = 0;
+}
+
+// NEOX rope angles, as GGML's rope cache: theta_0 = p, theta_{i+1} = theta_i *
+// powf(base, -2/n_dims); cos/sin by cosf/sinf (freq_scale 1, ext_factor 0,
+// attn_factor 1 as passed at src/diffuse-graph.cpp:76-79).
+void rope_table(int n_pos, int hd, float base, std::vector<float> & tab) {
+    const int half = hd / 2;
+    tab.resize((size_t)n_pos * half * 2);
+    const float theta_scale = powf(base, -2.0f / (float)hd);
+    for (int p = 0; p < n_pos; p++) {
+        float theta = (float)p;
+        for (int i = 0; i < half; i++) {
+            tab[((size_t)p * half + i) * 2 + 0] = cosf(theta);
+            tab[((size_t)p * half + i) * 2 + 1] = sinf(theta);
+            theta *= theta_scale;
+        }
+    }
+}
+
+int ensure_capacity(diffuse_context * c, int N) {
+    if (N <= c->cap) return DFX_OK;
+    free_buffers(c);
+    const dims D(c->model->hparams);
+    const int64_t n = N;
+    auto A = [&](void ** p, size_t bytes) { return hip_ok(hipMalloc(p, bytes ? bytes : 1), "context hipMalloc"); };
+    TRY(A((void **)&c->x, n * D.d * 4));
+    const int64_t kmax = std::max(D.d, D.F);
+    TRY(A((void **)&c->act, std::max({dfx_act_bytes(DFX_TYPE_Q4_K, n, kmax), dfx_act_bytes(DFX_TYPE_Q8_0, n, kmax),
+                                      dfx_act_bytes(DFX_TYPE_F16, n, kmax)})));
+    TRY(A((void **)&c->qkv, n * D.nqkv * 4));
+    TRY(A((void **)&c->qr, n * D.d * 4));
+    TRY(A((void **)&c->att, n * D.d * 4));
+    TRY(A((void **)&c->gu, n * 2 * D.F * 4));
+    TRY(A((void **)&c->logits, n * D.V * 4));
+    TRY(A((void **)&c->kc, D.L * n * D.dkv * 4));
+    TRY(A((void **)&c->vc, D.L * n * D.dkv * 4));
+    TRY(A((void **)&c->rope_tab, n * D.hd * 4));
+    TRY(A((void **)&c->d_tok, n * 4));
+    TRY(A((void **)&c->d_pos, n * 4));
+    TRY(A((void **)&c->d_hrows, n * 4));
+    TRY(A((void **)&c->d_hmap, n * 4));
+    TRY(A((void **)&c->d_srows, n * 4));
+    TRY(A((void **)&c->d_spos, n * 4));
+    c->ws_bytes = dfx_gemm_ws_bytes(n, std::max(D.nqkv, D.d));
+    TRY(A(&c->ws, c->ws_bytes));
+    TRY(A((void **)&c->d_stats, n * sizeof(dfx_row_stat)));
+    TRY(A((void **)&c->d_cand, n * sizeof(dfx_candidate)));
+    TRY(A((void **)&c->d_order, n * 4));
+    TRY(A((void **)&c->d_nun, 4));
+    TRY(hip_ok(hipHostMalloc((void **)&c->h_pin, n * 8 * 4, hipHostMallocDefault), "hipHostMalloc"));
+    // caches start at zero like diffuse_step_cache::init (src/diffuse-cache.h:43-49)
+    TRY(hip_ok(hipMemsetAsync(c->kc, 0, D.L * n * D.dkv * 4, c->stream), "memset"));
+    TRY(hip_ok(hipMemsetAsync(c->vc, 0, D.L * n * D.dkv * 4, c->stream), "memset"));
+    std::vector<float> tab;
+    rope_table(N, (int)D.hd, c->model->hparams.rope_theta, tab);
+    TRY(hip_ok(hipMemcpy(c->rope_tab, tab.data(), tab.size() * 4, hipMemcpyHostToDevice), "rope table upload"));
+    c->cap = N;
+    return DFX_OK;
+}
+
+// GEMMs of a projection group into out[M][g.n_out]; input rows already in x.
+int run_group(diffuse_context * c, const proj_group & g, const float * norm, int64_t M, int64_t K, float * out) {
+    const float eps = c->model->hparams.rms_norm_eps;
+    if (g.fused) {
+        TRY(dfx_rmsnorm_convert_ex(g.all.type, c->x, nullptr, norm, M, K, eps, c->act, c->stream));
+        return dfx_gemm_ex(g.all.type, g.all.data, g.n_out, K, c->act, M, g.bias, nullptr, out, g.n_out, nullptr,
+                           c->ws, c->ws_bytes, c->stream);
+    }
+    for (size_t i = 0; i < g.parts.size(); i++) {
+        const dev_matrix & p = g.parts[i];
+        TRY(dfx_rmsnorm_convert_ex(p.type, c->x, nullptr, norm, M, K, eps, c->act, c->stream));
+        TRY(dfx_gemm_ex(p.type, p.data, p.rows, K, c->act, M, g.bias ? g.bias + g.col_off[i] : nullptr, nullptr,
+                        out + g.col_off[i], g.n_out, nullptr, c->ws, c->ws_bytes, c->stream));
+    }
+    return DFX_OK;
+}
+
+// Enqueue one forward over the M rows in d_tok/d_pos, attending over keys
+// 0..n_keys-1 of the cache; logits for the n_head rows d_hrows go to logits[d_hmap].
+int forward_pass(diffuse_context * c, int M, int n_keys, int n_head) {
+    const diffuse_model & m = *c->model;
+    const dims D(m.hparams);
+    const float eps = m.hparams.rms_norm_eps;
+    TRY(dfx_embed(m.tok_embd.type, m.tok_embd.data, D.d, c->d_tok, M, c->x, c->stream));
+    for (int64_t il = 0; il < D.L; il++) {
+        const dev_layer & L = m.layers[il];
+        float * kc = c->kc + il * (int64_t)c->cap * D.dkv;
+        float * vc = c->vc + il * (int64_t)c->cap * D.dkv;
+        TRY(run_group(c, L.qkv, L.attn_norm, M, D.d, c->qkv));
+        TRY(dfx_rope_store(c->qkv, c->d_pos, M, (int)D.H, (int)D.Hkv, (int)D.hd, c->rope_tab, c->qr, kc, vc,
+                           c->stream));
+        TRY(dfx_attention(c->qr, kc, vc, M, n_keys, (int)D.H, (int)D.Hkv, (int)D.hd, c->att, c->stream));
+        TRY(dfx_act_convert(L.o.type, c->att, M, D.d, c->act, c->stream));
+        TRY(dfx_gemm_ex(L.o.type, L.o.data, D.d, D.d, c->act, M, nullptr, c->x, c->x, D.d, nullptr, c->ws,
+                        c->ws_bytes, c->stream));
+        TRY(run_group(c, L.gu, L.ffn_norm, M, D.d, c->gu));
+        TRY(dfx_swiglu_convert(L.down.type, c->gu, M, D.F, c->act, c->stream));
+        TRY(dfx_gemm_ex(L.down.type, L.down.data, D.d, D.F, c->act, M, nullptr, c->x, c->x, D.d, nullptr, c->ws,
+                        c->ws_bytes, c->stream));
+    }
+    if (n_head > 0) {
+        TRY(dfx_rmsnorm_convert_ex(m.output.type, c->x, c->d_hrows, m.output_norm, n_head, D.d, eps, c->act, c->stream));
+        TRY(dfx_gemm_ex(m.output.type, m.output.data, D.V, D.d, c->act, n_head, nullptr, nullptr, c->logits, D.V,
+                        c->d_hmap, nullptr, 0, c->stream));
+    }
+    return DFX_OK;
+}
+
+int upload_i32(diffuse_context * c, int32_t * dst, const int32_t * src, int n, int slot) {
+    if (n <= 0) return DFX_OK;
+    int32_t * stage = c->h_pin + (size_t)slot * c->cap;
+    memcpy(stage, src, (size_t)n * 4);
+    return hip_ok(hipMemcpyAsync(dst, stage, (size_t)n * 4, hipMemcpyHostToDevice, c->stream), "H2D");
+}
+
+// src/diffuse-sampler.cpp:12-31 (t * M_PI is a double product narrowed for cosf)
+int tokens_to_unmask(int step, int total_steps, int total_masked, int schedule) {
+    const float t0 = (float)step / total_steps;
+    const float t1 = (float)(step + 1) / total_steps;
+    float frac;
+    if (schedule == 0) {
+        const float cos0 = cosf(t0 * M_PI * 0.5f);
+        const float cos1 = cosf(t1 * M_PI * 0.5f);
+        frac = (cos0 - cos1) / cos0;
+    } else {
+        frac = 1.0f / (total_steps - step);
+    }
+    int n = (int)roundf(frac * total_masked);
+    if (n < 1 && total_masked > 0) n = 1;
+    return std::min(n, total_masked);
+}
+
+const char * remask_name(int r) {
+    return r == 2 ? "entropy_exit" : r == 0 ? "low_confidence" : r == 3 ? "maskgit_plus" : r == 4 ? "topk_margin"
+                                                                                               : "random";
+}
+
+}  // namespace
+
+int engine_context_new(const diffuse_model * m, int n_ctx, int n_threads, diffuse_context ** out) {
+    diffuse_context * c = new diffuse_context();
+    c->model = m;
+    c->n_ctx = n_ctx;
+    c->n_threads = n_threads;
+    int rc = hip_ok(hipStreamCreate(&c->stream), "hipStreamCreate");
+    if (rc == DFX_OK) rc = hip_ok(hipEventCreate(&c->ev0), "hipEventCreate");
+    if (rc == DFX_OK) rc = hip_ok(hipEventCreate(&c->ev1), "hipEventCreate");
+    if (rc == DFX_OK) rc = ensure_capacity(c, std::max(n_ctx, 1));
+    if (rc != DFX_OK) {
+        engine_context_free(c);
+        return rc;
+    }
+    *out = c;
+    return DFX_OK;
+}
+
+void engine_context_free(diffuse_context * c) {
+    if (!c) return;
+    if (c->stream) hipStreamSynchronize(c->stream);
+    free_buffers(c);
+    if (c->ev0) hipEventDestroy(c->ev0);
+    if (c->ev1) hipEventDestroy(c->ev1);
+    if (c->stream) hipStreamDestroy(c->stream);
+    delete c;
+}
+
+int engine_forward(diffuse_context * c, const int32_t * tokens, int n, float * logits_out) {
+    if (n <= 0 || !tokens || !logits_out) {
+        dfx_set_error("diffuse_forward: bad arguments");
+        return DFX_ERR_ARG;
+    }
+    const dims D(c->model->hparams);
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= c->model->tok_embd.rows) {
+            dfx_set_error("diffuse_forward: token %d out of range", tokens[i]);
+            return DFX_ERR_ARG;
+        }
+    TRY(ensure_capacity(c, n));
+    std::vector<int32_t> idx(n);
+    std::iota(idx.begin(), idx.end(), 0);
+    TRY(upload_i32(c, c->d_tok, tokens, n, 0));
+    TRY(upload_i32(c, c->d_pos, idx.data(), n, 1));
+    TRY(upload_i32(c, c->d_hrows, idx.data(), n, 2));
+    TRY(upload_i32(c, c->d_hmap, idx.data(), n, 3));
+    TRY(forward_pass(c, n, n, n));
+    TRY(hip_ok(hipMemcpyAsync(logits_out, c->logits, (size_t)n * D.V * 4, hipMemcpyDeviceToHost, c->stream), "D2H"));
+    return hip_ok(hipStreamSynchronize(c->stream), "forward");
+}
+
+int engine_generate(diffuse_context * c, const int32_t * prompt, int n_prompt, int n_generate,
+                    const dfx_sampler_params & p, int32_t * out, dfx_gen_stats * stats,
+                    const diffuse_step_callback * callback, int32_t * unmask_step) {
+    using clk = std::chrono::steady_clock;
+    const diffuse_model & md = *c->model;
+    const int V = (int)md.hparams.n_vocab;
+    const int mask_id = (int)md.hparams.mask_token_id;
+    const bool shift = md.is_dream;   // Dream reads logits of position max(i-1, 0)
+    const int N = n_prompt + n_generate;
+    if (n_prompt < 0 || n_generate < 0 || N <= 0 || p.n_steps < 0) {
+        dfx_set_error("diffuse_generate: bad arguments");
+        return DFX_ERR_ARG;
+    }
+    for (int i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= md.tok_embd.rows) {
+            dfx_set_error("diffuse_generate: prompt token %d out of range", prompt[i]);
+            return DFX_ERR_ARG;
+        }
+    if (mask_id < 0 || mask_id >= md.tok_embd.rows) {
+        dfx_set_error("diffuse_generate: mask token %d outside the embedding table", mask_id);
+        return DFX_ERR_FORMAT;
+    }
+    if (n_generate > 2048) {
+        dfx_set_error("diffuse_generate: n_generate %d exceeds the selection kernel's 2048", n_generate);
+        return DFX_ERR_UNSUPPORTED;
+    }
+    TRY(ensure_capacity(c, N));
+
+    std::vector<int32_t> seq(prompt, prompt + n_prompt);
+    seq.resize(N, mask_id);
+    std::vector<char> is_masked(N, 0);
+    for (int i = n_prompt; i < N; i++) is_masked[i] = 1;
+    int n_masked = n_generate;
+    std::mt19937 rng(p.seed);
+
+    const bool use_cache = p.use_cache != 0;
+    std::vector<int32_t> prev_seq(N, -1);
+    std::vector<int> last_changed(N, -1);
+    bool cache_init = false;
+    if (stats) memset(stats, 0, sizeof(*stats));
+    if (unmask_step)
+        for (int i = 0; i < n_generate; i++) unmask_step[i] = -1;
+
+    DIFFUSE_LOG("diffusion: %d steps, %d tokens to generate, scheduler=%s, cache=%s, refresh=%d, keep_active=%d",
+                p.n_steps, n_generate, remask_name(p.remasking), use_cache ? "ON" : "OFF", p.cache_refresh,
+                p.cache_keep_active);
+
+    double total_fwd = 0, total_sample = 0, total_sort = 0, total_unmask = 0;
+    int actual_steps = 0;
+    const auto gen_start = clk::now();
+    std::vector<int32_t> act, tok, hrows, hmap, srows, spos, order;
+    std::vector<dfx_candidate> cand;
+    std::vector<char> need(N);
+
+    for (int step = 0; step < p.n_steps && n_masked > 0; step++) {
+        actual_steps++;
+        const auto t0 = clk::now();
+        const bool force_full = !use_cache || !cache_init ||
+                                (p.cache_refresh > 0 && step > 0 && step % p.cache_refresh == 0);
+        bool full = force_full;
+        act.clear();
+        if (!force_full) {
+            // compute_active_set (src/diffuse-cache.h:79-116)
+            for (int i = 0; i < N; i++) {
+                const bool changed = seq[i] != prev_seq[i];
+                if (changed) last_changed[i] = step;
+                const bool recent = p.cache_keep_active > 0 && last_changed[i] >= 0 &&
+                                    (step - last_changed[i]) <= p.cache_keep_active;
+                if (changed || is_masked[i] || recent) act.push_back(i);
+            }
+            if ((int)act.size() >= N || act.empty()) full = true;
+        }
+        if (full) {
+            act.resize(N);
+            std::iota(act.begin(), act.end(), 0);
+        }
+        const int M = (int)act.size();
+        // rows whose logits the sampler reads this step (only masked positions, or
+        // their left neighbour for Dream); other rows skip the vocab head.
+        std::fill(need.begin(), need.end(), 0);
+        for (int i = 0; i < N; i++)
+            if (is_masked[i]) need[shift ? std::max(i - 1, 0) : i] = 1;
+        tok.resize(M);
+        hrows.clear();
+        hmap.clear();
+        for (int a = 0; a < M; a++) {
+            tok[a] = seq[act[a]];
+            if (need[act[a]]) {
+                hrows.push_back(a);
+                hmap.push_back(act[a]);
+            }
+        }
+        TRY(upload_i32(c, c->d_tok, tok.data(), M, 0));
+        TRY(upload_i32(c, c->d_pos, act.data(), M, 1));
+        TRY(upload_i32(c, c->d_hrows, hrows.data(), (int)hrows.size(), 2));
+        TRY(upload_i32(c, c->d_hmap, hmap.data(), (int)hmap.size(), 3));
+        TRY(hip_ok(hipEventRecord(c->ev0, c->stream), "event"));
+        TRY(forward_pass(c, M, N, (int)hrows.size()));
+        TRY(hip_ok(hipEventRecord(c->ev1, c->stream), "event"));
+        if (use_cache) {   // update_seq right after the forward (src/diffuse-sampler.cpp:154, 171, 194)
+            prev_seq = seq;
+            cache_init = true;
+        }
+        TRY(hip_ok(hipEventSynchronize(c->ev1), "forward"));
+        const auto t1 = clk::now();
+        const double fwd_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+        total_fwd += fwd_ms;
+
+        // ---- candidates (src/diffuse-sampler.cpp:222-270) ----
+        const auto t2 = clk::now();
+        srows.clear();
+        spos.clear();
+        for (int i = 0; i < N; i++)
+            if (is_masked[i]) {
+                srows.push_back(shift ? std::max(i - 1, 0) : i);
+                spos.push_back(i);
+            }
+        const int n_cand = (int)spos.size();
+        TRY(upload_i32(c, c->d_srows, srows.data(), n_cand, 4));
+        TRY(upload_i32(c, c->d_spos, spos.data(), n_cand, 5));
+        TRY(dfx_row_stats(c->logits, V, c->d_srows, n_cand, V, c->d_stats, c->stream));
+        const int n_sched = tokens_to_unmask(step, p.n_steps, n_masked, p.schedule);
+        int n_unmask = n_sched;
+        cand.resize(n_cand);
+        order.resize(n_cand);
+        if (p.temperature <= 0.0f) {
+            TRY(dfx_make_candidates(c->d_stats, c->d_spos, n_cand, p.remasking == 4 ? 1 : 0, c->d_cand, c->stream));
+            if (p.remasking != 1) {
+                TRY(dfx_select(c->d_cand, n_cand, p.remasking, p.entropy_threshold, n_sched, c->d_order, c->d_nun,
+                               c->stream));
+                TRY(hip_ok(hipMemcpyAsync(order.data(), c->d_order, (size_t)n_cand * 4, hipMemcpyDeviceToHost, c->stream), "D2H"));
+                TRY(hip_ok(hipMemcpyAsync(&n_unmask, c->d_nun, 4, hipMemcpyDeviceToHost, c->stream), "D2H"));
+            }
+            TRY(hip_ok(hipMemcpyAsync(cand.data(), c->d_cand, (size_t)n_cand * sizeof(dfx_candidate),
+                                      hipMemcpyDeviceToHost, c->stream), "D2H"));
+            TRY(hip_ok(hipStreamSynchronize(c->stream), "sampler"));
+        } else {
+            // Stochastic path stays on the host like the reference (src/diffuse-sampler.cpp:256-269).
+            std::vector<dfx_row_stat> st(n_cand);
+            std::vector<float> rowbuf((size_t)V);
+            TRY(hip_ok(hipMemcpyAsync(st.data(), c->d_stats, (size_t)n_cand * sizeof(dfx_row_stat),
+                                      hipMemcpyDeviceToHost, c->stream), "D2H"));
+            TRY(hip_ok(hipStreamSynchronize(c->stream), "sampler"));
+            std::vector<float> probs((size_t)V);
+            for (int j = 0; j < n_cand; j++) {
+                TRY(hip_ok(hipMemcpy(rowbuf.data(), c->logits + (size_t)srows[j] * V, (size_t)V * 4,
+                                     hipMemcpyDeviceToHost), "D2H"));
+                const float mx = *std::max_element(rowbuf.begin(), rowbuf.end());
+                float sum = 0.0f;
+                for (int v = 0; v < V; v++) {
+                    probs[v] = expf((rowbuf[v] - mx) / p.temperature);
+                    sum += probs[v];
+                }
+                for (int v = 0; v < V; v++) probs[v] /= sum;
+                std::discrete_distribution<int> dist(probs.begin(), probs.end());
+                const int s = dist(rng);
+                cand[j] = dfx_candidate{spos[j], s, probs[s], st[j].entropy};
+            }
+        }
+        const auto t3 = clk::now();
+        total_sample += std::chrono::duration<double, std::milli>(t3 - t2).count();
+
+        // ---- ordering (src/diffuse-sampler.cpp:277-308) ----
+        const auto t4 = clk::now();
+        std::vector<dfx_candidate> sorted(n_cand);
+        if (p.remasking == 1) {
+            std::shuffle(cand.begin(), cand.end(), rng);
+            sorted = cand;
+        } else if (p.temperature <= 0.0f) {
+            for (int j = 0; j < n_cand; j++) sorted[j] = cand[order[j]];
+        } else {
+            const bool by_ent = p.remasking == 2;
+            sorted = cand;
+            std::sort(sorted.begin(), sorted.end(), [by_ent](const dfx_candidate & a, const dfx_candidate & b) {
+                if (by_ent) {
+                    if (a.entropy != b.entropy) return a.entropy < b.entropy;
+                } else if (a.confidence != b.confidence) {
+                    return a.confidence > b.confidence;
+                }
+                return a.pos < b.pos;
+            });
+            if (by_ent) {
+                int n_easy = 0;
+                for (const auto & x : sorted) {
+                    if (x.entropy < p.entropy_threshold) n_easy++;
+                    else break;
+                }
+                n_unmask = std::min(std::max(n_sched, n_easy), n_cand);
+            }
+        }
+        const auto t5 = clk::now();
+        total_sort += std::chrono::duration<double, std::milli>(t5 - t4).count();
+
+        // ---- unmask (src/diffuse-sampler.cpp:316-323) ----
+        const auto t6 = clk::now();
+        int done = 0;
+        for (int j = 0; j < n_unmask && j < n_cand; j++) {
+            seq[sorted[j].pos] = sorted[j].token;
+            is_masked[sorted[j].pos] = 0;
+            if (unmask_step) unmask_step[sorted[j].pos - n_prompt] = step;
+            n_masked--;
+            done++;
+        }
+        const auto t7 = clk::now();
+        total_unmask += std::chrono::duration<double, std::milli>(t7 - t6).count();
+
+        DIFFUSE_LOG("  step %d/%d: unmasked %d tokens, %d remaining (fwd=%.1fms, active=%d/%d%s)", step + 1, p.n_steps,
+                    done, n_masked, fwd_ms, full ? N : M, N, !full ? " CACHED" : (force_full && step > 0) ? " REFRESH" : "");
+        if (stats && step < 256) {
+            stats->rows_per_step[step] = M;
+            stats->unmasked_per_step[step] = done;
+            stats->step_ms[step] = (float)fwd_ms;
+        }
+        if (callback && *callback) (*callback)(step + 1, p.n_steps, seq);
+    }
+
+    const double gen_ms = std::chrono::duration<double, std::milli>(clk::now() - gen_start).count();
+    const double overhead = gen_ms - total_fwd - total_sample - total_sort - total_unmask;
+    const int as = std::max(actual_steps, 1);
+    DIFFUSE_LOG("=== TIMING BREAKDOWN (%d steps, cache=%s) ===", actual_steps, use_cache ? "ON" : "OFF");
+    DIFFUSE_LOG("  forward:   %8.1f ms  (%5.1f%%)  avg=%.1f ms/step", total_fwd, 100.0 * total_fwd / gen_ms, total_fwd / as);
+    DIFFUSE_LOG("  sampling:  %8.1f ms  (%5.1f%%)  avg=%.1f ms/step", total_sample, 100.0 * total_sample / gen_ms,
+                total_sample / as);
+    DIFFUSE_LOG("  sorting:   %8.1f ms  (%5.1f%%)", total_sort, 100.0 * total_sort / gen_ms);
+    DIFFUSE_LOG("  unmask:    %8.1f ms  (%5.1f%%)", total_unmask, 100.0 * total_unmask / gen_ms);
+    DIFFUSE_LOG("  overhead:  %8.1f ms  (%5.1f%%)", overhead, 100.0 * overhead / gen_ms);
+    DIFFUSE_LOG("  TOTAL:     %8.1f ms  (%.2f tok/s)", gen_ms, 1000.0 * n_generate / gen_ms);
+    if (stats) {
+        stats->actual_steps = actual_steps;
+        stats->total_ms = gen_ms;
+        stats->forward_ms = total_fwd;
+        stats->sample_ms = total_sample + total_sort + total_unmask;
+    }
+    memcpy(out, seq.data() + n_prompt, (size_t)n_generate * 4);
+    return DFX_OK;
+}

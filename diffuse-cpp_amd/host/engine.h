@@ -1,0 +1,106 @@
+// engine.h — internal structures of the gfx950 engine behind diffuse.h / dfx.h.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "dfx.h"
+#include "diffuse.h"
+
+#define DIFFUSE_LOG(fmt, ...) fprintf(stderr, "[diffuse] " fmt "\n", ##__VA_ARGS__)
+
+// Internal kernel entry points with row maps (k_gemm.hip, k_quant.hip, k_sampler.hip).
+int dfx_gemm_ex(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M, const float * bias,
+                const float * residual, float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes,
+                void * stream);
+int dfx_rmsnorm_convert_ex(int wtype, const float * x, const int32_t * xmap, const float * w, int64_t M, int64_t K,
+                           float eps, void * act, void * stream);
+int dfx_make_candidates(const dfx_row_stat * stats, const int32_t * pos, int n, int margin, dfx_candidate * out,
+                        void * stream);
+extern "C" void dfx_set_error(const char * fmt, ...);
+
+// A weight matrix in the device layout of dfx.h: rows x cols, rows of super-blocks.
+struct dev_matrix {
+    int       type = -1;          // storage type (DFX_TYPE_*)
+    int64_t   rows = 0, cols = 0;
+    uint8_t * data = nullptr;
+};
+
+// Matrices that read the same activations (Q|K|V, gate|up), stacked by rows in
+// one allocation.  When every part has the same type one GEMM covers them all.
+struct proj_group {
+    std::vector<dev_matrix> parts;
+    std::vector<int64_t>    col_off;    // output column of each part
+    int64_t                 n_out = 0;
+    bool                    fused = false;
+    dev_matrix              all;        // valid when fused
+    float *                 bias = nullptr;   // [n_out] f32 or null
+};
+
+struct dev_layer {
+    float *    attn_norm = nullptr;   // f32 [n_embd]
+    float *    ffn_norm = nullptr;
+    proj_group qkv;                   // output [q | k | v]
+    dev_matrix o;
+    proj_group gu;                    // output [gate | up]
+    dev_matrix down;
+};
+
+struct diffuse_model {
+    diffuse_hparams hparams;
+    std::string     model_type;
+    bool            is_dream = false;
+    dev_matrix      tok_embd;        // gather table (F32 tables stay F32)
+    dev_matrix      output;          // vocab head in GEMM layout
+    float *         output_norm = nullptr;
+    std::vector<dev_layer> layers;
+    std::vector<void *>    allocs;
+    size_t          device_bytes = 0;
+};
+
+struct diffuse_context {
+    const diffuse_model * model = nullptr;
+    int          n_ctx = 0;
+    int          n_threads = 1;
+    hipStream_t  stream = nullptr;
+    int          cap = 0;            // rows the device buffers hold
+
+    float *      x = nullptr;        // [cap][d]       residual stream
+    uint8_t *    act = nullptr;      // converted GEMM input for up to cap rows of max(d, F)
+    float *      qkv = nullptr;      // [cap][d + 2 dkv]
+    float *      qr = nullptr;       // [cap][d]       roped queries
+    float *      att = nullptr;      // [cap][d]
+    float *      gu = nullptr;       // [cap][2F]
+    float *      logits = nullptr;   // [cap][V]       per position
+    float *      kc = nullptr;       // [L][cap][dkv]  inter-step cache
+    float *      vc = nullptr;
+    float *      rope_tab = nullptr; // [cap][hd/2][2]
+    int32_t *    d_tok = nullptr;    // [cap] tokens of this pass
+    int32_t *    d_pos = nullptr;    // [cap] positions of this pass
+    int32_t *    d_hrows = nullptr;  // [cap] pass rows that need logits
+    int32_t *    d_hmap = nullptr;   // [cap] logits row of each of them
+    int32_t *    d_srows = nullptr;  // [cap] logits rows scanned by the sampler
+    int32_t *    d_spos = nullptr;   // [cap] masked position of each scanned row
+    void *       ws = nullptr;       // split-K workspace
+    size_t       ws_bytes = 0;
+    dfx_row_stat *  d_stats = nullptr;
+    dfx_candidate * d_cand = nullptr;
+    int32_t *    d_order = nullptr;
+    int32_t *    d_nun = nullptr;
+    int32_t *    h_pin = nullptr;    // pinned staging, 8 * cap int32
+    hipEvent_t   ev0 = nullptr, ev1 = nullptr;
+};
+
+// model.cpp
+int  engine_model_load(const std::string & path, diffuse_model ** out);
+void engine_model_free(diffuse_model * m);
+
+// engine.cpp
+int  engine_context_new(const diffuse_model * m, int n_ctx, int n_threads, diffuse_context ** out);
+void engine_context_free(diffuse_context * c);
+int  engine_forward(diffuse_context * c, const int32_t * tokens, int n, float * logits_out);
+int  engine_generate(diffuse_context * c, const int32_t * prompt, int n_prompt, int n_generate,
+                     const dfx_sampler_params & p, int32_t * out, dfx_gen_stats * stats,
+                     const diffuse_step_callback * callback, int32_t * unmask_step = nullptr);

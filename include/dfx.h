@@ -1,0 +1,231 @@
+/*
+ * dfx.h — C ABI of the MI355X (gfx950) denoising path.
+ *
+ * Plain C types only: device pointers, sizes, an opaque stream handle
+ * (hipStream_t passed as void*, NULL = the library's default stream).
+ * Every entry point returns 0 on success or a negative DFX_ERR_* code;
+ * dfx_last_error() gives the message of the most recent failure on the
+ * calling thread.  No entry point allocates device memory except the ones
+ * named *_alloc / *_new / *_load.
+ *
+ * Two levels:
+ *   1. Kernel entry points (dfx_dequant ... dfx_select): one HIP kernel (or a
+ *      fixed short sequence) on caller-owned device buffers.  Each replaces a
+ *      GGML CPU op of the reference graph, cited per function.
+ *   2. Model / context entry points (dfx_model_load ... dfx_generate): the
+ *      C form of diffuse-cpp's public API (include/diffuse.h:71-91), for FFI
+ *      callers that cannot bind C++ (std::string / std::vector / std::function).
+ *      The C++ API in diffuse.h is implemented on top of these.
+ */
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status ---- */
+#define DFX_OK               0
+#define DFX_ERR_ARG         -1   /* bad argument / shape */
+#define DFX_ERR_UNSUPPORTED -2   /* tensor type or shape the kernels do not handle */
+#define DFX_ERR_HIP         -3   /* HIP runtime error */
+#define DFX_ERR_IO          -4   /* file could not be opened / read */
+#define DFX_ERR_FORMAT      -5   /* malformed GGUF or missing key / tensor */
+#define DFX_ERR_OOM         -6   /* device allocation failed */
+
+/* ---- tensor types: GGML ids, as stored in GGUF ---- */
+enum {
+    DFX_TYPE_F32  = 0,
+    DFX_TYPE_F16  = 1,
+    DFX_TYPE_Q8_0 = 8,
+    DFX_TYPE_Q4_K = 12,
+    DFX_TYPE_Q6_K = 14,
+    DFX_TYPE_Q8_K = 15,
+};
+
+const char * dfx_last_error(void);
+
+/* ---- device plumbing (lets FFI callers run kernels without another runtime) ---- */
+int dfx_device_count(int * n);
+int dfx_malloc(void ** ptr, size_t bytes);
+int dfx_free(void * ptr);
+int dfx_memcpy_h2d(void * dst, const void * src, size_t bytes, void * stream);
+int dfx_memcpy_d2h(void * dst, const void * src, size_t bytes, void * stream);
+int dfx_memcpy_d2d(void * dst, const void * src, size_t bytes, void * stream);
+int dfx_memset(void * dst, int value, size_t bytes, void * stream);
+int dfx_stream_create(void ** stream);
+int dfx_stream_destroy(void * stream);
+int dfx_stream_sync(void * stream);
+/* Elapsed ms between two points on a stream: start records, stop records + waits. */
+int dfx_timer_start(void ** timer, void * stream);
+int dfx_timer_stop(void * timer, void * stream, float * ms);
+
+/* ---- device weight layout ----
+ * Weights live in HBM as rows of 256-element super-blocks, each 16-byte aligned:
+ *   Q4_K  144 B  GGML block_q4_K as is                      {d, dmin, scales[12], qs[128]}
+ *   Q6_K  224 B  GGML block_q6_K (210 B) + 14 zero bytes    {ql[128], qh[64], scales[16], d, pad}
+ *   Q8_0  272 B  eight GGML block_q8_0 regrouped            {d[8], qs[8][32]}
+ *   F16   512 B  256 halves
+ * dfx_repack_rows converts GGUF bytes (n_rows x n_cols, GGML layout) into this
+ * layout on the host; F32 is stored as F16.  n_cols must be a multiple of 256.
+ */
+int64_t dfx_device_row_bytes(int type, int64_t n_cols);   /* -1 if unsupported */
+int     dfx_device_type(int gguf_type);                   /* storage type used for a GGUF type */
+int dfx_repack_rows(int gguf_type, const void * src, int64_t n_rows, int64_t n_cols, void * dst);
+
+/* ---- kernel entry points ---- */
+
+/* Dequantise n_rows x n_cols of a device-layout weight to f32 (bit-exact with
+ * GGML dequantize_row_*; used by get_rows at src/diffuse-graph.cpp:43). */
+int dfx_dequant(int type, const void * w, int64_t n_rows, int64_t n_cols, float * out, void * stream);
+
+/* Embedding gather: x[m][:] = dequant(table row tokens[m]) as f32
+ * (ggml_get_rows, src/diffuse-graph.cpp:43, 197, 433). */
+int dfx_embed(int type, const void * table, int64_t n_embd, const int32_t * tokens, int64_t M,
+              float * x, void * stream);
+
+/* Activation conversion to the weight's vec_dot_type, the way GGML's mul_mat
+ * converts src1 before its dot products (Q8_K blocks of 256 for Q4_K/Q6_K, Q8_0
+ * blocks of 32 for Q8_0, F16 for F16).  The result goes to an activation buffer
+ * of dfx_act_bytes(wtype, M, K) bytes:
+ *   q   f16 [M][K]      int8 quants as exact f16 integers (F16: the f16 values)
+ *   d   f32 [M][K/blk]  block scales (Q8_K: blk 256; Q8_0: blk 32, the f16 scale)
+ *   bs  f16 [M][K/16]   Q8_K only: sums of q over 16 elements
+ * each part starting at a 256-byte boundary, in this order. */
+size_t dfx_act_bytes(int wtype, int64_t M, int64_t K);
+int dfx_act_convert(int wtype, const float * x, int64_t M, int64_t K, void * act, void * stream);
+
+/* y = rms_norm(x) * w, then converted as dfx_act_convert (src/diffuse-graph.cpp:51-58,
+ * 127-134, 146-153). */
+int dfx_rmsnorm_convert(int wtype, const float * x, const float * w, int64_t M, int64_t K, float eps,
+                        void * act, void * stream);
+
+/* s = silu(g) * u converted for the down projection (src/diffuse-graph.cpp:136-139).
+ * gu is the [M][2F] output of the fused gate|up GEMM: row m holds gate then up. */
+int dfx_swiglu_convert(int wtype, const float * gu, int64_t M, int64_t F, void * act, void * stream);
+
+/* GEMM on MFMA (src/diffuse-graph.cpp:61-63, 122, 136-140, 154):
+ *   y[m][n] = sum_k x[m][k] * W[n][k]  (+ bias[n])  (+ residual[m][n])
+ * act: the converted activations of x (dfx_*_convert with the same wtype);
+ * W: device-layout [N][K]; y f32 [M][N].  For Q4_K / Q6_K / Q8_0 the result
+ * equals GGML's integer block dot products scaled and summed in K order, i.e. the
+ * CPU mul_mat value for value.  residual may alias y (in-place residual add).
+ * ws: split-K workspace of dfx_gemm_ws_bytes(M, N) bytes or NULL (used by F16). */
+size_t dfx_gemm_ws_bytes(int64_t M, int64_t N);
+int dfx_gemm(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
+             const float * bias, const float * residual, float * y, void * ws, void * stream);
+
+/* NEOX RoPE + cache store (src/diffuse-graph.cpp:71-79, 466-469; cache layout
+ * src/diffuse-cache.h:23-26 but at n_head_kv width — the GQA repeat of 84-95 is
+ * index math in the attention kernel).  qkv: [M][(H + 2*Hkv)*hd] f32 (Q | K | V);
+ * pos[M] absolute positions; tab: [n_pos][hd/2][cos, sin] f32.
+ * Writes q_out [M][H][hd] and kc/vc[pos][Hkv][hd]. */
+int dfx_rope_store(const float * qkv, const int32_t * pos, int64_t M, int H, int Hkv, int hd,
+                   const float * tab, float * q_out, float * kc, float * vc, void * stream);
+
+/* Bidirectional attention, no mask (src/diffuse-graph.cpp:97-119 / 528-553):
+ * out[m][h*hd + j] = sum_n softmax_n(q_m . k_n / sqrt(hd)) * v_n[j], keys 0..n_keys-1
+ * of the cache, query head h reads KV head h / (H/Hkv). */
+int dfx_attention(const float * q, const float * kc, const float * vc, int64_t M, int64_t n_keys,
+                  int H, int Hkv, int hd, float * out, void * stream);
+
+/* Per-row sampler statistics over logits rows (src/diffuse-sampler.cpp:34-57, 241-252):
+ * argmax (strict >, lowest index on ties), top-1 and top-2 values and entropy.
+ * rows[i] selects row rows[i] of the [*][ld] logits matrix. */
+typedef struct {
+    int32_t token;       /* argmax */
+    float   best;        /* top-1 logit */
+    float   second;      /* top-2 logit as the reference loop defines it */
+    float   entropy;     /* -sum p log p over p > 1e-10 */
+} dfx_row_stat;
+int dfx_row_stats(const float * logits, int64_t ld, const int32_t * rows, int64_t n_rows, int64_t V,
+                  dfx_row_stat * out, void * stream);
+
+/* Remask selection (src/diffuse-sampler.cpp:277-305): orders n candidates by the
+ * policy's key (ENTROPY_EXIT: entropy ascending; LOW_CONFIDENCE / MASKGIT_PLUS:
+ * top-1 logit descending; TOPK_MARGIN: top1-top2 descending), ties by position
+ * ascending.  Writes order[0..n) (candidate indices) and *n_unmask = the count to
+ * unmask (schedule count n_sched, or max(n_sched, #entropy < tau) for ENTROPY_EXIT,
+ * capped at n).  n <= 2048. */
+typedef struct { int32_t pos; int32_t token; float confidence; float entropy; } dfx_candidate;
+int dfx_select(const dfx_candidate * cand, int n, int remasking, float tau, int n_sched,
+               int32_t * order, int32_t * n_unmask, void * stream);
+
+/* ---- weight encoding, quantizer and synthetic models (host side) ---- */
+
+/* Encode n_rows x n_cols f32 into GGUF blocks of `type` (Q4_K, Q6_K, Q8_0, F16, F32). */
+int dfx_quantize_rows(int type, const float * src, int64_t n_rows, int64_t n_cols, void * dst);
+
+/* diffuse-quantize (tools/quantize.cpp:126-357): scheme "q4_k_m", "q8_0", "q6_k" or "f16",
+ * with the reference's per-tensor type mixture and keep rules. */
+int dfx_quantize_file(const char * in_path, const char * out_path, const char * scheme, int n_threads);
+
+/* Deterministic random-init model written as GGUF with the converters' keys and tensor
+ * names: weights sigma*N(0,1) drawn per tensor from `seed`, rounded to f16, then
+ * converted with `scheme`; norm weights 1.0; Dream adds Q/K/V biases. */
+typedef struct {
+    uint32_t    n_vocab, n_embd, n_head, n_head_kv, n_layer, n_ff, n_ctx_max;
+    float       rope_theta, rms_norm_eps;
+    uint32_t    mask_token_id;
+    int32_t     is_dream;      /* model_type "dream" (+ Q/K/V biases), else "llada" */
+    int32_t     tied_output;   /* omit output.weight (lm_head tied to token_embd) */
+    uint64_t    seed;
+    float       sigma;
+    const char * scheme;
+    int32_t     n_threads;     /* 0 = hardware threads, at most 16 */
+} dfx_synth_spec;
+int dfx_synth_model(const char * path, const dfx_synth_spec * spec);
+
+/* ---- model / context (C form of include/diffuse.h) ---- */
+typedef struct diffuse_model   dfx_model;
+typedef struct diffuse_context dfx_context;
+
+typedef struct {
+    uint32_t n_vocab, n_embd, n_head, n_head_kv, n_layer, n_ff, n_ctx_max;
+    float    rope_theta, rms_norm_eps;
+    uint32_t mask_token_id;
+    int32_t  is_dream;
+} dfx_hparams;
+
+/* remasking / schedule ids follow the enum order of include/diffuse.h:32-43 */
+typedef struct {
+    int      n_steps;
+    float    temperature;
+    int      schedule;
+    int      remasking;
+    uint32_t seed;
+    float    entropy_threshold;
+    int      use_cache;
+    int      cache_refresh;
+    int      cache_keep_active;
+} dfx_sampler_params;
+
+typedef struct {
+    int    actual_steps;
+    double total_ms, forward_ms, sample_ms;
+    int    rows_per_step[256];      /* rows of each step's forward */
+    int    unmasked_per_step[256];
+    float  step_ms[256];            /* forward time of each step */
+} dfx_gen_stats;
+
+int  dfx_model_load(const char * path, dfx_model ** out);              /* diffuse-model.cpp:83-185 */
+void dfx_model_free(dfx_model * m);
+int  dfx_model_hparams(const dfx_model * m, dfx_hparams * out);
+int  dfx_context_new(const dfx_model * m, int n_ctx, dfx_context ** out);  /* diffuse-graph.cpp:683 */
+void dfx_context_free(dfx_context * c);
+/* tokens[n] (host) -> logits_out[n][n_vocab] (host), src/diffuse-graph.cpp:676-680 */
+int  dfx_forward(dfx_context * c, const int32_t * tokens, int n, float * logits_out);
+/* diffuse_generate (src/diffuse-sampler.cpp:373-380); out[n_generate] host. */
+int  dfx_generate(dfx_context * c, const int32_t * prompt, int n_prompt, int n_generate,
+                  const dfx_sampler_params * p, int32_t * out, dfx_gen_stats * stats);
+/* dfx_generate that also records, for each generated position, the step (0-based)
+ * at which it was unmasked (-1 if still masked at the end).  Stands in for the
+ * per-step callback of include/diffuse.h:67-68 for C callers. */
+int  dfx_generate_trace(dfx_context * c, const int32_t * prompt, int n_prompt, int n_generate,
+                        const dfx_sampler_params * p, int32_t * out, dfx_gen_stats * stats,
+                        int32_t * unmask_step);
+
+#ifdef __cplusplus
+}
+#endif

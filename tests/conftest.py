@@ -1,0 +1,57 @@
+import os
+import sys
+
+import numpy as np
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(REPO, "diffuse-cpp_amd")
+for p in (PKG, os.path.dirname(os.path.abspath(__file__))):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+
+
+# Small architectures whose K dimensions are multiples of 256 (K-quant blocks),
+# head_dim 128 / 64, so every code path of the 8B models runs at test size.
+TINY_LLADA = dict(n_vocab=1536, n_embd=512, n_head=4, n_head_kv=4, n_layer=3, n_ff=1024,
+                  rope_theta=500000.0, rms_norm_eps=1e-5, mask_token_id=1500, is_dream=0)
+TINY_DREAM = dict(n_vocab=1280, n_embd=512, n_head=8, n_head_kv=2, n_layer=3, n_ff=768,
+                  rope_theta=1000000.0, rms_norm_eps=1e-6, mask_token_id=1270, is_dream=1)
+
+
+@pytest.fixture(scope="session")
+def model_dir(tmp_path_factory):
+    return tmp_path_factory.mktemp("models")
+
+
+@pytest.fixture(scope="session")
+def tiny_models(model_dir):
+    """GGUF files: {(arch, scheme): path}, written by the library's generator.
+    sigma 0.05 keeps the random-init logits from being near-uniform."""
+    import dfx
+    out = {}
+    for arch_name, arch, seed in (("llada", TINY_LLADA, 11), ("dream", TINY_DREAM, 12)):
+        for scheme in ("q4_k_m", "q8_0", "f16"):
+            p = model_dir / f"{arch_name}-{scheme}.gguf"
+            dfx.synth_model(p, arch, scheme=scheme, seed=seed, sigma=0.05, n_threads=4)
+            out[(arch_name, scheme)] = str(p)
+    return out
+
+
+@pytest.fixture(scope="session")
+def gpu():
+    import dfx
+    n = dfx.device_count()
+    if n < 1:
+        raise RuntimeError("no HIP device visible: the gpu tests need an MI355X")
+    return n
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))

@@ -1,0 +1,258 @@
+"""Kernel-level parity of the HIP path (through the C ABI) against the CPU oracle."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import dfx
+import oracle_py as O
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+rng = np.random.default_rng(7)
+L = dfx.lib
+
+
+def quant(typ, rows, cols, scale=0.02):
+    x = (rng.standard_normal((rows, cols)) * scale).astype(np.float32)
+    return dfx.quantize_rows(typ, x)
+
+
+def to_device_weights(typ, raw, rows, cols):
+    return dfx.Buf.of(dfx.repack(typ, raw, rows, cols))
+
+
+def oracle_dequant_rows(typ, raw, rows, cols):
+    rb = O.row_bytes(typ, cols)
+    return np.stack([O.dequant(typ, raw[r * rb:(r + 1) * rb], cols) for r in range(rows)])
+
+
+# ---------------------------------------------------------------- dequant: bit-exact
+@pytest.mark.parametrize("typ,rows,cols", [(dfx.TYPE_Q4_K, 4096, 4096), (dfx.TYPE_Q4_K, 12288, 4096),
+                                           (dfx.TYPE_Q6_K, 4096, 4096), (dfx.TYPE_Q8_0, 4096, 4096),
+                                           (dfx.TYPE_F16, 512, 4096)])
+def test_dequant_bit_exact(gpu, typ, rows, cols):
+    raw = quant(typ, rows, cols)
+    w = to_device_weights(typ, raw, rows, cols)
+    out = dfx.Buf(rows * cols * 4)
+    dfx.check(L().dfx_dequant(typ, w.ptr, rows, cols, out.ptr, None), "dequant")
+    got = out.download(np.float32, shape=(rows, cols))
+    rb = O.row_bytes(typ, cols)
+    ref = np.empty_like(got)
+    for r in range(rows):
+        ref[r] = O.dequant(typ, raw[r * rb:(r + 1) * rb], cols)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("typ,size", [(dfx.TYPE_Q4_K, 144), (dfx.TYPE_Q6_K, 210)])
+def test_dequant_random_blocks_bit_exact(gpu, typ, size):
+    rows, cols = 64, 1024
+    raw = rng.integers(0, 256, rows * cols // 256 * size, dtype=np.uint8).reshape(-1, size)
+    for p in ((0, 2) if typ == dfx.TYPE_Q4_K else (208,)):
+        raw[:, p + 1] &= 0x7B          # finite f16 scales
+    raw = raw.reshape(-1)
+    w = to_device_weights(typ, raw, rows, cols)
+    out = dfx.Buf(rows * cols * 4)
+    dfx.check(L().dfx_dequant(typ, w.ptr, rows, cols, out.ptr, None), "dequant")
+    got = out.download(np.float32, shape=(rows, cols))
+    assert np.array_equal(got.view(np.uint32), oracle_dequant_rows(typ, raw, rows, cols).view(np.uint32))
+
+
+# ---------------------------------------------------------------- activation conversion
+Q8K = np.dtype([("d", "<f4"), ("qs", "i1", 256), ("bs", "<i2", 16)])
+Q80 = np.dtype([("d", "<f2"), ("qs", "i1", 32)])
+
+
+def oracle_act(wtype, X):
+    """(q, d, bs) of GGML's conversion of X for weight type wtype, from the oracle."""
+    M, K = X.shape
+    if wtype in (dfx.TYPE_Q4_K, dfx.TYPE_Q6_K):
+        b = np.stack([np.frombuffer(O.quantize_q8_K(X[m]).tobytes(), Q8K) for m in range(M)])
+        return (b["qs"].reshape(M, K).astype(np.float16), b["d"].astype(np.float32),
+                b["bs"].reshape(M, -1).astype(np.float16))
+    if wtype == dfx.TYPE_Q8_0:
+        b = np.stack([np.frombuffer(O.quantize_q8_0(X[m]).tobytes(), Q80) for m in range(M)])
+        return b["qs"].reshape(M, K).astype(np.float16), b["d"].astype(np.float32), None
+    return X.astype(np.float16), None, None
+
+
+def same_bits(a, b):
+    return a is None and b is None or np.array_equal(np.asarray(a).view(np.uint8), np.asarray(b).view(np.uint8))
+
+
+def check_act(act, wtype, ref, M, K):
+    q, d, bs = dfx.act_parts(act, wtype, M, K)
+    rq, rd, rbs = ref
+    assert np.array_equal(q.astype(np.float32), rq.astype(np.float32)) and same_bits(d, rd) and same_bits(bs, rbs)
+
+
+@pytest.mark.parametrize("typ", [dfx.TYPE_Q4_K, dfx.TYPE_Q8_0, dfx.TYPE_F16])
+def test_act_convert_matches_oracle(gpu, typ):
+    M, K = 37, 4096
+    x = (rng.standard_normal((M, K)) * 10.0 ** rng.integers(-2, 2, (M, 1))).astype(np.float32)
+    x[3, 256:512] = 0.0
+    x[5, :256] = 1.0        # ties on |max|: first index wins
+    x[5, 100] = -1.0
+    xb, ab = dfx.Buf.of(x), dfx.Buf(L().dfx_act_bytes(typ, M, K))
+    dfx.check(L().dfx_act_convert(typ, xb.ptr, M, K, ab.ptr, None), "act_convert")
+    check_act(ab, typ, oracle_act(typ, x), M, K)
+
+
+def test_rmsnorm_convert_matches_oracle(gpu):
+    M, K, eps = 29, 4096, 1e-5
+    x = (rng.standard_normal((M, K)) * 3).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    for typ in (dfx.TYPE_Q4_K, dfx.TYPE_Q8_0, dfx.TYPE_F16):
+        xb, wb, ab = dfx.Buf.of(x), dfx.Buf.of(w), dfx.Buf(L().dfx_act_bytes(typ, M, K))
+        dfx.check(L().dfx_rmsnorm_convert(typ, xb.ptr, wb.ptr, M, K, eps, ab.ptr, None), "rmsnorm")
+        check_act(ab, typ, oracle_act(typ, O.rms_norm_mul(x, w, eps)), M, K)
+
+
+def test_swiglu_convert_matches_oracle(gpu):
+    M, F = 19, 2048
+    gu = rng.standard_normal((M, 2 * F)).astype(np.float32) * 2
+    s = np.array([[O.oracle().orc_silu(float(v)) for v in r] for r in gu[:, :F]], np.float32) * gu[:, F:]
+    for typ in (dfx.TYPE_Q4_K, dfx.TYPE_Q8_0, dfx.TYPE_F16):
+        gb, ab = dfx.Buf.of(gu), dfx.Buf(L().dfx_act_bytes(typ, M, F))
+        dfx.check(L().dfx_swiglu_convert(typ, gb.ptr, M, F, ab.ptr, None), "swiglu")
+        check_act(ab, typ, oracle_act(typ, s), M, F)
+
+
+# ---------------------------------------------------------------- GEMM
+GEMM_CASES = [(dfx.TYPE_Q4_K, 4096, 4096, m) for m in (1, 5, 50, 96, 128, 255, 288)] + [
+    (dfx.TYPE_Q4_K, 12288, 4096, 288), (dfx.TYPE_Q6_K, 4096, 4096, 64), (dfx.TYPE_Q6_K, 2048, 12288, 100),
+    (dfx.TYPE_Q6_K, 1000, 4096, 288), (dfx.TYPE_Q8_0, 4096, 4096, 77), (dfx.TYPE_Q4_K, 4096, 12288, 288),
+    (dfx.TYPE_Q8_0, 1024, 4096, 300)]
+
+
+def gpu_gemm(typ, raw, N, K, X, ws=True):
+    M = X.shape[0]
+    w = to_device_weights(typ, raw, N, K)
+    xb, ab, yb = dfx.Buf.of(X), dfx.Buf(L().dfx_act_bytes(typ, M, K)), dfx.Buf(M * N * 4)
+    dfx.check(L().dfx_act_convert(typ, xb.ptr, M, K, ab.ptr, None), "convert")
+    wsb = dfx.Buf(L().dfx_gemm_ws_bytes(M, N)) if ws else None
+    dfx.check(L().dfx_gemm(typ, w.ptr, N, K, ab.ptr, M, None, None, yb.ptr, wsb.ptr if ws else None, None), "gemm")
+    return yb.download(np.float32, shape=(M, N))
+
+
+@pytest.mark.parametrize("typ,N,K,M", GEMM_CASES)
+def test_gemm_quantized_bit_exact(gpu, typ, N, K, M):
+    """Q4_K / Q6_K / Q8_0: the GPU reproduces the oracle's GGML block dot products
+    (integer sums, float scaling and accumulation in K order) bit for bit."""
+    raw = quant(typ, N, K)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    got = gpu_gemm(typ, raw, N, K, X)
+    ref = O.mul_mat(typ, raw, N, K, X)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
+
+
+@pytest.mark.parametrize("N,K,M", [(1000, 4096, 33), (4096, 4096, 288), (4096, 12288, 64)])
+def test_gemm_f16_matches_oracle(gpu, N, K, M):
+    """F16: exact f16 products accumulated by MFMA in f32 (the oracle sums in f64)."""
+    raw = quant(dfx.TYPE_F16, N, K)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    got = gpu_gemm(dfx.TYPE_F16, raw, N, K, X)
+    ref = O.mul_mat(dfx.TYPE_F16, raw, N, K, X)
+    assert rel_l2(got, ref) < 1e-6
+    assert rel_l2(gpu_gemm(dfx.TYPE_F16, raw, N, K, X, ws=False), got) < 1e-6
+
+
+def test_gemm_bias_and_residual_epilogue(gpu):
+    typ, N, K, M = dfx.TYPE_Q4_K, 1024, 2048, 40
+    raw = quant(typ, N, K)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    res = rng.standard_normal((M, N)).astype(np.float32)
+    w = to_device_weights(typ, raw, N, K)
+    xb, ab = dfx.Buf.of(X), dfx.Buf(L().dfx_act_bytes(typ, M, K))
+    dfx.check(L().dfx_act_convert(typ, xb.ptr, M, K, ab.ptr, None), "convert")
+    plain = dfx.Buf(M * N * 4)
+    dfx.check(L().dfx_gemm(typ, w.ptr, N, K, ab.ptr, M, None, None, plain.ptr, None, None), "gemm")
+    p = plain.download(np.float32, shape=(M, N))
+    bb, yb = dfx.Buf.of(bias), dfx.Buf(M * N * 4)
+    dfx.check(L().dfx_gemm(typ, w.ptr, N, K, ab.ptr, M, bb.ptr, None, yb.ptr, None, None), "gemm+bias")
+    assert np.array_equal(yb.download(np.float32, shape=(M, N)), p + bias)
+    rb = dfx.Buf.of(res)        # in-place residual: y = y + A W
+    dfx.check(L().dfx_gemm(typ, w.ptr, N, K, ab.ptr, M, None, rb.ptr, rb.ptr, None, None), "gemm+res")
+    assert np.array_equal(rb.download(np.float32, shape=(M, N)), p + res)
+
+
+# ---------------------------------------------------------------- RoPE + attention
+def test_rope_store_matches_oracle(gpu):
+    M, H, Hkv, hd, n_ctx = 23, 8, 2, 128, 64
+    qkv = rng.standard_normal((M, (H + 2 * Hkv) * hd)).astype(np.float32)
+    pos = rng.permutation(n_ctx)[:M].astype(np.int32)
+    tab = O.rope_table(n_ctx, hd, 1000000.0)
+    qb, pb, tb = dfx.Buf.of(qkv), dfx.Buf.of(pos), dfx.Buf.of(tab)
+    qo, kc, vc = dfx.Buf(M * H * hd * 4), dfx.Buf(n_ctx * Hkv * hd * 4), dfx.Buf(n_ctx * Hkv * hd * 4)
+    kc.zero()
+    vc.zero()
+    dfx.check(L().dfx_rope_store(qb.ptr, pb.ptr, M, H, Hkv, hd, tb.ptr, qo.ptr, kc.ptr, vc.ptr, None), "rope")
+    q_ref = qkv[:, :H * hd].reshape(M, H, hd).copy()
+    k_ref = qkv[:, H * hd:(H + Hkv) * hd].reshape(M, Hkv, hd).copy()
+    O.oracle().orc_rope_neox(O.ptr(q_ref), M, H, hd, O.ptr(pos), O.ptr(tab))
+    O.oracle().orc_rope_neox(O.ptr(k_ref), M, Hkv, hd, O.ptr(pos), O.ptr(tab))
+    assert np.array_equal(qo.download(np.float32, shape=(M, H, hd)), q_ref)
+    kg = kc.download(np.float32, shape=(n_ctx, Hkv, hd))
+    vg = vc.download(np.float32, shape=(n_ctx, Hkv, hd))
+    assert np.array_equal(kg[pos], k_ref)
+    assert np.array_equal(vg[pos], qkv[:, (H + Hkv) * hd:].reshape(M, Hkv, hd))
+    untouched = np.setdiff1d(np.arange(n_ctx), pos)
+    assert not kg[untouched].any() and not vg[untouched].any()
+
+
+@pytest.mark.parametrize("M,n_keys,H,Hkv,hd", [(288, 288, 32, 32, 128), (50, 288, 32, 32, 128),
+                                               (128, 128, 28, 4, 128), (7, 768, 8, 2, 64), (3, 2000, 4, 4, 128)])
+def test_attention_matches_f64(gpu, M, n_keys, H, Hkv, hd):
+    q = rng.standard_normal((M, H, hd)).astype(np.float32)
+    k = rng.standard_normal((n_keys, Hkv, hd)).astype(np.float32)
+    v = rng.standard_normal((n_keys, Hkv, hd)).astype(np.float32)
+    qb, kb, vb, ob = dfx.Buf.of(q), dfx.Buf.of(k), dfx.Buf.of(v), dfx.Buf(M * H * hd * 4)
+    dfx.check(L().dfx_attention(qb.ptr, kb.ptr, vb.ptr, M, n_keys, H, Hkv, hd, ob.ptr, None), "attention")
+    got = ob.download(np.float32, shape=(M, H, hd))
+    rep = H // Hkv
+    kd = np.repeat(k.astype(np.float64), rep, axis=1)        # query head h reads KV head h // rep
+    vd = np.repeat(v.astype(np.float64), rep, axis=1)
+    s = np.einsum("mhd,nhd->hmn", q.astype(np.float64), kd) / np.sqrt(hd)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    ref = np.einsum("hmn,nhd->mhd", p, vd)
+    assert rel_l2(got, ref) < 1e-6
+
+
+# ---------------------------------------------------------------- sampler kernels
+@pytest.mark.parametrize("sigma", [0.5, 2.0, 8.0])
+def test_row_stats_matches_oracle(gpu, sigma):
+    """Sampler microbench shape: [256 x 126464] N(0, sigma) logits.  argmax / top-1 / top-2
+    exact; entropy within the reference's own float-accumulation error (2e-3 relative)."""
+    R, V = 256, 126464
+    x = (np.random.default_rng(4).standard_normal((R, V)) * sigma).astype(np.float32)
+    x[0, [5, 77]] = x[0].max() + 1.0           # tie on the max: lowest index
+    x[1, 0] = x[1].max() + 1.0                 # argmax at index 0
+    rows = np.arange(R, dtype=np.int32)[::-1].copy()
+    xb, rb, sb = dfx.Buf.of(x), dfx.Buf.of(rows), dfx.Buf(R * 16)
+    dfx.check(L().dfx_row_stats(xb.ptr, V, rb.ptr, R, V, sb.ptr, None), "row_stats")
+    st = np.frombuffer(sb.download(np.uint8).tobytes(), dtype=dfx.ROW_STAT)
+    for i, r in enumerate(rows):
+        b, bv, sv = O.top2(x[r])
+        assert (st["token"][i], st["best"][i], st["second"][i]) == (b, np.float32(bv), np.float32(sv)), r
+        e_ref = O.entropy(x[r])
+        assert abs(st["entropy"][i] - e_ref) <= 2e-3 * abs(e_ref) + 1e-5, r
+
+
+@pytest.mark.parametrize("remasking", [0, 2, 3, 4])
+def test_select_bit_exact(gpu, remasking):
+    for trial in range(10):
+        n = int(rng.integers(1, 2049)) if trial else 2048
+        c = np.zeros(n, dfx.CANDIDATE)
+        c["pos"] = rng.permutation(4096)[:n]
+        c["token"] = rng.integers(0, 1000, n)
+        c["confidence"] = rng.integers(0, 20, n).astype(np.float32) * 0.25
+        c["entropy"] = rng.integers(0, 12, n).astype(np.float32) * 0.25
+        n_sched = int(rng.integers(1, n + 1))
+        cb, ob, nb = dfx.Buf.of(c), dfx.Buf(n * 4), dfx.Buf(4)
+        dfx.check(L().dfx_select(cb.ptr, n, remasking, 1.5, n_sched, ob.ptr, nb.ptr, None), "select")
+        order = ob.download(np.int32)
+        ref, n_ref = O.order_candidates(c, remasking, 1.5, n_sched)
+        assert np.array_equal(c[order], ref)
+        assert int(nb.download(np.int32)[0]) == n_ref
