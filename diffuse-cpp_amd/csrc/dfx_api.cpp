@@ -95,8 +95,8 @@ extern "C" int dfx_timer_stop(void * timer, void * stream, float * ms) {
     hipError_t e = hipEventRecord(t->b, (hipStream_t)stream);
     if (e == hipSuccess) e = hipEventSynchronize(t->b);
     if (e == hipSuccess) e = hipEventElapsedTime(ms, t->a, t->b);
-    hipEventDestroy(t->a);
-    hipEventDestroy(t->b);
+    (void)hipEventDestroy(t->a);
+    (void)hipEventDestroy(t->b);
     delete t;
     if (e != hipSuccess) {
         dfx_set_error("timer: %s", hipGetErrorString(e));

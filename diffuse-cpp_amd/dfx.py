@@ -122,6 +122,9 @@ def _declare(L):
         "dfx_forward": (I32, [P, P, I32, P]),
         "dfx_generate": (I32, [P, P, I32, I32, C.POINTER(SamplerParams), P, C.POINTER(GenStats)]),
         "dfx_generate_trace": (I32, [P, P, I32, I32, C.POINTER(SamplerParams), P, C.POINTER(GenStats), P]),
+        "dfx_context_profile": (I32, [P, I32]),
+        "dfx_context_profile_read": (I32, [P, I32, C.POINTER(C.c_int64), C.POINTER(C.c_double),
+                                           C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -299,6 +302,16 @@ class Context:
         check(lib().dfx_generate_trace(self.h, _ptr(prompt), len(prompt), n_generate, C.byref(params),
                                        _ptr(out), C.byref(st), _ptr(steps)), "dfx_generate_trace")
         return out, steps
+
+    def profile(self, enable=True):
+        check(lib().dfx_context_profile(self.h, 1 if enable else 0), "dfx_context_profile")
+
+    def profile_read(self, wtype):
+        """{launches, ms, flops, bytes} of the GEMMs on weights of type wtype since profiling began."""
+        n, ms, fl, by = C.c_int64(), C.c_double(), C.c_double(), C.c_double()
+        check(lib().dfx_context_profile_read(self.h, wtype, C.byref(n), C.byref(ms), C.byref(fl), C.byref(by)),
+              "dfx_context_profile_read")
+        return dict(launches=n.value, ms=ms.value, flops=fl.value, bytes=by.value)
 
     def close(self):
         if self.h:

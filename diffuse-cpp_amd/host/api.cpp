@@ -78,6 +78,17 @@ extern "C" int dfx_generate_trace(dfx_context * c, const int32_t * prompt, int n
     return engine_generate(c, prompt, n_prompt, n_generate, *p, out, stats, nullptr, unmask_step);
 }
 
+extern "C" int dfx_context_profile(dfx_context * c, int enable) {
+    if (!c) return DFX_ERR_ARG;
+    return engine_profile(c, enable != 0);
+}
+
+extern "C" int dfx_context_profile_read(dfx_context * c, int wtype, int64_t * launches, double * ms, double * flops,
+                                        double * bytes) {
+    if (!c) return DFX_ERR_ARG;
+    return engine_profile_read(c, wtype, launches, ms, flops, bytes);
+}
+
 // ---- C++ API (include/diffuse.h) ----
 diffuse_model * diffuse_model_load(const std::string & path, int /*n_threads*/) {
     diffuse_model * m = nullptr;

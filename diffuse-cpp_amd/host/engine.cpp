@@ -49,8 +49,8 @@ void free_buffers(diffuse_context * c) {
                      c->d_tok, c->d_pos, c->d_hrows, c->d_hmap, c->d_srows, c->d_spos, c->ws, c->d_stats,
                      c->d_cand, c->d_order, c->d_nun};
     for (void * p : bufs)
-        if (p) hipFree(p);
-    if (c->h_pin) hipHostFree(c->h_pin);
+        if (p) (void)hipFree(p);
+    if (c->h_pin) (void)hipHostFree(c->h_pin);
     c->x = c->qkv = c->qr = c->att = c->gu = c->logits = c->kc = c->vc = c->rope_tab = nullptr;
     c->act = nullptr;
     c->d_tok = c->d_pos = c->d_hrows = c->d_hmap = c->d_srows = c->d_spos = c->d_order = c->d_nun = nullptr;
@@ -119,19 +119,67 @@ int ensure_capacity(diffuse_context * c, int N) {
     return DFX_OK;
 }
 
+hipEvent_t take_event(diffuse_context * c) {
+    if (!c->prof_pool.empty()) {
+        hipEvent_t e = c->prof_pool.back();
+        c->prof_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// Every GEMM of the forward goes through here; with profiling on, a pair of events
+// brackets the launch on the context stream (read back by prof_collect).
+int gemm(diffuse_context * c, const dev_matrix & w, int64_t N, int64_t K, int64_t M, const float * bias,
+         const float * res, float * y, int64_t ldy, const int32_t * ymap, bool split_ok) {
+    void * ws = split_ok ? c->ws : nullptr;
+    const size_t wsb = split_ok ? c->ws_bytes : 0;
+    if (!c->prof || M == 0) return dfx_gemm_ex(w.type, w.data, N, K, c->act, M, bias, res, y, ldy, ymap, ws, wsb, c->stream);
+    diffuse_context::gemm_rec r;
+    r.a = take_event(c);
+    r.b = take_event(c);
+    r.type = w.type;
+    r.flops = 2.0 * (double)M * N * K;
+    r.bytes = (double)dfx_device_row_bytes(w.type, K) * N + (double)M * K * 2 + (double)M * N * 4;
+    if (!r.a || !r.b) return hip_ok(hipErrorOutOfMemory, "hipEventCreate");
+    TRY(hip_ok(hipEventRecord(r.a, c->stream), "event"));
+    TRY(dfx_gemm_ex(w.type, w.data, N, K, c->act, M, bias, res, y, ldy, ymap, ws, wsb, c->stream));
+    TRY(hip_ok(hipEventRecord(r.b, c->stream), "event"));
+    c->prof_pending.push_back(r);
+    return DFX_OK;
+}
+
+// After a stream sync: fold the pending GEMM timings into the per-type totals.
+void prof_collect(diffuse_context * c) {
+    for (auto & r : c->prof_pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess && r.type >= 0 && r.type < 32) {
+            auto & t = c->prof_tot[r.type];
+            t.launches++;
+            t.ms += ms;
+            t.flops += r.flops;
+            t.bytes += r.bytes;
+        }
+        c->prof_pool.push_back(r.a);
+        c->prof_pool.push_back(r.b);
+    }
+    c->prof_pending.clear();
+}
+
 // GEMMs of a projection group into out[M][g.n_out]; input rows already in x.
 int run_group(diffuse_context * c, const proj_group & g, const float * norm, int64_t M, int64_t K, float * out) {
     const float eps = c->model->hparams.rms_norm_eps;
     if (g.fused) {
         TRY(dfx_rmsnorm_convert_ex(g.all.type, c->x, nullptr, norm, M, K, eps, c->act, c->stream));
-        return dfx_gemm_ex(g.all.type, g.all.data, g.n_out, K, c->act, M, g.bias, nullptr, out, g.n_out, nullptr,
-                           c->ws, c->ws_bytes, c->stream);
+        return gemm(c, g.all, g.n_out, K, M, g.bias, nullptr, out, g.n_out, nullptr, true);
     }
     for (size_t i = 0; i < g.parts.size(); i++) {
         const dev_matrix & p = g.parts[i];
         TRY(dfx_rmsnorm_convert_ex(p.type, c->x, nullptr, norm, M, K, eps, c->act, c->stream));
-        TRY(dfx_gemm_ex(p.type, p.data, p.rows, K, c->act, M, g.bias ? g.bias + g.col_off[i] : nullptr, nullptr,
-                        out + g.col_off[i], g.n_out, nullptr, c->ws, c->ws_bytes, c->stream));
+        TRY(gemm(c, p, p.rows, K, M, g.bias ? g.bias + g.col_off[i] : nullptr, nullptr, out + g.col_off[i], g.n_out,
+                 nullptr, true));
     }
     return DFX_OK;
 }
@@ -152,17 +200,14 @@ int forward_pass(diffuse_context * c, int M, int n_keys, int n_head) {
                            c->stream));
         TRY(dfx_attention(c->qr, kc, vc, M, n_keys, (int)D.H, (int)D.Hkv, (int)D.hd, c->att, c->stream));
         TRY(dfx_act_convert(L.o.type, c->att, M, D.d, c->act, c->stream));
-        TRY(dfx_gemm_ex(L.o.type, L.o.data, D.d, D.d, c->act, M, nullptr, c->x, c->x, D.d, nullptr, c->ws,
-                        c->ws_bytes, c->stream));
+        TRY(gemm(c, L.o, D.d, D.d, M, nullptr, c->x, c->x, D.d, nullptr, true));
         TRY(run_group(c, L.gu, L.ffn_norm, M, D.d, c->gu));
         TRY(dfx_swiglu_convert(L.down.type, c->gu, M, D.F, c->act, c->stream));
-        TRY(dfx_gemm_ex(L.down.type, L.down.data, D.d, D.F, c->act, M, nullptr, c->x, c->x, D.d, nullptr, c->ws,
-                        c->ws_bytes, c->stream));
+        TRY(gemm(c, L.down, D.d, D.F, M, nullptr, c->x, c->x, D.d, nullptr, true));
     }
     if (n_head > 0) {
         TRY(dfx_rmsnorm_convert_ex(m.output.type, c->x, c->d_hrows, m.output_norm, n_head, D.d, eps, c->act, c->stream));
-        TRY(dfx_gemm_ex(m.output.type, m.output.data, D.V, D.d, c->act, n_head, nullptr, nullptr, c->logits, D.V,
-                        c->d_hmap, nullptr, 0, c->stream));
+        TRY(gemm(c, m.output, D.V, D.d, n_head, nullptr, nullptr, c->logits, D.V, c->d_hmap, false));
     }
     return DFX_OK;
 }
@@ -217,12 +262,35 @@ int engine_context_new(const diffuse_model * m, int n_ctx, int n_threads, diffus
 
 void engine_context_free(diffuse_context * c) {
     if (!c) return;
-    if (c->stream) hipStreamSynchronize(c->stream);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    prof_collect(c);
     free_buffers(c);
-    if (c->ev0) hipEventDestroy(c->ev0);
-    if (c->ev1) hipEventDestroy(c->ev1);
-    if (c->stream) hipStreamDestroy(c->stream);
+    if (c->ev0) (void)hipEventDestroy(c->ev0);
+    if (c->ev1) (void)hipEventDestroy(c->ev1);
+    for (hipEvent_t e : c->prof_pool) (void)hipEventDestroy(e);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
+}
+
+int engine_profile(diffuse_context * c, bool enable) {
+    if (c->stream) TRY(hip_ok(hipStreamSynchronize(c->stream), "profile"));
+    prof_collect(c);
+    c->prof = enable;
+    for (auto & t : c->prof_tot) t = diffuse_context::prof_total();
+    return DFX_OK;
+}
+
+int engine_profile_read(diffuse_context * c, int wtype, int64_t * launches, double * ms, double * flops,
+                        double * bytes) {
+    if (wtype < 0 || wtype >= 32) return DFX_ERR_ARG;
+    TRY(hip_ok(hipStreamSynchronize(c->stream), "profile"));
+    prof_collect(c);
+    const auto & t = c->prof_tot[wtype];
+    if (launches) *launches = t.launches;
+    if (ms) *ms = t.ms;
+    if (flops) *flops = t.flops;
+    if (bytes) *bytes = t.bytes;
+    return DFX_OK;
 }
 
 int engine_forward(diffuse_context * c, const int32_t * tokens, int n, float * logits_out) {
@@ -245,7 +313,9 @@ int engine_forward(diffuse_context * c, const int32_t * tokens, int n, float * l
     TRY(upload_i32(c, c->d_hmap, idx.data(), n, 3));
     TRY(forward_pass(c, n, n, n));
     TRY(hip_ok(hipMemcpyAsync(logits_out, c->logits, (size_t)n * D.V * 4, hipMemcpyDeviceToHost, c->stream), "D2H"));
-    return hip_ok(hipStreamSynchronize(c->stream), "forward");
+    TRY(hip_ok(hipStreamSynchronize(c->stream), "forward"));
+    prof_collect(c);
+    return DFX_OK;
 }
 
 int engine_generate(diffuse_context * c, const int32_t * prompt, int n_prompt, int n_generate,
@@ -461,6 +531,7 @@ int engine_generate(diffuse_context * c, const int32_t * prompt, int n_prompt, i
             stats->unmasked_per_step[step] = done;
             stats->step_ms[step] = (float)fwd_ms;
         }
+        prof_collect(c);   // the stream was synchronised by the sampler
         if (callback && *callback) (*callback)(step + 1, p.n_steps, seq);
     }
 

@@ -91,6 +91,14 @@ struct diffuse_context {
     int32_t *    d_nun = nullptr;
     int32_t *    h_pin = nullptr;    // pinned staging, 8 * cap int32
     hipEvent_t   ev0 = nullptr, ev1 = nullptr;
+
+    // Optional per-GEMM timing: a pair of events around every GEMM launch on `stream`.
+    struct gemm_rec { hipEvent_t a, b; int type; double flops, bytes; };
+    bool                  prof = false;
+    std::vector<gemm_rec> prof_pending;      // launched, not yet read
+    std::vector<hipEvent_t> prof_pool;       // reusable events
+    struct prof_total { long launches = 0; double ms = 0, flops = 0, bytes = 0; };
+    prof_total            prof_tot[32];      // by weight type id
 };
 
 // model.cpp
@@ -101,6 +109,9 @@ void engine_model_free(diffuse_model * m);
 int  engine_context_new(const diffuse_model * m, int n_ctx, int n_threads, diffuse_context ** out);
 void engine_context_free(diffuse_context * c);
 int  engine_forward(diffuse_context * c, const int32_t * tokens, int n, float * logits_out);
+int  engine_profile(diffuse_context * c, bool enable);
+int  engine_profile_read(diffuse_context * c, int wtype, int64_t * launches, double * ms, double * flops,
+                         double * bytes);
 int  engine_generate(diffuse_context * c, const int32_t * prompt, int n_prompt, int n_generate,
                      const dfx_sampler_params & p, int32_t * out, dfx_gen_stats * stats,
                      const diffuse_step_callback * callback, int32_t * unmask_step = nullptr);

@@ -307,6 +307,6 @@ int engine_model_load(const std::string & path, diffuse_model ** out) {
 
 void engine_model_free(diffuse_model * m) {
     if (!m) return;
-    for (void * p : m->allocs) hipFree(p);
+    for (void * p : m->allocs) (void)hipFree(p);
     delete m;
 }

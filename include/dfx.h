@@ -219,6 +219,13 @@ int  dfx_forward(dfx_context * c, const int32_t * tokens, int n, float * logits_
 /* diffuse_generate (src/diffuse-sampler.cpp:373-380); out[n_generate] host. */
 int  dfx_generate(dfx_context * c, const int32_t * prompt, int n_prompt, int n_generate,
                   const dfx_sampler_params * p, int32_t * out, dfx_gen_stats * stats);
+/* Instrumentation: with profiling on, every GEMM the context launches is bracketed by
+ * HIP events on its stream.  _read returns, for one weight type, the number of
+ * launches, their summed duration, and their algorithmic FLOPs (2*M*N*K) and bytes
+ * (weights + converted activations + f32 output).  Enabling resets the totals. */
+int  dfx_context_profile(dfx_context * c, int enable);
+int  dfx_context_profile_read(dfx_context * c, int wtype, int64_t * launches, double * ms, double * flops,
+                              double * bytes);
 /* dfx_generate that also records, for each generated position, the step (0-based)
  * at which it was unmasked (-1 if still masked at the end).  Stands in for the
  * per-step callback of include/diffuse.h:67-68 for C callers. */

@@ -236,24 +236,60 @@ extern "C" void orc_quantize_row_q8_0(const float * x, void * vy, int64_t k) {
 /* vec_dot (GGML ggml_vec_dot_*_generic: integer block sums, float scale per */
 /* block; float accumulation order across blocks is unpinned)               */
 /* ------------------------------------------------------------------------ */
+/* Integer parts of the block dots.  The AVX2 forms compute the same integers as the
+ * scalar definitions (u8 x s8 pair sums fit int16 without saturation: 2*63*127). */
+static inline int32_t hsum_i32(__m256i v) {
+    __m128i s = _mm_add_epi32(_mm256_castsi256_si128(v), _mm256_extracti128_si256(v, 1));
+    s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0x4E));
+    s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0xB1));
+    return _mm_cvtsi128_si32(s);
+}
+
+/* isum = sum_j sc_j * sum_{l<32} q4[32j+l] * q8[32j+l] over one Q4_K super-block */
+static inline int32_t q4k_isum(const uint8_t * qs, const int8_t * q8, const uint8_t sc[8]) {
+    const __m256i m4 = _mm256_set1_epi8(0x0F);
+    __m256i acc = _mm256_setzero_si256();
+    for (int g = 0; g < 4; g++) {
+        const __m256i q4 = _mm256_loadu_si256((const __m256i *)(qs + 32 * g));
+        const __m256i lo = _mm256_and_si256(q4, m4);
+        const __m256i hi = _mm256_and_si256(_mm256_srli_epi16(q4, 4), m4);
+        const __m256i p0 = _mm256_maddubs_epi16(lo, _mm256_loadu_si256((const __m256i *)(q8 + 64 * g)));
+        const __m256i p1 = _mm256_maddubs_epi16(hi, _mm256_loadu_si256((const __m256i *)(q8 + 64 * g + 32)));
+        acc = _mm256_add_epi32(acc, _mm256_madd_epi16(p0, _mm256_set1_epi16(sc[2 * g])));
+        acc = _mm256_add_epi32(acc, _mm256_madd_epi16(p1, _mm256_set1_epi16(sc[2 * g + 1])));
+    }
+    return hsum_i32(acc);
+}
+
+/* sum_j sc_j * sum_{l<16} u6[16j+l] * q8[16j+l] with u6 = q + 32 in [0, 63] */
+static inline int32_t q6k_usum(const uint8_t * u6, const int8_t * q8, const int8_t * sc) {
+    __m256i acc = _mm256_setzero_si256();
+    for (int j = 0; j < 16; j += 2) {
+        const __m256i p = _mm256_maddubs_epi16(_mm256_loadu_si256((const __m256i *)(u6 + 16 * j)),
+                                               _mm256_loadu_si256((const __m256i *)(q8 + 16 * j)));
+        const __m256i s = _mm256_setr_epi16(sc[j], sc[j], sc[j], sc[j], sc[j], sc[j], sc[j], sc[j], sc[j + 1],
+                                            sc[j + 1], sc[j + 1], sc[j + 1], sc[j + 1], sc[j + 1], sc[j + 1], sc[j + 1]);
+        acc = _mm256_add_epi32(acc, _mm256_madd_epi16(p, s));
+    }
+    return hsum_i32(acc);
+}
+
+/* sum_{l<32} a[l] * b[l], both int8 */
+static inline int32_t i8_dot32(const int8_t * a, const int8_t * b) {
+    const __m256i va = _mm256_loadu_si256((const __m256i *)a), vb = _mm256_loadu_si256((const __m256i *)b);
+    const __m256i p = _mm256_maddubs_epi16(_mm256_sign_epi8(va, va), _mm256_sign_epi8(vb, va));
+    return hsum_i32(_mm256_madd_epi16(p, _mm256_set1_epi16(1)));
+}
+
 static float dot_q4_K_q8_K(int64_t n, const blk_q4_K * x, const blk_q8_K * y) {
     float sum_sc = 0.0f, sum_m = 0.0f;
-    int8_t aux[QK_K];
     for (int64_t i = 0; i < n / QK_K; i++) {
-        const uint8_t * q = x[i].qs;
-        for (int g = 0; g < 4; g++) {
-            for (int l = 0; l < 32; l++) aux[64 * g + l]      = (int8_t)(q[32 * g + l] & 0x0F);
-            for (int l = 0; l < 32; l++) aux[64 * g + 32 + l] = (int8_t)(q[32 * g + l] >> 4);
-        }
-        int32_t isum = 0, msum = 0;
-        for (int j = 0; j < 8; j++) {
-            uint8_t sc, m;
-            q4k_scale_min(j, x[i].scales, &sc, &m);
-            int32_t s = 0;
-            for (int l = 0; l < 32; l++) s += (int32_t)aux[32 * j + l] * (int32_t)y[i].qs[32 * j + l];
-            isum += (int32_t)sc * s;
-            msum += (int32_t)m * ((int32_t)y[i].bsums[2 * j] + (int32_t)y[i].bsums[2 * j + 1]);
-        }
+        uint8_t sc[8], mn[8];
+        for (int j = 0; j < 8; j++) q4k_scale_min(j, x[i].scales, &sc[j], &mn[j]);
+        const int32_t isum = q4k_isum(x[i].qs, y[i].qs, sc);
+        int32_t msum = 0;
+        for (int j = 0; j < 8; j++)
+            msum += (int32_t)mn[j] * ((int32_t)y[i].bsums[2 * j] + (int32_t)y[i].bsums[2 * j + 1]);
         const float d    = orc_fp16_to_fp32(x[i].d) * y[i].d;
         const float dmin = orc_fp16_to_fp32(x[i].dmin) * y[i].d;
         sum_sc += d * (float)isum;
@@ -264,15 +300,24 @@ static float dot_q4_K_q8_K(int64_t n, const blk_q4_K * x, const blk_q8_K * y) {
 
 static float dot_q6_K_q8_K(int64_t n, const blk_q6_K * x, const blk_q8_K * y) {
     float sum = 0.0f;
-    int8_t aux[QK_K];
+    uint8_t u6[QK_K];
     for (int64_t i = 0; i < n / QK_K; i++) {
-        for (int e = 0; e < QK_K; e++) aux[e] = (int8_t)q6k_value(&x[i], e);
-        int32_t isum = 0;
-        for (int j = 0; j < 16; j++) {
-            int32_t s = 0;
-            for (int l = 0; l < 16; l++) s += (int32_t)aux[16 * j + l] * (int32_t)y[i].qs[16 * j + l];
-            isum += (int32_t)x[i].scales[j] * s;
+        /* unpack q + 32 (ql low/high nibbles and qh 2-bit fields, GGML block_q6_K order) */
+        for (int half = 0; half < 2; half++) {
+            const uint8_t * ql = x[i].ql + 64 * half;
+            const uint8_t * qh = x[i].qh + 32 * half;
+            uint8_t * u = u6 + 128 * half;
+            for (int l = 0; l < 32; l++) {
+                u[l]      = (uint8_t)((ql[l] & 0x0F)      | (((qh[l] >> 0) & 3) << 4));
+                u[l + 32] = (uint8_t)((ql[l + 32] & 0x0F) | (((qh[l] >> 2) & 3) << 4));
+                u[l + 64] = (uint8_t)((ql[l] >> 4)        | (((qh[l] >> 4) & 3) << 4));
+                u[l + 96] = (uint8_t)((ql[l + 32] >> 4)   | (((qh[l] >> 6) & 3) << 4));
+            }
         }
+        /* isum = sum_j sc_j * sum_l (u6 - 32) * q8 */
+        int32_t corr = 0;
+        for (int j = 0; j < 16; j++) corr += (int32_t)x[i].scales[j] * (int32_t)y[i].bsums[j];
+        const int32_t isum = q6k_usum(u6, y[i].qs, x[i].scales) - 32 * corr;
         const float d = orc_fp16_to_fp32(x[i].d) * y[i].d;
         sum += d * (float)isum;
     }
@@ -282,8 +327,7 @@ static float dot_q6_K_q8_K(int64_t n, const blk_q6_K * x, const blk_q8_K * y) {
 static float dot_q8_0_q8_0(int64_t n, const blk_q8_0 * x, const blk_q8_0 * y) {
     float sum = 0.0f;
     for (int64_t i = 0; i < n / QK8_0; i++) {
-        int32_t s = 0;
-        for (int j = 0; j < QK8_0; j++) s += (int32_t)x[i].qs[j] * (int32_t)y[i].qs[j];
+        const int32_t s = i8_dot32(x[i].qs, y[i].qs);
         sum += (float)s * (orc_fp16_to_fp32(x[i].d) * orc_fp16_to_fp32(y[i].d));
     }
     return sum;
