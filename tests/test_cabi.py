@@ -63,6 +63,22 @@ int main() {
     assert r.returncode == 0 and r.stdout.strip() == "1"
 
 
+REF_CALLERS = ("tools/main-cli.cpp", "tools/main-bench.cpp", "tools/dump-logits.cpp", "tests/test-forward.cpp")
+
+
+@pytest.mark.skipif(not os.path.isdir("/root/reference/tools"), reason="reference sources not present on this host")
+@pytest.mark.parametrize("rel", REF_CALLERS)
+def test_reference_callers_link_unchanged(tmp_path, rel):
+    """The reference's own callers of diffuse.h compile, unmodified, against this
+    include/diffuse.h and link against libdiffuse (drop-in check; nothing is run)."""
+    exe = tmp_path / os.path.basename(rel).replace(".cpp", "")
+    lib = os.path.dirname(dfx.LIB_PATH)
+    subprocess.check_call(["g++", "-std=c++17", "-O0", "-I", os.path.join(REPO, "include"),
+                           os.path.join("/root/reference", rel), "-o", str(exe), "-L", lib, "-ldiffuse",
+                           f"-Wl,-rpath,{lib}", "-Wl,--allow-shlib-undefined"])
+    assert exe.exists()
+
+
 @pytest.mark.parametrize("typ,bound", [(dfx.TYPE_Q4_K, 0.12), (dfx.TYPE_Q6_K, 0.03), (dfx.TYPE_Q8_0, 0.006),
                                        (dfx.TYPE_F16, 1e-3)])
 def test_encoder_roundtrip(typ, bound):
