@@ -10,6 +10,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef float float16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // value type for 16-byte loads/stores
 
 #define WAVE 64
 
@@ -59,12 +60,24 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 //   q   f16 [M][K]        Q8_K / Q8_0: the int8 quants (exact in f16); F16: the values
 //   d   f32 [M][K/blk]    block scale (Q8_K: blk 256, f32; Q8_0: blk 32, the f16 scale)
 //   bs  f16 [M][K/16]     Q8_K only: sums of q over 16-element groups (GGML bsums)
-enum { CONV_Q8_K = 0, CONV_Q8_0 = 1, CONV_F16 = 2 };
+// For Q4_K weights (CONV_Q8_K_P4) q is stored in the order in which the GEMM unpacks
+// Q4_K nibbles: inside every 64-element group, slot 8i+s holds element
+//   s < 4:  4i + P[s]        s >= 4:  32 + 4i + P[s-4]        P = {0, 2, 1, 3}
+// (one 32-bit word of packed nibbles gives the 8 operands of slots 8i..8i+7).
+enum { CONV_Q8_K = 0, CONV_Q8_0 = 1, CONV_F16 = 2, CONV_Q8_K_P4 = 3 };
+
+// Quantised GEMMs sum the scaled block dot products of each chunk of DFX_DOT_CHUNK
+// K elements from zero, in K order, and add the chunk sums in order (T = T + S).
+// The order does not depend on the launch, so a GEMM may split K at chunk borders.
+#define DFX_DOT_CHUNK 2048
+__host__ __device__ inline int dot_chunks(int64_t K) { return (int)((K + DFX_DOT_CHUNK - 1) / DFX_DOT_CHUNK); }
 
 __host__ __device__ inline int conv_mode(int wtype) {
-    return (wtype == DFX_TYPE_Q4_K || wtype == DFX_TYPE_Q6_K) ? CONV_Q8_K
+    return wtype == DFX_TYPE_Q4_K ? CONV_Q8_K_P4
+         : wtype == DFX_TYPE_Q6_K ? CONV_Q8_K
          : (wtype == DFX_TYPE_Q8_0) ? CONV_Q8_0 : CONV_F16;
 }
+__host__ __device__ inline bool conv_is_q8k(int mode) { return mode == CONV_Q8_K || mode == CONV_Q8_K_P4; }
 
 struct act_layout {
     size_t q, d, bs, bytes;
@@ -74,9 +87,9 @@ __host__ __device__ inline act_layout act_layout_of(int mode, int64_t M, int64_t
     act_layout L;
     L.q = 0;
     L.d = align256((size_t)M * K * 2);
-    const size_t nd = mode == CONV_Q8_K ? (size_t)M * (K / 256) : mode == CONV_Q8_0 ? (size_t)M * (K / 32) : 0;
+    const size_t nd = conv_is_q8k(mode) ? (size_t)M * (K / 256) : mode == CONV_Q8_0 ? (size_t)M * (K / 32) : 0;
     L.bs = align256(L.d + nd * 4);
-    const size_t nbs = mode == CONV_Q8_K ? (size_t)M * (K / 16) : 0;
+    const size_t nbs = conv_is_q8k(mode) ? (size_t)M * (K / 16) : 0;
     L.bytes = align256(L.bs + nbs * 2);
     return L;
 }

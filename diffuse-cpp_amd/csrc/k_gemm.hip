@@ -8,10 +8,11 @@
 // Quantised weights (Q4_K, Q6_K, Q8_0) run the "exact" kernel k_mmq, which
 // reproduces GGML's CPU dot products (ggml_vec_dot_q4_K_q8_K / q6_K_q8_K /
 // q8_0_q8_0): integer products summed exactly per block, then scaled and
-// accumulated in float in increasing K order with the same operations:
-//   Q4_K  sum_sc += (d_w*d_a) * isum;  sum_m += (dmin_w*d_a) * msum;  y = sum_sc - sum_m
-//   Q6_K  sum    += (d_w*d_a) * isum
-//   Q8_0  sum    += isum * (d_w*d_a)         (per 32-element block)
+// accumulated in float in increasing K order, in the same order as the CPU
+// oracle:
+//   Q4_K  x = d_w*isum;  x = fma(-dmin_w, msum, x);  S = fma(d_a, x, S)
+//   Q6_K  x = d_w*isum;  S = fma(d_a, x, S)
+//   Q8_0  x = d_w*isum;  S = fma(d_a, x, S)         (per 32-element block)
 // The MFMA operands are integer-valued f16: activations q_a (int8), weights
 // sc*q (Q4_K, <= 945), 8*sc*c and sc*e with q = 8c+e (Q6_K, a power-of-two
 // multiple of an integer below 1024) or q (Q8_0).  Every product is exact in
@@ -31,6 +32,10 @@
 #include "dfx_device.h"
 
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <type_traits>
 
 #define BK 128
 
@@ -194,11 +199,11 @@ k_mmq(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
         }
     };
 
-    float16v P[TM], S1[TM], S2[TM];
+    float16v P[TM], S1[TM], T1[TM];
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) P[i][r] = S1[i][r] = S2[i][r] = 0.0f;
+        for (int r = 0; r < 16; r++) P[i][r] = S1[i][r] = T1[i][r] = 0.0f;
 
     const uint8_t * wp = Ws + (wn * 32 + (lane & 31)) * WSTR;   // this lane's weight row
     const int hl = lane >> 5;
@@ -270,10 +275,17 @@ k_mmq(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
 #pragma unroll
                     for (int r = 0; r < 16; r++) {
                         const float da = Ad[(i * 32 + tile_row(r, lane)) * 4 + bl];
-                        S1[i][r] = S1[i][r] + P[i][r] * (dw * da);
+                        S1[i][r] = fmaf(da, dw * P[i][r], S1[i][r]);
                         P[i][r] = 0.0f;
                     }
             }
+        }
+        if (!KQ && ((kt + 1) % (DFX_DOT_CHUNK / BK) == 0 || kt + 1 == n_kt)) {
+            // chunk complete: T = T + S
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) { T1[i][r] = T1[i][r] + S1[i][r]; S1[i][r] = 0.0f; }
         }
         if (KQ && h == 1) {
             // super-block complete
@@ -299,8 +311,8 @@ k_mmq(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
 #pragma unroll
                     for (int r = 0; r < 16; r++) {
                         const float da = Ad[i * 32 + tile_row(r, lane)];
-                        S1[i][r] = S1[i][r] + (dw * da) * P[i][r];
-                        S2[i][r] = S2[i][r] + (dmw * da) * Q[r];
+                        const float x = fmaf(-dmw, Q[r], dw * P[i][r]);
+                        S1[i][r] = fmaf(da, x, S1[i][r]);
                         P[i][r] = 0.0f;
                     }
                 }
@@ -311,9 +323,16 @@ k_mmq(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
 #pragma unroll
                     for (int r = 0; r < 16; r++) {
                         const float da = Ad[i * 32 + tile_row(r, lane)];
-                        S1[i][r] = S1[i][r] + (dw * da) * P[i][r];
+                        S1[i][r] = fmaf(da, dw * P[i][r], S1[i][r]);
                         P[i][r] = 0.0f;
                     }
+            }
+            if (((kt >> 1) + 1) % (DFX_DOT_CHUNK / 256) == 0 || kt + 1 == n_kt) {
+                // chunk complete: T = T + S
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) { T1[i][r] = T1[i][r] + S1[i][r]; S1[i][r] = 0.0f; }
             }
         }
     }
@@ -326,9 +345,301 @@ k_mmq(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
         for (int r = 0; r < 16; r++) {
             const int m = m0 + i * 32 + tile_row(r, lane);
             if (m >= M) continue;
-            const float v = WT == DFX_TYPE_Q4_K ? S1[i][r] - S2[i][r] : S1[i][r];
+            const float v = T1[i][r];
             epilogue_store(v, m, n, bias, res, Y, ldy, ymap);
         }
+}
+
+// ---------------------------------------------------------------------------
+// Q4_K: register-blocked kernel with packed-f16 dequantisation
+// ---------------------------------------------------------------------------
+// Workgroup = 4 waves side by side along N; wave w owns TN column tiles of 32 weight
+// rows and every wave covers all TM row tiles of 32 activation rows, so a
+// dequantised B fragment feeds TM MFMAs and an A fragment (LDS) feeds TN.
+// A K step is half a super-block (128): lane (row n, half hl) holds the 32 bytes of
+// packed nibbles of group g = 2h+hl, and MFMA kk takes word kk of them.  One word w
+// (bytes b0..b3) gives the eight operands
+//   [lo b0, lo b2, lo b1, lo b3, hi b0, hi b2, hi b1, hi b3] * sc
+// as f16 integers with no conversion instructions: (w & 0x000F000F) | 0x64006400 is
+// the f16 pair (1024+lo b0, 1024+lo b2), and one packed FMA x*sc - 1024*sc leaves
+// sc*lo exactly (high nibbles: mask 0x00F000F0, factor sc/16, constant -64*sc).  The
+// activation buffer stores q in the same slot order (CONV_Q8_K_P4).
+// The weights of the next K step are loaded into registers during the current one;
+// the A tile is double-buffered in LDS (one barrier per K step).  Workgroups are
+// numbered so that all row tiles of one column tile run on the same XCD (L2).
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pk_fma_h2(uint32_t x, uint32_t a, uint32_t c) {
+    const half2v r = __builtin_elementwise_fma(__builtin_bit_cast(half2v, x), __builtin_bit_cast(half2v, a),
+                                               __builtin_bit_cast(half2v, c));
+    return __builtin_bit_cast(uint32_t, r);
+}
+__device__ __forceinline__ uint32_t h2pair(float v) {
+    const uint32_t h = (uint32_t)__builtin_bit_cast(uint16_t, (half_t)v);
+    return h | (h << 16);
+}
+
+// v_and_or_b32 (x & m) | o; the masks live in VGPRs (gfx9 VOP3 takes no literals).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(o));
+    return r;
+}
+
+// Q4_K header of one super-block held in registers: x = {d, dmin}, y/z/w = scales[0..11].
+// The eight 6-bit scales and mins (GGML get_scale_min_k4) as bytes of two words each:
+//   sc[0..3] = y & 63              sc[4..7] = (w & 15) | ((y >> 6) << 4)
+//   mn[0..3] = z & 63              mn[4..7] = (w >> 4) | ((z >> 6) << 4)
+struct q4k_sm { uint32_t sc_lo, sc_hi, mn_lo, mn_hi; };
+__device__ __forceinline__ q4k_sm q4k_unpack(const u32x4 & h) {
+    q4k_sm r;
+    r.sc_lo = h.y & 0x3F3F3F3Fu;
+    r.sc_hi = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+    r.mn_lo = h.z & 0x3F3F3F3Fu;
+    r.mn_hi = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+    return r;
+}
+
+// Scale constants of the two sub-blocks (low / high nibbles) of one 64-element group.
+struct q4k_consts { uint32_t slo, clo, shi, chi; };
+__device__ __forceinline__ q4k_consts q4k_group_consts(uint32_t sc_word, int shift) {
+    const float s0 = (float)((sc_word >> shift) & 0xFFu), s1 = (float)((sc_word >> (shift + 8)) & 0xFFu);
+    q4k_consts k;
+    k.slo = h2pair(s0);
+    k.clo = h2pair(-1024.0f * s0);
+    k.shi = h2pair(s1 * 0.0625f);
+    k.chi = h2pair(-64.0f * s1);
+    return k;
+}
+
+// Eight f16 operands [lo b0, lo b2, lo b1, lo b3, hi b0, hi b2, hi b1, hi b3] * sc from
+// one word of packed nibbles.
+__device__ __forceinline__ half8 q4k_word(uint32_t w, const q4k_consts & k, uint32_t m_lo, uint32_t m_hi,
+                                          uint32_t magic) {
+    const uint32_t s8 = w >> 8;
+    u32x4 r;
+    r.x = pk_fma_h2(and_or(w, m_lo, magic), k.slo, k.clo);
+    r.y = pk_fma_h2(and_or(s8, m_lo, magic), k.slo, k.clo);
+    r.z = pk_fma_h2(and_or(w, m_hi, magic), k.shi, k.chi);
+    r.w = pk_fma_h2(and_or(s8, m_hi, magic), k.shi, k.chi);
+    return __builtin_bit_cast(half8, r);
+}
+
+// Four 6-bit mins (bytes of m4) as the half8 [m0, m0, m1, m1, m2, m2, m3, m3].
+__device__ __forceinline__ half8 mins_half8(uint32_t m4) {
+    u32x4 r;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t v = (m4 >> (8 * k)) & 0xFFu;
+        r[k] = h2pair((float)v);
+    }
+    return __builtin_bit_cast(half8, r);
+}
+
+template <int TM, int TN, int D>
+__global__ void __launch_bounds__(256, TM * TN >= 4 ? 1 : 2)
+k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__ act, int M,
+      const float * __restrict__ bias, const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
+      int n_tiles, int m_tiles, float * __restrict__ ws) {
+#pragma clang fp contract(off)
+    constexpr int BM = TM * 32, BN = 4 * TN * 32;
+    constexpr int AST = 128 + 8;             // LDS halves per activation row and K step
+    constexpr int BST = 24;                  // LDS halves per row of 16 block sums
+    constexpr int A_PER_T = BM * 16 / 256;   // 16-byte chunks of the A tile per thread
+    __shared__ __attribute__((aligned(16))) half_t As[2][BM * AST];
+    __shared__ __attribute__((aligned(16))) float Ad[2][BM];
+    __shared__ __attribute__((aligned(16))) half_t Abs[2][BM * BST];
+
+    // XCD-aware tile order: workgroup L runs on XCD L % 8; column tile x always maps
+    // to XCD x % 8, and its row tiles are consecutive there.  With ws (split K) the
+    // grid repeats once per K chunk: chunk z = blockIdx.x / (tiles of one pass).
+    const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
+    const int z = blockIdx.x / per_pass, L = blockIdx.x - z * per_pass, xcd = L & 7, j = L >> 3;
+    const int ty = j % m_tiles, tx = 8 * (j / m_tiles) + xcd;
+    if (tx >= n_tiles) return;
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, hl = lane >> 5, l32 = lane & 31;
+    const int n0 = tx * BN, m0 = ty * BM;
+    constexpr int SB_CHUNK = DFX_DOT_CHUNK / 256;
+    const int n_sb_all = K >> 8;
+    const int sb_first = ws ? z * SB_CHUNK : 0;                       // this workgroup's super-blocks
+    const int n_sb = ws ? min(SB_CHUNK, n_sb_all - sb_first) : n_sb_all;
+    const int n_kt = 2 * n_sb;
+    const uint32_t row_bytes = (uint32_t)n_sb_all * SB_Q4_K;
+    const act_layout Lay = act_layout_of(CONV_Q8_K_P4, M, K);
+    const uint8_t * Aq = act + Lay.q;
+    const uint8_t * Adg = act + Lay.d;
+    const uint8_t * Absg = act + Lay.bs;
+
+    // Per-thread 32-bit byte offsets from bases that only move with the K step (so the
+    // loads use a scalar base and the step costs no vector instructions).  Every load
+    // is unconditional, at a clamped (always valid) address: padded rows (m >= M) only
+    // feed output rows that are never stored, and steps past the end are never used.
+    uint32_t off_a[A_PER_T], off_w[TN];
+#pragma unroll
+    for (int i = 0; i < A_PER_T; i++) {
+        const int c = tid + 256 * i, r = c >> 4, cc = c & 15;
+        off_a[i] = ((uint32_t)min(m0 + r, M - 1) * (uint32_t)K + (uint32_t)cc * 8u) * 2u;
+    }
+#pragma unroll
+    for (int t = 0; t < TN; t++) off_w[t] = (uint32_t)min(n0 + (wv * TN + t) * 32 + l32, N - 1) * row_bytes;
+    const uint32_t off_d = (uint32_t)min(m0 + tid % BM, M - 1) * (uint32_t)n_sb_all * 4u;
+    const uint32_t off_b = ((uint32_t)min(m0 + (tid >> 1) % BM, M - 1) * (uint32_t)(K / 16) + (tid & 1) * 8u) * 2u;
+
+    // Register ring: stage s holds everything K step kt (kt % D == s) reads from memory.
+    u32x4 a_st[D][A_PER_T];          // A tile chunks of this thread
+    u32x4 q_st[D][TN][2];            // this lane's 32 bytes of nibbles, per column tile
+    u32x4 h_st[D][TN];               // super-block header (even K steps)
+    float d_st[D];                   // d_a of row tid % BM (even K steps)
+    u32x4 b_st[D];                   // 8 block sums of row (tid/2) % BM (even K steps)
+
+    // Stage indices are compile-time constants (generic lambdas over integral_constant),
+    // so the ring stays in registers.  n_kt is a multiple of D (even): stage s only ever
+    // holds K steps kt with kt % D == s, hence of parity s & 1.
+    auto issue = [&](auto stage, int kt_req) __attribute__((always_inline)) {
+        constexpr int s = decltype(stage)::value, h = s & 1;
+        const int kt = 2 * sb_first + min(kt_req, n_kt - 1);      // global K step
+        const int sb = kt >> 1;
+        const uint8_t * abase = Aq + (size_t)kt * 256;
+#pragma unroll
+        for (int i = 0; i < A_PER_T; i++) a_st[s][i] = *(const u32x4 *)(abase + off_a[i]);
+        const uint8_t * wbase = W + (size_t)sb * SB_Q4_K;
+#pragma unroll
+        for (int t = 0; t < TN; t++) {
+            if (h == 0) h_st[s][t] = *(const u32x4 *)(wbase + off_w[t]);
+            q_st[s][t][0] = *(const u32x4 *)(wbase + off_w[t] + 16 + 32 * (2 * h + hl));
+            q_st[s][t][1] = *(const u32x4 *)(wbase + off_w[t] + 32 + 32 * (2 * h + hl));
+        }
+        if (h == 0) {
+            d_st[s] = *(const float *)(Adg + (size_t)sb * 4 + off_d);
+            b_st[s] = *(const u32x4 *)(Absg + (size_t)sb * 32 + off_b);
+        }
+    };
+
+    float16v P[TM][TN], S[TM][TN], T[TM][TN];
+    const float16v zero16 = {};
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int t = 0; t < TN; t++) { P[i][t] = zero16; S[i][t] = zero16; T[i][t] = zero16; }
+    u32x4 hdr[TN];
+    q4k_sm sm[TN];
+    const uint32_t MASK_LO = 0x000F000Fu, MASK_HI = 0x00F000F0u, MAGIC = 0x64006400u;
+
+    auto step = [&](auto stage, int kt) __attribute__((always_inline)) {
+        constexpr int s = decltype(stage)::value, h = s & 1, buf = s & 1;
+        const int mbuf = (kt >> 1) & 1;
+        // stage s -> LDS
+#pragma unroll
+        for (int i = 0; i < A_PER_T; i++) {
+            const int c = tid + 256 * i, r = c >> 4, cc = c & 15;
+            *(u32x4 *)(&As[buf][r * AST + cc * 8]) = a_st[s][i];
+        }
+        if (h == 0) {
+            if (tid < BM) Ad[mbuf][tid] = d_st[s];
+            if (tid < 2 * BM) *(u32x4 *)(&Abs[mbuf][(tid >> 1) * BST + (tid & 1) * 8]) = b_st[s];
+#pragma unroll
+            for (int t = 0; t < TN; t++) {
+                hdr[t] = h_st[s][t];
+                sm[t] = q4k_unpack(hdr[t]);
+            }
+        }
+        __syncthreads();
+        // keep D-1 K steps in flight
+        issue(std::integral_constant<int, (s + D - 1) % D>{}, kt + D - 1);
+
+        // group g = 2h + hl: scales of sub-blocks 4h + 2hl and 4h + 2hl + 1
+        q4k_consts kc[TN];
+#pragma unroll
+        for (int t = 0; t < TN; t++) kc[t] = q4k_group_consts(h == 0 ? sm[t].sc_lo : sm[t].sc_hi, 16 * hl);
+        // all A fragments of the step in flight at once (one LDS latency per step)
+        half8 afr[8][TM];
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++)
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                afr[kk][i] = *(const half8 *)(&As[buf][(i * 32 + l32) * AST + 64 * hl + 8 * kk]);
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) {
+            half8 b[TN];
+#pragma unroll
+            for (int t = 0; t < TN; t++) b[t] = q4k_word(q_st[s][t][kk >> 2][kk & 3], kc[t], MASK_LO, MASK_HI, MAGIC);
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+#pragma unroll
+                for (int t = 0; t < TN; t++)
+                    P[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afr[kk][i], b[t],
+                                                                     (h == 0 && kk == 0) ? zero16 : P[i][t], 0, 0, 0);
+            }
+        }
+
+        if (h == 1) {
+            // super-block complete: x = d_w*isum; x = fma(-dmin_w, msum, x); S = fma(d_a, x, S)
+#pragma unroll
+            for (int t = 0; t < TN; t++) {
+                const half8 bm = mins_half8(hl ? sm[t].mn_hi : sm[t].mn_lo);
+                const float dw = h2f((uint16_t)(hdr[t].x & 0xFFFFu)), dmw = h2f((uint16_t)(hdr[t].x >> 16));
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+                    const half8 a = *(const half8 *)(&Abs[mbuf][(i * 32 + l32) * BST + 8 * hl]);
+                    const float16v Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bm, zero16, 0, 0, 0);
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; q4++) {
+                        const float4 da = *(const float4 *)(&Ad[mbuf][i * 32 + 8 * q4 + 4 * hl]);
+                        const float dav[4] = {da.x, da.y, da.z, da.w};
+#pragma unroll
+                        for (int rr = 0; rr < 4; rr++) {
+                            const int r = 4 * q4 + rr;
+                            const float x = fmaf(-dmw, Q[r], dw * P[i][t][r]);
+                            S[i][t][r] = fmaf(dav[rr], x, S[i][t][r]);
+                        }
+                    }
+                }
+            }
+            // chunk complete: T = T + S
+            const int sb_local = kt >> 1;
+            if ((sb_first + sb_local + 1) % SB_CHUNK == 0 || sb_local + 1 == n_sb) {
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int t = 0; t < TN; t++) {
+                        T[i][t] = T[i][t] + S[i][t];
+                        S[i][t] = zero16;
+                    }
+            }
+        }
+    };
+
+    issue(std::integral_constant<int, 0>{}, 0);
+    if constexpr (D == 4) {
+        issue(std::integral_constant<int, 1>{}, 1);
+        issue(std::integral_constant<int, 2>{}, 2);
+    }
+    for (int kt0 = 0; kt0 < n_kt; kt0 += D) {
+        step(std::integral_constant<int, 0>{}, kt0);
+        step(std::integral_constant<int, 1>{}, kt0 + 1);
+        if constexpr (D == 4) {
+            step(std::integral_constant<int, 2>{}, kt0 + 2);
+            step(std::integral_constant<int, 3>{}, kt0 + 3);
+        }
+    }
+
+    // split K: the chunk sum goes to ws[z][m][n]; the reduction adds the chunks in order
+#pragma unroll
+    for (int t = 0; t < TN; t++) {
+        const int n = n0 + (wv * TN + t) * 32 + l32;
+        if (n >= N) continue;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + i * 32 + tile_row(r, lane);
+                if (m >= M) continue;
+                if (ws) ws[((int64_t)z * M + m) * N + n] = T[i][t][r];
+                else epilogue_store(T[i][t][r], m, n, bias, res, Y, ldy, ymap);
+            }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -392,15 +703,19 @@ __global__ void k_gemm_reduce(const float * __restrict__ ws, int S, int64_t MN, 
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < MN;
          idx += (int64_t)gridDim.x * blockDim.x) {
         const int64_t m = idx / N, n = idx - m * N;
-        float v = ws[idx];
-        for (int s = 1; s < S; s++) v += ws[(int64_t)s * MN + idx];
+        float v = 0.0f;
+        for (int s = 0; s < S; s++) v = v + ws[(int64_t)s * MN + idx];
         epilogue_store(v, (int)m, (int)n, bias, res, Y, ldy, ymap);
     }
 }
 
 #define MAX_SPLIT 8
 
-extern "C" size_t dfx_gemm_ws_bytes(int64_t M, int64_t N) { return (size_t)MAX_SPLIT * M * N * sizeof(float); }
+// Split-K partials: F16 up to MAX_SPLIT slices, quantised types one slice per K chunk.
+extern "C" size_t dfx_gemm_ws_bytes(int64_t M, int64_t N, int64_t K) {
+    const int64_t slices = std::max<int64_t>(MAX_SPLIT, dot_chunks(K));
+    return (size_t)slices * M * N * sizeof(float);
+}
 
 template <int TM>
 static int launch_f16(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
@@ -443,6 +758,81 @@ static int launch_mmq(const void * w, int N, int K, const void * act, int M, con
     return DFX_OK;
 }
 
+template <int TM, int TN, int D>
+static int launch_q4k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
+                      float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st) {
+    constexpr int BM = TM * 32, BN = 4 * TN * 32;
+    const int n_tiles = (N + BN - 1) / BN, m_tiles = (M + BM - 1) / BM;
+    const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
+    const int chunks = dot_chunks(K), passes = ws ? chunks : 1;
+    static_assert(D == 2 || D == 4, "ring depth 2 or 4");
+    // every workgroup's K steps (whole super-blocks, two per super-block) must be a
+    // multiple of the ring depth
+    const int sb = K / 256, sb_last = sb - (chunks - 1) * (DFX_DOT_CHUNK / 256);
+    if ((2 * (ws ? sb_last : sb)) % D || (ws && chunks > 1 && (2 * (DFX_DOT_CHUNK / 256)) % D)) {
+        dfx_set_error("dfx_gemm q4_k: K=%d does not fit the pipeline depth %d", K, D);
+        return DFX_ERR_ARG;
+    }
+    hipLaunchKernelGGL((k_q4k<TM, TN, D>), dim3((unsigned)(per_pass * passes)), dim3(256), 0, st,
+                       (const uint8_t *)w, N, K, (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles, ws);
+    DFX_CHECK_LAUNCH("dfx_gemm q4_k");
+    if (ws) {
+        const int64_t MN = (int64_t)M * N;
+        const int64_t blocks = std::min<int64_t>((MN + 255) / 256, 8192);
+        hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)blocks), dim3(256), 0, st, (const float *)ws, chunks, MN, N,
+                           bias, res, y, ldy, ymap);
+        DFX_CHECK_LAUNCH("dfx_gemm q4_k reduce");
+    }
+    return DFX_OK;
+}
+
+// Tile of the Q4_K kernel (TM x TN 32x32 tiles per wave, D = K steps in flight).
+// When the grid leaves the SIMDs short of two waves each, K is split at chunk
+// borders (workspace permitting).
+static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
+                        float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st) {
+    struct cand { int tm, tn, d; };
+    static const cand cands[] = {{2, 2, 2}, {4, 1, 2}, {3, 1, 2}, {2, 1, 2}, {1, 2, 2}, {1, 1, 4},
+                                 {1, 1, 2}};
+    constexpr int n_cand = 7;
+    // measured on MI355X for the LLaDA-8B shapes (N 4096..24576, K 4096/12288,
+    // M 50..288): 64x128 workgroup tiles with a 2-deep ring win from M ~ 100 up,
+    // 32x128 tiles with a 4-deep ring below
+    int pick = M > 96 ? 3 : 5;
+    const int chunks = dot_chunks(K);
+    int64_t tiles;
+    {
+        const int BM = 32 * cands[pick].tm, BN = 128 * cands[pick].tn;
+        tiles = (int64_t)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    }
+    bool split = chunks > 1 && tiles * 4 < 2048 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
+    // DFX_Q4K_TILE="<TM>x<TN>[x<D>][s|n]" forces a configuration (tuning, tests):
+    // s = split K when possible, n = never split.
+    if (const char * f = getenv("DFX_Q4K_TILE")) {
+        int tm = 0, tn = 0, d = 0;
+        const int got = sscanf(f, "%dx%dx%d", &tm, &tn, &d);
+        if (got >= 2)
+            for (int c = n_cand - 1; c >= 0; c--)
+                if (cands[c].tm == tm && cands[c].tn == tn && (got < 3 || cands[c].d == d)) pick = c;
+        if (strchr(f, 's')) split = chunks > 1 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
+        if (strchr(f, 'n')) split = false;
+    }
+    // a 4-deep ring needs a multiple of 4 K steps in every workgroup
+    const int sb = K / 256, sb_last = sb - (chunks - 1) * (DFX_DOT_CHUNK / 256);
+    if (cands[pick].d == 4 && ((split ? sb_last : sb) % 2))
+        for (int c = 0; c < n_cand; c++)
+            if (cands[c].tm == cands[pick].tm && cands[c].tn == cands[pick].tn && cands[c].d == 2) { pick = c; break; }
+    float * wsf = split ? (float *)ws : nullptr;
+#define Q4K_CASE(c, TM_, TN_, D_) \
+    case c: return launch_q4k<TM_, TN_, D_>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st);
+    switch (pick) {
+        Q4K_CASE(0, 2, 2, 2) Q4K_CASE(1, 4, 1, 2) Q4K_CASE(2, 3, 1, 2) Q4K_CASE(3, 2, 1, 2) Q4K_CASE(4, 1, 2, 2)
+        Q4K_CASE(5, 1, 1, 4)
+        default: return launch_q4k<1, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st);
+    }
+#undef Q4K_CASE
+}
+
 // M tile (32 * TM rows) with the least row padding, larger tiles on ties.
 static int pick_tm(int M, int max_tm) {
     int best = 1, best_pad = 1 << 30;
@@ -478,7 +868,7 @@ int dfx_gemm_ex(int wtype, const void * w, int64_t N, int64_t K, const void * ac
     hipStream_t st = (hipStream_t)stream;
     const int n = (int)N, k = (int)K, m = (int)M;
     switch (wtype) {
-        case DFX_TYPE_Q4_K: return dispatch_mmq<DFX_TYPE_Q4_K>(w, n, k, act, m, bias, residual, y, ldy, ymap, st);
+        case DFX_TYPE_Q4_K: return dispatch_q4k(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st);
         case DFX_TYPE_Q6_K: return dispatch_mmq<DFX_TYPE_Q6_K>(w, n, k, act, m, bias, residual, y, ldy, ymap, st);
         case DFX_TYPE_Q8_0: return dispatch_mmq<DFX_TYPE_Q8_0>(w, n, k, act, m, bias, residual, y, ldy, ymap, st);
         case DFX_TYPE_F16:
@@ -496,5 +886,5 @@ int dfx_gemm_ex(int wtype, const void * w, int64_t N, int64_t K, const void * ac
 extern "C" int dfx_gemm(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
                         const float * bias, const float * residual, float * y, void * ws, void * stream) {
     return dfx_gemm_ex(wtype, w, N, K, act, M, bias, residual, y, N, nullptr, ws,
-                       ws ? dfx_gemm_ws_bytes(M, N) : 0, stream);
+                       ws ? dfx_gemm_ws_bytes(M, N, K) : 0, stream);
 }

@@ -97,7 +97,7 @@ __device__ __forceinline__ void convert_block256(const float v[4], int lane, int
 #pragma clang fp contract(off)
     uint16_t * q = (uint16_t *)(act + Lay.q) + m * K + b * 256 + 4 * lane;
     uint16_t o[4];
-    if (mode == CONV_Q8_K) {
+    if (conv_is_q8k(mode)) {
         // GGML quantize_row_q8_K_ref: max = the signed value of the first element
         // with the largest |x|; iscale = -127/max; q = min(127, nearest_int(iscale*x));
         // d = 1/iscale; bsums over 16.  All-zero block -> d = 0, q = 0.
@@ -122,7 +122,14 @@ __device__ __forceinline__ void convert_block256(const float v[4], int lane, int
             for (int j = 0; j < 4; j++) qi[j] = min((int)__builtin_rintf(iscale * v[j]), 127);
         }
         for (int j = 0; j < 4; j++) o[j] = f2h((float)qi[j]);
-        store_q4(q, o);
+        if (mode == CONV_Q8_K_P4) {
+            // elements 4L..4L+3 of a 64-group (L = lane % 16) go to slots 8(L%8) + 4(L/8) + {0,2,1,3}
+            const int L = lane & 15;
+            const uint16_t p[4] = {o[0], o[2], o[1], o[3]};
+            store_q4((uint16_t *)(act + Lay.q) + m * K + b * 256 + 64 * (lane >> 4) + 8 * (L & 7) + 4 * (L >> 3), p);
+        } else {
+            store_q4(q, o);
+        }
         int s = qi[0] + qi[1] + qi[2] + qi[3];
         s += __shfl_xor(s, 1, WAVE);
         s += __shfl_xor(s, 2, WAVE);

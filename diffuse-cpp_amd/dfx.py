@@ -105,7 +105,7 @@ def _declare(L):
         "dfx_act_convert": (I32, [I32, P, I64, I64, P, P]),
         "dfx_rmsnorm_convert": (I32, [I32, P, P, I64, I64, F, P, P]),
         "dfx_swiglu_convert": (I32, [I32, P, I64, I64, P, P]),
-        "dfx_gemm_ws_bytes": (S, [I64, I64]),
+        "dfx_gemm_ws_bytes": (S, [I64, I64, I64]),
         "dfx_gemm": (I32, [I32, P, I64, I64, P, I64, P, P, P, P, P]),
         "dfx_rope_store": (I32, [P, P, I64, I32, I32, I32, P, P, P, P, P]),
         "dfx_attention": (I32, [P, P, P, I64, I64, I32, I32, I32, P, P]),
@@ -196,13 +196,26 @@ def device_count():
     return n.value if rc == 0 else 0
 
 
+def q4k_slot_order():
+    """Element index held by each slot of a 64-element group of a Q4_K activation
+    buffer (slot 8i+s: s<4 -> 4i+P[s], s>=4 -> 32+4i+P[s-4], P = 0,2,1,3)."""
+    P = (0, 2, 1, 3)
+    return np.array([(32 if s >= 4 else 0) + 4 * i + P[s % 4] for i in range(8) for s in range(8)], np.int64)
+
+
 def act_parts(act_buf, wtype, M, K):
-    """Split a downloaded activation buffer (layout of dfx_act_bytes) into (q, d, bs)."""
+    """Split a downloaded activation buffer (layout of dfx_act_bytes) into (q, d, bs);
+    q is returned in element order."""
     raw = act_buf.download(np.uint8)
 
     def a256(x):
         return (x + 255) // 256 * 256
     q = raw[:M * K * 2].view(np.float16).reshape(M, K)
+    if wtype == TYPE_Q4_K:
+        stored = q.reshape(M, K // 64, 64)
+        q = np.empty_like(stored)
+        q[:, :, q4k_slot_order()] = stored
+        q = q.reshape(M, K)
     d_off = a256(M * K * 2)
     if wtype in (TYPE_Q4_K, TYPE_Q6_K):
         nd, nbs = M * (K // 256), M * (K // 16)

@@ -102,7 +102,10 @@ int ensure_capacity(diffuse_context * c, int N) {
     TRY(A((void **)&c->d_hmap, n * 4));
     TRY(A((void **)&c->d_srows, n * 4));
     TRY(A((void **)&c->d_spos, n * 4));
-    c->ws_bytes = dfx_gemm_ws_bytes(n, std::max(D.nqkv, D.d));
+    // split-K workspace for the GEMMs with few output tiles (Q|K|V, O, down); gate|up
+    // (N = 2F) always has enough tiles and gets whatever fits
+    c->ws_bytes = std::max(std::max(dfx_gemm_ws_bytes(n, D.nqkv, D.d), dfx_gemm_ws_bytes(n, D.d, D.d)),
+                           dfx_gemm_ws_bytes(n, D.d, D.F));
     TRY(A(&c->ws, c->ws_bytes));
     TRY(A((void **)&c->d_stats, n * sizeof(dfx_row_stat)));
     TRY(A((void **)&c->d_cand, n * sizeof(dfx_candidate)));

@@ -109,10 +109,11 @@ int dfx_swiglu_convert(int wtype, const float * gu, int64_t M, int64_t F, void *
  *   y[m][n] = sum_k x[m][k] * W[n][k]  (+ bias[n])  (+ residual[m][n])
  * act: the converted activations of x (dfx_*_convert with the same wtype);
  * W: device-layout [N][K]; y f32 [M][N].  For Q4_K / Q6_K / Q8_0 the result
- * equals GGML's integer block dot products scaled and summed in K order, i.e. the
- * CPU mul_mat value for value.  residual may alias y (in-place residual add).
- * ws: split-K workspace of dfx_gemm_ws_bytes(M, N) bytes or NULL (used by F16). */
-size_t dfx_gemm_ws_bytes(int64_t M, int64_t N);
+ * equals GGML's integer block dot products scaled and summed in a fixed K order
+ * (chunks of 2048 elements, chunk sums added in order), i.e. the CPU mul_mat value
+ * for value.  residual may alias y (in-place residual add).
+ * ws: split-K workspace of dfx_gemm_ws_bytes(M, N, K) bytes, or NULL (no split). */
+size_t dfx_gemm_ws_bytes(int64_t M, int64_t N, int64_t K);
 int dfx_gemm(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
              const float * bias, const float * residual, float * y, void * ws, void * stream);
 

@@ -5,7 +5,8 @@
  * CPU baseline.  The product never links, loads or calls this file.
  *
  * Compiled with -ffp-contract=off so every a*b+c rounds twice, as the reference's
- * own files (built for baseline x86-64, no FMA) and GGML's scalar codecs do.
+ * own files (built for baseline x86-64, no FMA) and GGML's scalar codecs do; the
+ * only fused multiply-adds are the explicit fmaf() calls of the block dot products.
  *
  * Parity pins (what fixes each function; the tests live in tests/test_oracle_*.py):
  *   fp16 conversion ........ numpy float16 (IEEE binary16, round-to-nearest-even), all 65536 codes
@@ -281,8 +282,19 @@ static inline int32_t i8_dot32(const int8_t * a, const int8_t * b) {
     return hsum_i32(_mm256_madd_epi16(p, _mm256_set1_epi16(1)));
 }
 
+/* Block dot products.  Integer parts are GGML's (exact int32 sums); the float part
+ * folds the block scales in a fixed order that the GPU kernels reproduce bit for bit:
+ *   Q4_K  x = d_w*isum;  x = fma(-dmin_w, msum, x);  S = fma(d_a, x, S)
+ *   Q6_K  x = d_w*isum;  S = fma(d_a, x, S)
+ *   Q8_0  x = d_w*isum;  S = fma(d_a, x, S)         (per 32-element block)
+ * The K range is cut into chunks of ORC_DOT_CHUNK elements: S restarts at 0 in every
+ * chunk and the chunk sums are added in order, T = T + S (T starts at 0).  GGML folds
+ * the same factors as (d_w*d_a)*isum, in float, in its own SIMD lane order; the value
+ * is the same up to float rounding. */
+#define ORC_DOT_CHUNK 2048
 static float dot_q4_K_q8_K(int64_t n, const blk_q4_K * x, const blk_q8_K * y) {
-    float sum_sc = 0.0f, sum_m = 0.0f;
+    float T = 0.0f, S = 0.0f;
+    const int64_t per = ORC_DOT_CHUNK / QK_K;
     for (int64_t i = 0; i < n / QK_K; i++) {
         uint8_t sc[8], mn[8];
         for (int j = 0; j < 8; j++) q4k_scale_min(j, x[i].scales, &sc[j], &mn[j]);
@@ -290,16 +302,18 @@ static float dot_q4_K_q8_K(int64_t n, const blk_q4_K * x, const blk_q8_K * y) {
         int32_t msum = 0;
         for (int j = 0; j < 8; j++)
             msum += (int32_t)mn[j] * ((int32_t)y[i].bsums[2 * j] + (int32_t)y[i].bsums[2 * j + 1]);
-        const float d    = orc_fp16_to_fp32(x[i].d) * y[i].d;
-        const float dmin = orc_fp16_to_fp32(x[i].dmin) * y[i].d;
-        sum_sc += d * (float)isum;
-        sum_m  += dmin * (float)msum;
+        const float dw = orc_fp16_to_fp32(x[i].d), dmw = orc_fp16_to_fp32(x[i].dmin);
+        float t = dw * (float)isum;
+        t = fmaf(-dmw, (float)msum, t);
+        S = fmaf(y[i].d, t, S);
+        if ((i + 1) % per == 0 || i + 1 == n / QK_K) { T = T + S; S = 0.0f; }
     }
-    return sum_sc - sum_m;
+    return T;
 }
 
 static float dot_q6_K_q8_K(int64_t n, const blk_q6_K * x, const blk_q8_K * y) {
-    float sum = 0.0f;
+    float T = 0.0f, sum = 0.0f;
+    const int64_t per = ORC_DOT_CHUNK / QK_K;
     uint8_t u6[QK_K];
     for (int64_t i = 0; i < n / QK_K; i++) {
         /* unpack q + 32 (ql low/high nibbles and qh 2-bit fields, GGML block_q6_K order) */
@@ -318,19 +332,23 @@ static float dot_q6_K_q8_K(int64_t n, const blk_q6_K * x, const blk_q8_K * y) {
         int32_t corr = 0;
         for (int j = 0; j < 16; j++) corr += (int32_t)x[i].scales[j] * (int32_t)y[i].bsums[j];
         const int32_t isum = q6k_usum(u6, y[i].qs, x[i].scales) - 32 * corr;
-        const float d = orc_fp16_to_fp32(x[i].d) * y[i].d;
-        sum += d * (float)isum;
+        const float t = orc_fp16_to_fp32(x[i].d) * (float)isum;
+        sum = fmaf(y[i].d, t, sum);
+        if ((i + 1) % per == 0 || i + 1 == n / QK_K) { T = T + sum; sum = 0.0f; }
     }
-    return sum;
+    return T;
 }
 
 static float dot_q8_0_q8_0(int64_t n, const blk_q8_0 * x, const blk_q8_0 * y) {
-    float sum = 0.0f;
+    float T = 0.0f, sum = 0.0f;
+    const int64_t per = ORC_DOT_CHUNK / QK8_0;
     for (int64_t i = 0; i < n / QK8_0; i++) {
         const int32_t s = i8_dot32(x[i].qs, y[i].qs);
-        sum += (float)s * (orc_fp16_to_fp32(x[i].d) * orc_fp16_to_fp32(y[i].d));
+        const float t = orc_fp16_to_fp32(x[i].d) * (float)s;
+        sum = fmaf(orc_fp16_to_fp32(y[i].d), t, sum);
+        if ((i + 1) % per == 0 || i + 1 == n / QK8_0) { T = T + sum; sum = 0.0f; }
     }
-    return sum;
+    return T;
 }
 
 static float dot_f16_f16(int64_t n, const uint16_t * x, const uint16_t * y) {
@@ -342,6 +360,15 @@ static float dot_f16_f16(int64_t n, const uint16_t * x, const uint16_t * y) {
 static float dot_f32(int64_t n, const float * x, const float * y) {
     double s = 0.0;
     for (int64_t i = 0; i < n; i++) s += (double)(x[i] * y[i]);
+    return (float)s;
+}
+
+/* Attention dot products: f32 x f32 products are exact in f64 and are summed in f64,
+ * then rounded once, so the float result does not depend on the summation order
+ * (the CPU path accumulates in its own SIMD order; the value it approximates is this). */
+static float dot_f32_exact(int64_t n, const float * x, const float * y) {
+    double s = 0.0;
+    for (int64_t i = 0; i < n; i++) s += (double)x[i] * (double)y[i];
     return (float)s;
 }
 
@@ -499,7 +526,7 @@ static void attention(const float * q, const float * k, const float * v, int M, 
             const float * qm = q + ((size_t)m * H + h) * hd;
             float mx = -INFINITY;
             for (int n = 0; n < n_keys; n++) {
-                s[n] = dot_f32(hd, k + ((size_t)n * H + h) * hd, qm) * scale;
+                s[n] = dot_f32_exact(hd, k + ((size_t)n * H + h) * hd, qm) * scale;
                 mx = fmaxf(mx, s[n]);
             }
             double sum = 0.0;
@@ -509,11 +536,16 @@ static void attention(const float * q, const float * k, const float * v, int M, 
             float * o = out + (size_t)m * H * hd + (size_t)h * hd;
             for (int dd = 0; dd < hd; dd++) {
                 double acc = 0.0;
-                for (int n = 0; n < n_keys; n++) acc += (double)(v[((size_t)n * H + h) * hd + dd] * s[n]);
+                for (int n = 0; n < n_keys; n++) acc += (double)v[((size_t)n * H + h) * hd + dd] * (double)s[n];
                 o[dd] = (float)acc;
             }
         }
     }
+}
+
+extern "C" void orc_attention(const float * q, const float * k, const float * v, int M, int n_keys, int H, int hd,
+                              float * out, int n_threads) {
+    attention(q, k, v, M, n_keys, H, hd, out, n_threads);
 }
 
 /* GQA repeat (src/diffuse-graph.cpp:84-95): query head h reads KV head h / n_rep. */

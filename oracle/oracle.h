@@ -63,6 +63,9 @@ void orc_rope_table(int n_pos, int head_dim, float theta_base, float * tab);
 void orc_rope_neox(float * x, int64_t M, int n_heads, int head_dim, const int32_t * pos,
                    const float * tab);
 float orc_silu(float x);
+/* Bidirectional attention, q [M][H][hd], k/v [n_keys][H][hd] (heads already expanded), out [M][H*hd]. */
+void  orc_attention(const float * q, const float * k, const float * v, int M, int n_keys, int H, int hd,
+                    float * out, int n_threads);
 
 /* ---- model ---- */
 typedef struct {

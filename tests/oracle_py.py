@@ -37,6 +37,7 @@ def oracle():
         L.orc_rope_neox.argtypes = [P, I64, I, I, P, P]
         L.orc_silu.restype = C.c_float
         L.orc_silu.argtypes = [C.c_float]
+        L.orc_attention.argtypes = [P, P, P, I, I, I, I, P, I]
         L.orc_tokens_to_unmask.argtypes = [I, I, I, I]
         L.orc_entropy.restype = C.c_float
         L.orc_entropy.argtypes = [P, I]
@@ -117,6 +118,18 @@ def rope_table(n_pos, hd, base):
     tab = np.empty(n_pos * hd, dtype=np.float32)
     oracle().orc_rope_table(n_pos, hd, base, ptr(tab))
     return tab
+
+
+def attention(q, k, v, n_threads=8):
+    """q [M][H][hd], k/v [n_keys][Hkv][hd] (GQA: head h reads KV head h // (H/Hkv)) -> [M][H][hd]."""
+    M, H, hd = q.shape
+    rep = H // k.shape[1]
+    ke = np.ascontiguousarray(np.repeat(k, rep, axis=1), dtype=np.float32)
+    ve = np.ascontiguousarray(np.repeat(v, rep, axis=1), dtype=np.float32)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    out = np.empty((M, H, hd), np.float32)
+    oracle().orc_attention(ptr(q), ptr(ke), ptr(ve), M, k.shape[0], H, hd, ptr(out), n_threads)
+    return out
 
 
 def entropy(row):

@@ -130,7 +130,7 @@ def gpu_gemm(typ, raw, N, K, X, ws=True):
     w = to_device_weights(typ, raw, N, K)
     xb, ab, yb = dfx.Buf.of(X), dfx.Buf(L().dfx_act_bytes(typ, M, K)), dfx.Buf(M * N * 4)
     dfx.check(L().dfx_act_convert(typ, xb.ptr, M, K, ab.ptr, None), "convert")
-    wsb = dfx.Buf(L().dfx_gemm_ws_bytes(M, N)) if ws else None
+    wsb = dfx.Buf(L().dfx_gemm_ws_bytes(M, N, K)) if ws else None
     dfx.check(L().dfx_gemm(typ, w.ptr, N, K, ab.ptr, M, None, None, yb.ptr, wsb.ptr if ws else None, None), "gemm")
     return yb.download(np.float32, shape=(M, N))
 
@@ -143,6 +143,33 @@ def test_gemm_quantized_bit_exact(gpu, typ, N, K, M):
     X = rng.standard_normal((M, K)).astype(np.float32)
     got = gpu_gemm(typ, raw, N, K, X)
     ref = O.mul_mat(typ, raw, N, K, X)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
+
+
+@pytest.mark.parametrize("tile", ["2x2x2", "4x1x2", "3x1x2", "2x1x2", "1x2x2", "1x1x4", "1x1x2"])
+@pytest.mark.parametrize("N,K,M", [(1000, 2048, 77), (4096, 4096, 288)])
+def test_gemm_q4k_every_tile_bit_exact(gpu, monkeypatch, tile, N, K, M):
+    """Every register tile of the Q4_K kernel (forced with DFX_Q4K_TILE), with ragged
+    N and M, reproduces the oracle bit for bit."""
+    monkeypatch.setenv("DFX_Q4K_TILE", tile)
+    raw = quant(dfx.TYPE_Q4_K, N, K)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    got = gpu_gemm(dfx.TYPE_Q4_K, raw, N, K, X)
+    ref = O.mul_mat(dfx.TYPE_Q4_K, raw, N, K, X)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
+
+
+@pytest.mark.parametrize("tile", ["1x1x4s", "2x1x2s", "1x2x2s"])
+@pytest.mark.parametrize("N,K,M", [(512, 12288, 70), (1000, 3584, 33), (640, 2304, 40), (4096, 4096, 256)])
+def test_gemm_q4k_split_k_bit_exact(gpu, monkeypatch, tile, N, K, M):
+    """Split K (one workgroup per 2048-element chunk, chunk sums added in order by the
+    reduction) gives the same bits as the oracle's chunked K order; covers a short last
+    chunk (3584 = 2048 + 1536) and a last chunk of one super-block (2304)."""
+    monkeypatch.setenv("DFX_Q4K_TILE", tile)
+    raw = quant(dfx.TYPE_Q4_K, N, K)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    got = gpu_gemm(dfx.TYPE_Q4_K, raw, N, K, X)
+    ref = O.mul_mat(dfx.TYPE_Q4_K, raw, N, K, X)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
 
 
@@ -202,8 +229,12 @@ def test_rope_store_matches_oracle(gpu):
 
 
 @pytest.mark.parametrize("M,n_keys,H,Hkv,hd", [(288, 288, 32, 32, 128), (50, 288, 32, 32, 128),
-                                               (128, 128, 28, 4, 128), (7, 768, 8, 2, 64), (3, 2000, 4, 4, 128)])
-def test_attention_matches_f64(gpu, M, n_keys, H, Hkv, hd):
+                                               (128, 128, 28, 4, 128), (7, 768, 8, 2, 64), (3, 2000, 4, 4, 128),
+                                               (2, 3000, 2, 1, 128), (17, 1, 4, 4, 128), (33, 21, 4, 2, 64)])
+def test_attention_matches_oracle_and_f64(gpu, M, n_keys, H, Hkv, hd):
+    """Bit-exact with the oracle (f64 accumulation of exact products, correctly rounded
+    exp), and within 1e-6 of an independent f64 evaluation.  Covers the matrix-core
+    kernel (score rows in LDS) and the VALU kernel (3000 keys)."""
     q = rng.standard_normal((M, H, hd)).astype(np.float32)
     k = rng.standard_normal((n_keys, Hkv, hd)).astype(np.float32)
     v = rng.standard_normal((n_keys, Hkv, hd)).astype(np.float32)
@@ -218,6 +249,8 @@ def test_attention_matches_f64(gpu, M, n_keys, H, Hkv, hd):
     p /= p.sum(-1, keepdims=True)
     ref = np.einsum("hmn,nhd->mhd", p, vd)
     assert rel_l2(got, ref) < 1e-6
+    exact = O.attention(q, k, v)
+    assert np.array_equal(got, exact), int((got != exact).sum())
 
 
 # ---------------------------------------------------------------- sampler kernels

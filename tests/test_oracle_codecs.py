@@ -249,6 +249,31 @@ def test_rope_neox_rotates_half_pairs():
     assert np.allclose(np.hypot(y[..., :hd // 2], y[..., hd // 2:]), np.hypot(x0, x1), rtol=1e-5)
 
 
+@pytest.mark.parametrize("M,n_keys,H,Hkv,hd", [(5, 37, 4, 4, 128), (9, 64, 8, 2, 64)])
+def test_attention_bruteforce_and_invariances(M, n_keys, H, Hkv, hd):
+    """f64 brute force of softmax(q k^T / sqrt(hd)) v with head h reading KV head
+    h // (H/Hkv); the result is invariant (bitwise) to the order of the keys."""
+    r = np.random.default_rng(7)
+    q = r.standard_normal((M, H, hd)).astype(np.float32) * 2
+    k = r.standard_normal((n_keys, Hkv, hd)).astype(np.float32)
+    v = r.standard_normal((n_keys, Hkv, hd)).astype(np.float32)
+    got = O.attention(q, k, v)
+    rep = H // Hkv
+    kd, vd = np.repeat(k.astype(np.float64), rep, 1), np.repeat(v.astype(np.float64), rep, 1)
+    s = np.einsum("mhd,nhd->hmn", q.astype(np.float64), kd) / np.sqrt(hd)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    ref = np.einsum("hmn,nhd->mhd", p, vd)
+    assert np.abs(got - ref).max() < 1e-5 * np.abs(ref).max()
+    perm = r.permutation(n_keys)
+    assert np.array_equal(O.attention(q, k[perm], v[perm]), got)
+    # one dominant key: the output is (almost) that key's value row
+    q1 = q[:1, ::rep].repeat(rep, axis=1)            # heads of one KV group share the query
+    k2 = k.copy()
+    k2[3] = q1[0, ::rep] * 50
+    assert np.allclose(O.attention(q1, k2, v)[0], np.repeat(v[3], rep, 0), atol=1e-4)
+
+
 def test_silu():
     for v in (-20.0, -1.0, 0.0, 0.5, 3.0, 30.0):
         assert abs(O.oracle().orc_silu(v) - v / (1 + np.exp(-v))) < 1e-6 * max(1, abs(v))
