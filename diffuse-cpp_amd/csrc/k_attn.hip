@@ -1,7 +1,9 @@
 // k_attn.hip — NEOX RoPE + KV-cache store, and bidirectional attention.
 //
-// The inter-step cache lives in HBM as kc/vc[pos][n_head_kv][head_dim] f32 per
-// layer.  The reference keeps it expanded to n_head (src/diffuse-cache.h:23-26)
+// The inter-step cache lives in HBM per layer as kc[pos][n_head_kv][head_dim] and the
+// transposed vt[n_head_kv][head_dim][capacity] (f32); the attention reads four
+// consecutive keys of one value column with one 16-byte load.  The reference keeps
+// it expanded to n_head (src/diffuse-cache.h:23-26)
 // and concatenates [cached ‖ active] keys (src/diffuse-graph.cpp:524-525); here the
 // active rows are scattered into the cache first and every query attends over the
 // cache in position order.  Softmax without a mask is invariant to key order, and
@@ -13,7 +15,7 @@
 // One thread per (row, head of Q|K|V, rotation pair).
 __global__ void k_rope_store(const float * __restrict__ qkv, const int32_t * __restrict__ pos, int64_t M, int H,
                              int Hkv, int hd, const float * __restrict__ tab, float * __restrict__ q_out,
-                             float * __restrict__ kc, float * __restrict__ vc) {
+                             float * __restrict__ kc, float * __restrict__ vt, int64_t v_ld) {
 #pragma clang fp contract(off)
     const int half = hd / 2, heads = H + 2 * Hkv;
     const int64_t total = M * heads * half;
@@ -37,9 +39,9 @@ __global__ void k_rope_store(const float * __restrict__ qkv, const int32_t * __r
             dst[i] = y0;
             dst[i + half] = y1;
         } else {
-            float * dst = vc + ((int64_t)p * Hkv + (hh - H - Hkv)) * hd;
-            dst[i] = x0;
-            dst[i + half] = x1;
+            float * dst = vt + (int64_t)(hh - H - Hkv) * hd * v_ld + p;
+            dst[(int64_t)i * v_ld] = x0;
+            dst[(int64_t)(i + half) * v_ld] = x1;
         }
     }
 }
@@ -60,23 +62,30 @@ __device__ __forceinline__ double4v mfma_f64(double a, double b, double4v c) {
     return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
 }
 
-// Matrix-core attention: one head, RT tiles of 16 query rows per workgroup (4 waves).
-// Phase 1: S = Q K^T on the f64 MFMA, each wave taking key tiles of 16 (two at a time);
-// a reduction step of 16 head dims is split so that lane group g = l/16 supplies dims
-// 16s+4g+c to MFMA c (c < 4): one float4 load per lane per operand and step.
+// Matrix-core attention: one head and 16 query rows per workgroup (4 waves).
+// Phase 1: S = Q K^T on the f64 MFMA; each wave takes key tiles of 16 (t = wave + 4j),
+// the next tile's keys are loaded while the current one multiplies, and the 128
+// head dims are reduced in two independent accumulation chains (dims 16s+4g+c to
+// MFMA c for step s, chains s even / odd), added at the end.
 // Phase 2: softmax, one wave per row, scores resident in LDS.
-// Phase 3: O = P V on the f64 MFMA; each wave owns head-dim column tiles, keys are
-// the reduction (keys 16s+4g+c to MFMA c, the same split).
-template <int HD, int RT>
+// Phase 3: O = P V on the f64 MFMA; wave w owns head-dim columns 16w+64ct+(0..15),
+// keys are the reduction: lane group g supplies keys 16s+4g+c to MFMA c, read as one
+// float4 of the transposed value cache, two key steps ahead.
+// Workgroups are numbered so that all query tiles of head h run on XCD h % 8.
+template <int HD>
 __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q, const float * __restrict__ kc,
-                                                   const float * __restrict__ vc, int M, int n_keys, int H, int Hkv,
-                                                   int sstride, float * __restrict__ out) {
+                                                   const float * __restrict__ vt, int64_t v_ld, int M, int n_keys,
+                                                   int H, int Hkv, int sstride, int q_tiles,
+                                                   float * __restrict__ out) {
 #pragma clang fp contract(off)
-    extern __shared__ float S[];       // [RT*16][sstride] scores, then probabilities
+    extern __shared__ float S[];       // [16][sstride] scores, then probabilities
     constexpr int SS = HD / 16;        // reduction steps of 16 head dims
-    constexpr int CT = HD / 16 / 4;    // phase-3 column tiles per wave (HD=128: 2, HD=64: 1)
-    const int h = blockIdx.y, kvh = h / (H / Hkv);
-    const int q0 = blockIdx.x * RT * 16;
+    constexpr int CT = HD / 64;        // phase-3 column tiles per wave (HD=128: 2, HD=64: 1)
+    const int L = blockIdx.x, xcd = L & 7, j = L >> 3;
+    const int h = 8 * (j / q_tiles) + xcd, qt = j % q_tiles;
+    if (h >= H) return;
+    const int kvh = h / (H / Hkv);
+    const int q0 = qt * 16;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
     const int64_t kvstride = (int64_t)Hkv * HD;
@@ -85,59 +94,42 @@ __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q,
     const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
 
     // ---- phase 1
-    float4 qf[RT][SS];
+    float4 qf[SS];
+    {
+        const int row = q0 + li;
+        const float * qr = q + ((int64_t)min(row, M - 1) * H + h) * HD + 4 * lg;
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
-        const int row = q0 + 16 * rt + li;
-        const float * qr = q + ((int64_t)row * H + h) * HD + 4 * lg;
-#pragma unroll
-        for (int s = 0; s < SS; s++) qf[rt][s] = (row < M) ? *(const float4 *)(qr + 16 * s) : zero4;
+        for (int s = 0; s < SS; s++) qf[s] = (row < M) ? *(const float4 *)(qr + 16 * s) : zero4;
     }
-    for (int t0 = wv; t0 < ntiles; t0 += 8) {
-        const int t1 = t0 + 4;
-        const bool has1 = t1 < ntiles;
-        const int n0 = 16 * t0 + li, n1 = 16 * t1 + li;
-        const float * k0 = kc + (int64_t)n0 * kvstride + (int64_t)kvh * HD + 4 * lg;
-        const float * k1 = kc + (int64_t)n1 * kvstride + (int64_t)kvh * HD + 4 * lg;
-        float4 kf0[SS], kf1[SS];
+    const float * kbase = kc + (int64_t)kvh * HD + 4 * lg;
+    auto load_k = [&](float4 (&kf)[SS], int t) {
+        const int n = 16 * t + li;
+        const float * kr = kbase + (int64_t)min(n, n_keys - 1) * kvstride;
+#pragma unroll
+        for (int s = 0; s < SS; s++) kf[s] = (n < n_keys) ? *(const float4 *)(kr + 16 * s) : zero4;
+    };
+    float4 kcur[SS], knext[SS];
+    if (wv < ntiles) load_k(kcur, wv);
+    for (int t = wv; t < ntiles; t += 4) {
+        if (t + 4 < ntiles) load_k(knext, t + 4);
+        double4v a[4] = {0.0, 0.0, 0.0, 0.0};      // four independent chains: MFMA c of each step
 #pragma unroll
         for (int s = 0; s < SS; s++) {
-            kf0[s] = (n0 < n_keys) ? *(const float4 *)(k0 + 16 * s) : zero4;
-            kf1[s] = (has1 && n1 < n_keys) ? *(const float4 *)(k1 + 16 * s) : zero4;
+            const float kb[4] = {kcur[s].x, kcur[s].y, kcur[s].z, kcur[s].w};
+            const float qa[4] = {qf[s].x, qf[s].y, qf[s].z, qf[s].w};
+#pragma unroll
+            for (int c = 0; c < 4; c++) a[c] = mfma_f64((double)qa[c], (double)kb[c], a[c]);
         }
-        double4v a0[RT], a1[RT];
+        const double4v acc = (a[0] + a[1]) + (a[2] + a[3]);
 #pragma unroll
-        for (int rt = 0; rt < RT; rt++) { a0[rt] = 0.0; a1[rt] = 0.0; }
+        for (int i = 0; i < 4; i++) S[(lg + 4 * i) * sstride + 16 * t + li] = (float)acc[i] * scale;
 #pragma unroll
-        for (int s = 0; s < SS; s++) {
-            const float kb0[4] = {kf0[s].x, kf0[s].y, kf0[s].z, kf0[s].w};
-            const float kb1[4] = {kf1[s].x, kf1[s].y, kf1[s].z, kf1[s].w};
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const double b0 = (double)kb0[c], b1 = (double)kb1[c];
-#pragma unroll
-                for (int rt = 0; rt < RT; rt++) {
-                    const float qa[4] = {qf[rt][s].x, qf[rt][s].y, qf[rt][s].z, qf[rt][s].w};
-                    const double a = (double)qa[c];
-                    a0[rt] = mfma_f64(a, b0, a0[rt]);
-                    a1[rt] = mfma_f64(a, b1, a1[rt]);
-                }
-            }
-        }
-#pragma unroll
-        for (int rt = 0; rt < RT; rt++) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int r = 16 * rt + lg + 4 * i;
-                S[r * sstride + 16 * t0 + li] = (float)a0[rt][i] * scale;
-                if (has1) S[r * sstride + 16 * t1 + li] = (float)a1[rt][i] * scale;
-            }
-        }
+        for (int s = 0; s < SS; s++) kcur[s] = knext[s];
     }
     __syncthreads();
 
     // ---- phase 2
-    for (int r = wv; r < RT * 16; r += 4) {
+    for (int r = wv; r < 16; r += 4) {
         float * sr = S + r * sstride;
         float mx = -INFINITY;
         for (int n = lane; n < n_keys; n += 64) mx = fmaxf(mx, sr[n]);
@@ -156,52 +148,68 @@ __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q,
     __syncthreads();
 
     // ---- phase 3
-    double4v o[RT][CT];
+    double4v o[CT][2];                              // chains: column tile x MFMA parity
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++)
+    for (int ct = 0; ct < CT; ct++) o[ct][0] = o[ct][1] = 0.0;
+    // value column of this lane for column tile ct: 16*wv + 64*ct + li; keys 16s+4g..+3
+    const float * vb = vt + ((int64_t)kvh * HD + 16 * wv + li) * v_ld + 4 * lg;
+    auto load_v = [&](float4 (&vf)[CT], int s) {
+        const int n = 16 * s + 4 * lg;                 // first of this lane's 4 keys
 #pragma unroll
-        for (int ct = 0; ct < CT; ct++) o[rt][ct] = 0.0;
-    const float * vb = vc + (int64_t)kvh * HD + 16 * wv + li;     // column tile wv (+4 per ct)
-    for (int s = 0; s < ntiles; s++) {
-        float4 pf[RT];
-#pragma unroll
-        for (int rt = 0; rt < RT; rt++) pf[rt] = *(const float4 *)(S + (16 * rt + li) * sstride + 16 * s + 4 * lg);
-        float vf[CT][4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int n = 16 * s + 4 * lg + c;
-#pragma unroll
-            for (int ct = 0; ct < CT; ct++) vf[ct][c] = (n < n_keys) ? vb[(int64_t)n * kvstride + 64 * ct] : 0.0f;
+        for (int ct = 0; ct < CT; ct++) {
+            const float * p = vb + (int64_t)64 * ct * v_ld + 16 * min(s, ntiles - 1);
+            // v_ld and n are multiples of 4 and n_keys <= v_ld: the load stays in the row
+            vf[ct] = (n < n_keys) ? *(const float4 *)p : zero4;
+            if (n + 4 > n_keys) {        // keys past the end of the sequence count as 0
+                if (n + 1 >= n_keys) vf[ct].y = 0.0f;
+                if (n + 2 >= n_keys) vf[ct].z = 0.0f;
+                if (n + 3 >= n_keys) vf[ct].w = 0.0f;
+            }
         }
+    };
+    constexpr int PV = 2;                           // value steps in flight
+    float4 vq[PV][CT];
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
+    for (int u = 0; u < PV; u++) load_v(vq[u], u);
+    for (int s0 = 0; s0 < ntiles; s0 += PV) {
 #pragma unroll
-            for (int rt = 0; rt < RT; rt++) {
-                const float pa[4] = {pf[rt].x, pf[rt].y, pf[rt].z, pf[rt].w};
-                const double a = (double)pa[c];
+        for (int u = 0; u < PV; u++) {
+            const int s = s0 + u;
+            if (s < ntiles) {
+                float4 vcur[CT];
 #pragma unroll
-                for (int ct = 0; ct < CT; ct++) o[rt][ct] = mfma_f64(a, (double)vf[ct][c], o[rt][ct]);
+                for (int ct = 0; ct < CT; ct++) vcur[ct] = vq[u][ct];
+                load_v(vq[u], s + PV);
+                const float4 pf = *(const float4 *)(S + li * sstride + 16 * s + 4 * lg);
+                const float pa[4] = {pf.x, pf.y, pf.z, pf.w};
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const double a = (double)pa[c];
+#pragma unroll
+                    for (int ct = 0; ct < CT; ct++) {
+                        const float vv[4] = {vcur[ct].x, vcur[ct].y, vcur[ct].z, vcur[ct].w};
+                        o[ct][c & 1] = mfma_f64(a, (double)vv[c], o[ct][c & 1]);
+                    }
+                }
             }
         }
     }
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++)
+    for (int i = 0; i < 4; i++) {
+        const int row = q0 + lg + 4 * i;
+        if (row >= M) continue;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int row = q0 + 16 * rt + lg + 4 * i;
-            if (row >= M) continue;
-#pragma unroll
-            for (int ct = 0; ct < CT; ct++)
-                out[(int64_t)row * H * HD + (int64_t)h * HD + 16 * wv + 64 * ct + li] = (float)o[rt][ct][i];
-        }
+        for (int ct = 0; ct < CT; ct++)
+            out[(int64_t)row * H * HD + (int64_t)h * HD + 16 * wv + 64 * ct + li] = (float)(o[ct][0][i] + o[ct][1][i]);
+    }
 }
 
 // VALU form for key counts whose score rows do not fit the matrix-core kernel's LDS:
 // TQ query rows of one head per workgroup (256 threads), full score rows in LDS.
 template <int HD, int TQ>
 __global__ void __launch_bounds__(256) k_attention(const float * __restrict__ q, const float * __restrict__ kc,
-                                                   const float * __restrict__ vc, int M, int n_keys, int H,
-                                                   int Hkv, float * __restrict__ out) {
+                                                   const float * __restrict__ vt, int64_t v_ld, int M, int n_keys,
+                                                   int H, int Hkv, float * __restrict__ out) {
 #pragma clang fp contract(off)
     extern __shared__ float smem[];
     float * Qs = smem;                 // [TQ][HD]
@@ -268,8 +276,9 @@ __global__ void __launch_bounds__(256) k_attention(const float * __restrict__ q,
     double acc[RP];
 #pragma unroll
     for (int r = 0; r < RP; r++) acc[r] = 0.0;
+    const float * vcol = vt + ((int64_t)kvh * HD + j) * v_ld;
     for (int n = 0; n < n_keys; n++) {
-        const double v = (double)vc[((int64_t)n * Hkv + kvh) * HD + j];
+        const double v = (double)vcol[n];
 #pragma unroll
         for (int r = 0; r < RP; r++) acc[r] += v * (double)S[(r0 + r) * n_keys + n];
     }
@@ -279,16 +288,17 @@ __global__ void __launch_bounds__(256) k_attention(const float * __restrict__ q,
 }
 
 extern "C" int dfx_rope_store(const float * qkv, const int32_t * pos, int64_t M, int H, int Hkv, int hd,
-                              const float * tab, float * q_out, float * kc, float * vc, void * stream) {
-    if (M < 0 || H <= 0 || Hkv <= 0 || H % Hkv || hd <= 0 || (hd & 1)) {
-        dfx_set_error("dfx_rope_store: bad shape M=%lld H=%d Hkv=%d hd=%d", (long long)M, H, Hkv, hd);
+                              const float * tab, float * q_out, float * kc, float * vt, int64_t v_ld, void * stream) {
+    if (M < 0 || H <= 0 || Hkv <= 0 || H % Hkv || hd <= 0 || (hd & 1) || v_ld <= 0) {
+        dfx_set_error("dfx_rope_store: bad shape M=%lld H=%d Hkv=%d hd=%d v_ld=%lld", (long long)M, H, Hkv, hd,
+                      (long long)v_ld);
         return DFX_ERR_ARG;
     }
     if (M == 0) return DFX_OK;
     const int64_t total = M * (H + 2 * Hkv) * (hd / 2);
     const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
     hipLaunchKernelGGL(k_rope_store, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, qkv, pos, M, H, Hkv,
-                       hd, tab, q_out, kc, vc);
+                       hd, tab, q_out, kc, vt, v_ld);
     DFX_CHECK_LAUNCH("dfx_rope_store");
     return DFX_OK;
 }
@@ -313,44 +323,43 @@ static size_t attn_lds_limit() {
 // rows of a 16-row fragment start in different LDS banks.
 static inline int attn_sstride(int64_t n_keys) { return (int)(((n_keys + 15) / 16) * 16 + 4); }
 
-extern "C" int dfx_attention(const float * q, const float * kc, const float * vc, int64_t M, int64_t n_keys,
-                             int H, int Hkv, int hd, float * out, void * stream) {
-    if (M < 0 || n_keys <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || (hd != 64 && hd != 128)) {
-        dfx_set_error("dfx_attention: unsupported shape M=%lld keys=%lld H=%d Hkv=%d hd=%d", (long long)M,
-                      (long long)n_keys, H, Hkv, hd);
+extern "C" int dfx_attention(const float * q, const float * kc, const float * vt, int64_t v_ld, int64_t M,
+                             int64_t n_keys, int H, int Hkv, int hd, float * out, void * stream) {
+    if (M < 0 || n_keys <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || (hd != 64 && hd != 128) || v_ld < n_keys ||
+        (v_ld % 4)) {
+        dfx_set_error("dfx_attention: unsupported shape M=%lld keys=%lld H=%d Hkv=%d hd=%d v_ld=%lld "
+                      "(v_ld must be a multiple of 4, >= keys)", (long long)M, (long long)n_keys, H, Hkv, hd,
+                      (long long)v_ld);
         return DFX_ERR_UNSUPPORTED;
     }
     if (M == 0) return DFX_OK;
     hipStream_t st = (hipStream_t)stream;
     const int sstride = attn_sstride(n_keys);
-    // One 16-row query tile per workgroup: the two-tile form needs every VGPR of the
-    // SIMD (one wave per SIMD), the one-tile form runs two.
-    const size_t lds_max = attn_lds_limit();
-    const int RT = 1;
-    if ((size_t)RT * 16 * sstride * sizeof(float) <= lds_max) {
-        const size_t lds = (size_t)RT * 16 * sstride * sizeof(float);
-        dim3 grid((unsigned)((M + 16 * RT - 1) / (16 * RT)), (unsigned)H);
-#define ATTN_MFMA_CASE(HD_, RT_)                                                                         \
-    if (hd == HD_ && RT == RT_)                                                                          \
-        hipLaunchKernelGGL((k_attn_mfma<HD_, RT_>), grid, dim3(256), lds, st, q, kc, vc, (int)M, (int)n_keys, H, \
-                           Hkv, sstride, out);
-        ATTN_MFMA_CASE(128, 1) ATTN_MFMA_CASE(64, 1)
-#undef ATTN_MFMA_CASE
+    const size_t lds = (size_t)16 * sstride * sizeof(float);
+    if (lds <= attn_lds_limit()) {
+        const int q_tiles = (int)((M + 15) / 16);
+        const dim3 grid((unsigned)(8 * ((H + 7) / 8) * q_tiles));
+        if (hd == 128)
+            hipLaunchKernelGGL((k_attn_mfma<128>), grid, dim3(256), lds, st, q, kc, vt, v_ld, (int)M, (int)n_keys, H,
+                               Hkv, sstride, q_tiles, out);
+        else
+            hipLaunchKernelGGL((k_attn_mfma<64>), grid, dim3(256), lds, st, q, kc, vt, v_ld, (int)M, (int)n_keys, H,
+                               Hkv, sstride, q_tiles, out);
         DFX_CHECK_LAUNCH("dfx_attention");
         return DFX_OK;
     }
     int TQ = 32;
     while (TQ > 1 && (size_t)TQ * (hd + n_keys) * sizeof(float) > ATTN_LDS_MAX) TQ >>= 1;
-    const size_t lds = (size_t)TQ * (hd + n_keys) * sizeof(float);
-    if (lds > ATTN_LDS_MAX) {
+    const size_t lds2 = (size_t)TQ * (hd + n_keys) * sizeof(float);
+    if (lds2 > ATTN_LDS_MAX) {
         dfx_set_error("dfx_attention: %lld keys exceed the LDS score row", (long long)n_keys);
         return DFX_ERR_UNSUPPORTED;
     }
     dim3 grid((unsigned)((M + TQ - 1) / TQ), (unsigned)H);
-#define ATTN_CASE(HD_, TQ_)                                                                              \
-    if (hd == HD_ && TQ == TQ_)                                                                          \
-        hipLaunchKernelGGL((k_attention<HD_, TQ_>), grid, dim3(256), lds, st, q, kc, vc, (int)M, (int)n_keys, \
-                           H, Hkv, out);
+#define ATTN_CASE(HD_, TQ_)                                                                                \
+    if (hd == HD_ && TQ == TQ_)                                                                            \
+        hipLaunchKernelGGL((k_attention<HD_, TQ_>), grid, dim3(256), lds2, st, q, kc, vt, v_ld, (int)M,   \
+                           (int)n_keys, H, Hkv, out);
     ATTN_CASE(128, 32) ATTN_CASE(128, 16) ATTN_CASE(128, 8) ATTN_CASE(128, 4) ATTN_CASE(128, 2) ATTN_CASE(128, 1)
     ATTN_CASE(64, 32) ATTN_CASE(64, 16) ATTN_CASE(64, 8) ATTN_CASE(64, 4) ATTN_CASE(64, 2) ATTN_CASE(64, 1)
 #undef ATTN_CASE

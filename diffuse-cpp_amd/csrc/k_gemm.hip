@@ -487,23 +487,23 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
     const uint32_t off_d = (uint32_t)min(m0 + tid % BM, M - 1) * (uint32_t)n_sb_all * 4u;
     const uint32_t off_b = ((uint32_t)min(m0 + (tid >> 1) % BM, M - 1) * (uint32_t)(K / 16) + (tid & 1) * 8u) * 2u;
 
-    // Register ring: stage s holds everything K step kt (kt % D == s) reads from memory.
-    u32x4 a_st[D][A_PER_T];          // A tile chunks of this thread
+    // Register rings: weight stage s holds the nibbles (and header) of K step kt with
+    // kt % D == s, D-1 steps ahead (weights stream from HBM); the activation rows and
+    // their block scales / sums (small, L2-resident) are loaded one step ahead into a
+    // 2-deep ring (stage kt % 2).
+    u32x4 a_st[2][A_PER_T];          // A tile chunks of this thread
+    float d_st[2];                   // d_a of row tid % BM (even K steps)
+    u32x4 b_st[2];                   // 8 block sums of row (tid/2) % BM (even K steps)
     u32x4 q_st[D][TN][2];            // this lane's 32 bytes of nibbles, per column tile
     u32x4 h_st[D][TN];               // super-block header (even K steps)
-    float d_st[D];                   // d_a of row tid % BM (even K steps)
-    u32x4 b_st[D];                   // 8 block sums of row (tid/2) % BM (even K steps)
 
     // Stage indices are compile-time constants (generic lambdas over integral_constant),
-    // so the ring stays in registers.  n_kt is a multiple of D (even): stage s only ever
+    // so the rings stay in registers.  n_kt is a multiple of D (even): stage s only ever
     // holds K steps kt with kt % D == s, hence of parity s & 1.
-    auto issue = [&](auto stage, int kt_req) __attribute__((always_inline)) {
+    auto issue_w = [&](auto stage, int kt_req) __attribute__((always_inline)) {
         constexpr int s = decltype(stage)::value, h = s & 1;
         const int kt = 2 * sb_first + min(kt_req, n_kt - 1);      // global K step
         const int sb = kt >> 1;
-        const uint8_t * abase = Aq + (size_t)kt * 256;
-#pragma unroll
-        for (int i = 0; i < A_PER_T; i++) a_st[s][i] = *(const u32x4 *)(abase + off_a[i]);
         const uint8_t * wbase = W + (size_t)sb * SB_Q4_K;
 #pragma unroll
         for (int t = 0; t < TN; t++) {
@@ -511,6 +511,14 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
             q_st[s][t][0] = *(const u32x4 *)(wbase + off_w[t] + 16 + 32 * (2 * h + hl));
             q_st[s][t][1] = *(const u32x4 *)(wbase + off_w[t] + 32 + 32 * (2 * h + hl));
         }
+    };
+    auto issue_a = [&](auto stage, int kt_req) __attribute__((always_inline)) {
+        constexpr int s = decltype(stage)::value, h = s & 1;
+        const int kt = 2 * sb_first + min(kt_req, n_kt - 1);
+        const int sb = kt >> 1;
+        const uint8_t * abase = Aq + (size_t)kt * 256;
+#pragma unroll
+        for (int i = 0; i < A_PER_T; i++) a_st[s][i] = *(const u32x4 *)(abase + off_a[i]);
         if (h == 0) {
             d_st[s] = *(const float *)(Adg + (size_t)sb * 4 + off_d);
             b_st[s] = *(const u32x4 *)(Absg + (size_t)sb * 32 + off_b);
@@ -530,15 +538,15 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
     auto step = [&](auto stage, int kt) __attribute__((always_inline)) {
         constexpr int s = decltype(stage)::value, h = s & 1, buf = s & 1;
         const int mbuf = (kt >> 1) & 1;
-        // stage s -> LDS
+        // activation stage -> LDS
 #pragma unroll
         for (int i = 0; i < A_PER_T; i++) {
             const int c = tid + 256 * i, r = c >> 4, cc = c & 15;
-            *(u32x4 *)(&As[buf][r * AST + cc * 8]) = a_st[s][i];
+            *(u32x4 *)(&As[buf][r * AST + cc * 8]) = a_st[buf][i];
         }
         if (h == 0) {
-            if (tid < BM) Ad[mbuf][tid] = d_st[s];
-            if (tid < 2 * BM) *(u32x4 *)(&Abs[mbuf][(tid >> 1) * BST + (tid & 1) * 8]) = b_st[s];
+            if (tid < BM) Ad[mbuf][tid] = d_st[buf];
+            if (tid < 2 * BM) *(u32x4 *)(&Abs[mbuf][(tid >> 1) * BST + (tid & 1) * 8]) = b_st[buf];
 #pragma unroll
             for (int t = 0; t < TN; t++) {
                 hdr[t] = h_st[s][t];
@@ -546,8 +554,9 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
             }
         }
         __syncthreads();
-        // keep D-1 K steps in flight
-        issue(std::integral_constant<int, (s + D - 1) % D>{}, kt + D - 1);
+        // weights D-1 K steps ahead, activations one
+        issue_w(std::integral_constant<int, (s + D - 1) % D>{}, kt + D - 1);
+        issue_a(std::integral_constant<int, (s + 1) & 1>{}, kt + 1);
 
         // group g = 2h + hl: scales of sub-blocks 4h + 2hl and 4h + 2hl + 1
         q4k_consts kc[TN];
@@ -597,32 +606,35 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
                     }
                 }
             }
-            // chunk complete: T = T + S
-            const int sb_local = kt >> 1;
-            if ((sb_first + sb_local + 1) % SB_CHUNK == 0 || sb_local + 1 == n_sb) {
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int t = 0; t < TN; t++) {
-                        T[i][t] = T[i][t] + S[i][t];
-                        S[i][t] = zero16;
-                    }
-            }
         }
     };
 
-    issue(std::integral_constant<int, 0>{}, 0);
+    issue_w(std::integral_constant<int, 0>{}, 0);
     if constexpr (D == 4) {
-        issue(std::integral_constant<int, 1>{}, 1);
-        issue(std::integral_constant<int, 2>{}, 2);
+        issue_w(std::integral_constant<int, 1>{}, 1);
+        issue_w(std::integral_constant<int, 2>{}, 2);
     }
-    for (int kt0 = 0; kt0 < n_kt; kt0 += D) {
-        step(std::integral_constant<int, 0>{}, kt0);
-        step(std::integral_constant<int, 1>{}, kt0 + 1);
-        if constexpr (D == 4) {
-            step(std::integral_constant<int, 2>{}, kt0 + 2);
-            step(std::integral_constant<int, 3>{}, kt0 + 3);
+    issue_a(std::integral_constant<int, 0>{}, 0);
+    // chunks of SB_CHUNK super-blocks (the first at sb_first, a multiple of SB_CHUNK);
+    // every chunk's K steps are a multiple of D
+    for (int c0 = 0; c0 < n_kt; c0 += 2 * SB_CHUNK) {
+        const int c1 = min(c0 + 2 * SB_CHUNK, n_kt);
+        for (int kt0 = c0; kt0 < c1; kt0 += D) {
+            step(std::integral_constant<int, 0>{}, kt0);
+            step(std::integral_constant<int, 1>{}, kt0 + 1);
+            if constexpr (D == 4) {
+                step(std::integral_constant<int, 2>{}, kt0 + 2);
+                step(std::integral_constant<int, 3>{}, kt0 + 3);
+            }
         }
+        // chunk complete: T = T + S
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int t = 0; t < TN; t++) {
+                T[i][t] = T[i][t] + S[i][t];
+                S[i][t] = zero16;
+            }
     }
 
     // split K: the chunk sum goes to ws[z][m][n]; the reduction adds the chunks in order
@@ -769,7 +781,7 @@ static int launch_q4k(const void * w, int N, int K, const void * act, int M, con
     // every workgroup's K steps (whole super-blocks, two per super-block) must be a
     // multiple of the ring depth
     const int sb = K / 256, sb_last = sb - (chunks - 1) * (DFX_DOT_CHUNK / 256);
-    if ((2 * (ws ? sb_last : sb)) % D || (ws && chunks > 1 && (2 * (DFX_DOT_CHUNK / 256)) % D)) {
+    if ((2 * sb_last) % D || (chunks > 1 && (2 * (DFX_DOT_CHUNK / 256)) % D)) {
         dfx_set_error("dfx_gemm q4_k: K=%d does not fit the pipeline depth %d", K, D);
         return DFX_ERR_ARG;
     }
@@ -819,7 +831,7 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
     }
     // a 4-deep ring needs a multiple of 4 K steps in every workgroup
     const int sb = K / 256, sb_last = sb - (chunks - 1) * (DFX_DOT_CHUNK / 256);
-    if (cands[pick].d == 4 && ((split ? sb_last : sb) % 2))
+    if (cands[pick].d == 4 && (sb_last % 2))
         for (int c = 0; c < n_cand; c++)
             if (cands[c].tm == cands[pick].tm && cands[c].tn == cands[pick].tn && cands[c].d == 2) { pick = c; break; }
     float * wsf = split ? (float *)ws : nullptr;

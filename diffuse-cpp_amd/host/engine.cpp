@@ -80,6 +80,7 @@ void rope_table(int n_pos, int hd, float base, std::vector<float> & tab) {
 
 int ensure_capacity(diffuse_context * c, int N) {
     if (N <= c->cap) return DFX_OK;
+    N = (N + 15) & ~15;     // the transposed value cache rows are read 4 keys at a time
     free_buffers(c);
     const dims D(c->model->hparams);
     const int64_t n = N;
@@ -200,8 +201,8 @@ int forward_pass(diffuse_context * c, int M, int n_keys, int n_head) {
         float * vc = c->vc + il * (int64_t)c->cap * D.dkv;
         TRY(run_group(c, L.qkv, L.attn_norm, M, D.d, c->qkv));
         TRY(dfx_rope_store(c->qkv, c->d_pos, M, (int)D.H, (int)D.Hkv, (int)D.hd, c->rope_tab, c->qr, kc, vc,
-                           c->stream));
-        TRY(dfx_attention(c->qr, kc, vc, M, n_keys, (int)D.H, (int)D.Hkv, (int)D.hd, c->att, c->stream));
+                           c->cap, c->stream));
+        TRY(dfx_attention(c->qr, kc, vc, c->cap, M, n_keys, (int)D.H, (int)D.Hkv, (int)D.hd, c->att, c->stream));
         TRY(dfx_act_convert(L.o.type, c->att, M, D.d, c->act, c->stream));
         TRY(gemm(c, L.o, D.d, D.d, M, nullptr, c->x, c->x, D.d, nullptr, true));
         TRY(run_group(c, L.gu, L.ffn_norm, M, D.d, c->gu));

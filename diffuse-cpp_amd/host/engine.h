@@ -74,8 +74,8 @@ struct diffuse_context {
     float *      att = nullptr;      // [cap][d]
     float *      gu = nullptr;       // [cap][2F]
     float *      logits = nullptr;   // [cap][V]       per position
-    float *      kc = nullptr;       // [L][cap][dkv]  inter-step cache
-    float *      vc = nullptr;
+    float *      kc = nullptr;       // [L][cap][dkv]        inter-step key cache
+    float *      vc = nullptr;       // [L][Hkv][hd][cap]    inter-step value cache, transposed
     float *      rope_tab = nullptr; // [cap][hd/2][2]
     int32_t *    d_tok = nullptr;    // [cap] tokens of this pass
     int32_t *    d_pos = nullptr;    // [cap] positions of this pass

@@ -117,18 +117,20 @@ size_t dfx_gemm_ws_bytes(int64_t M, int64_t N, int64_t K);
 int dfx_gemm(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
              const float * bias, const float * residual, float * y, void * ws, void * stream);
 
-/* NEOX RoPE + cache store (src/diffuse-graph.cpp:71-79, 466-469; cache layout
+/* NEOX RoPE + cache store (src/diffuse-graph.cpp:71-79, 466-469; cache contents of
  * src/diffuse-cache.h:23-26 but at n_head_kv width — the GQA repeat of 84-95 is
  * index math in the attention kernel).  qkv: [M][(H + 2*Hkv)*hd] f32 (Q | K | V);
- * pos[M] absolute positions; tab: [n_pos][hd/2][cos, sin] f32.
- * Writes q_out [M][H][hd] and kc/vc[pos][Hkv][hd]. */
+ * pos[M] absolute positions (< v_ld); tab: [n_pos][hd/2][cos, sin] f32.
+ * Writes q_out [M][H][hd], kc[pos][Hkv][hd] and the transposed value cache
+ * vt[Hkv][hd][v_ld] (v_ld = cache capacity in positions). */
 int dfx_rope_store(const float * qkv, const int32_t * pos, int64_t M, int H, int Hkv, int hd,
-                   const float * tab, float * q_out, float * kc, float * vc, void * stream);
+                   const float * tab, float * q_out, float * kc, float * vt, int64_t v_ld, void * stream);
 
 /* Bidirectional attention, no mask (src/diffuse-graph.cpp:97-119 / 528-553):
  * out[m][h*hd + j] = sum_n softmax_n(q_m . k_n / sqrt(hd)) * v_n[j], keys 0..n_keys-1
- * of the cache, query head h reads KV head h / (H/Hkv). */
-int dfx_attention(const float * q, const float * kc, const float * vc, int64_t M, int64_t n_keys,
+ * of the cache (kc[n][Hkv][hd], vt[Hkv][hd][v_ld], n_keys <= v_ld), query head h
+ * reads KV head h / (H/Hkv). */
+int dfx_attention(const float * q, const float * kc, const float * vt, int64_t v_ld, int64_t M, int64_t n_keys,
                   int H, int Hkv, int hd, float * out, void * stream);
 
 /* Per-row sampler statistics over logits rows (src/diffuse-sampler.cpp:34-57, 241-252):

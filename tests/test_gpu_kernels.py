@@ -214,14 +214,15 @@ def test_rope_store_matches_oracle(gpu):
     qo, kc, vc = dfx.Buf(M * H * hd * 4), dfx.Buf(n_ctx * Hkv * hd * 4), dfx.Buf(n_ctx * Hkv * hd * 4)
     kc.zero()
     vc.zero()
-    dfx.check(L().dfx_rope_store(qb.ptr, pb.ptr, M, H, Hkv, hd, tb.ptr, qo.ptr, kc.ptr, vc.ptr, None), "rope")
+    dfx.check(L().dfx_rope_store(qb.ptr, pb.ptr, M, H, Hkv, hd, tb.ptr, qo.ptr, kc.ptr, vc.ptr, n_ctx, None),
+              "rope")
     q_ref = qkv[:, :H * hd].reshape(M, H, hd).copy()
     k_ref = qkv[:, H * hd:(H + Hkv) * hd].reshape(M, Hkv, hd).copy()
     O.oracle().orc_rope_neox(O.ptr(q_ref), M, H, hd, O.ptr(pos), O.ptr(tab))
     O.oracle().orc_rope_neox(O.ptr(k_ref), M, Hkv, hd, O.ptr(pos), O.ptr(tab))
     assert np.array_equal(qo.download(np.float32, shape=(M, H, hd)), q_ref)
     kg = kc.download(np.float32, shape=(n_ctx, Hkv, hd))
-    vg = vc.download(np.float32, shape=(n_ctx, Hkv, hd))
+    vg = vc.download(np.float32, shape=(Hkv, hd, n_ctx)).transpose(2, 0, 1)     # stored [Hkv][hd][n_ctx]
     assert np.array_equal(kg[pos], k_ref)
     assert np.array_equal(vg[pos], qkv[:, (H + Hkv) * hd:].reshape(M, Hkv, hd))
     untouched = np.setdiff1d(np.arange(n_ctx), pos)
@@ -234,12 +235,17 @@ def test_rope_store_matches_oracle(gpu):
 def test_attention_matches_oracle_and_f64(gpu, M, n_keys, H, Hkv, hd):
     """Bit-exact with the oracle (f64 accumulation of exact products, correctly rounded
     exp), and within 1e-6 of an independent f64 evaluation.  Covers the matrix-core
-    kernel (score rows in LDS) and the VALU kernel (3000 keys)."""
+    kernel (score rows in LDS) and the VALU kernel (3000 keys); the transposed value
+    cache has a padded row (v_ld > n_keys) holding NaN past the sequence, which must
+    not leak into the result."""
     q = rng.standard_normal((M, H, hd)).astype(np.float32)
     k = rng.standard_normal((n_keys, Hkv, hd)).astype(np.float32)
     v = rng.standard_normal((n_keys, Hkv, hd)).astype(np.float32)
-    qb, kb, vb, ob = dfx.Buf.of(q), dfx.Buf.of(k), dfx.Buf.of(v), dfx.Buf(M * H * hd * 4)
-    dfx.check(L().dfx_attention(qb.ptr, kb.ptr, vb.ptr, M, n_keys, H, Hkv, hd, ob.ptr, None), "attention")
+    v_ld = (n_keys + 15) // 16 * 16 + 16
+    vt = np.full((Hkv, hd, v_ld), np.nan, np.float32)
+    vt[:, :, :n_keys] = v.transpose(1, 2, 0)
+    qb, kb, vb, ob = dfx.Buf.of(q), dfx.Buf.of(k), dfx.Buf.of(vt), dfx.Buf(M * H * hd * 4)
+    dfx.check(L().dfx_attention(qb.ptr, kb.ptr, vb.ptr, v_ld, M, n_keys, H, Hkv, hd, ob.ptr, None), "attention")
     got = ob.download(np.float32, shape=(M, H, hd))
     rep = H // Hkv
     kd = np.repeat(k.astype(np.float64), rep, axis=1)        # query head h reads KV head h // rep
