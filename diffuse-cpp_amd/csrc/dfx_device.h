@@ -64,7 +64,11 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 // Q4_K nibbles: inside every 64-element group, slot 8i+s holds element
 //   s < 4:  4i + P[s]        s >= 4:  32 + 4i + P[s-4]        P = {0, 2, 1, 3}
 // (one 32-bit word of packed nibbles gives the 8 operands of slots 8i..8i+7).
-enum { CONV_Q8_K = 0, CONV_Q8_0 = 1, CONV_F16 = 2, CONV_Q8_K_P4 = 3 };
+// For Q6_K weights (CONV_Q8_K_P6), inside every 128-element half super-block, slot
+// 64*g + 8*(i + 4*p) + s holds element 32*q + 16*g + 4*i + P[s % 4] with quarter
+// q = p + 2*(s >= 4) (g, p in 0..1, i in 0..3): one word of low bits (4 bytes l..l+3)
+// carries quarters p and p+2.
+enum { CONV_Q8_K = 0, CONV_Q8_0 = 1, CONV_F16 = 2, CONV_Q8_K_P4 = 3, CONV_Q8_K_P6 = 4 };
 
 // Quantised GEMMs sum the scaled block dot products of each chunk of DFX_DOT_CHUNK
 // K elements from zero, in K order, and add the chunk sums in order (T = T + S).
@@ -74,10 +78,12 @@ __host__ __device__ inline int dot_chunks(int64_t K) { return (int)((K + DFX_DOT
 
 __host__ __device__ inline int conv_mode(int wtype) {
     return wtype == DFX_TYPE_Q4_K ? CONV_Q8_K_P4
-         : wtype == DFX_TYPE_Q6_K ? CONV_Q8_K
+         : wtype == DFX_TYPE_Q6_K ? CONV_Q8_K_P6
          : (wtype == DFX_TYPE_Q8_0) ? CONV_Q8_0 : CONV_F16;
 }
-__host__ __device__ inline bool conv_is_q8k(int mode) { return mode == CONV_Q8_K || mode == CONV_Q8_K_P4; }
+__host__ __device__ inline bool conv_is_q8k(int mode) {
+    return mode == CONV_Q8_K || mode == CONV_Q8_K_P4 || mode == CONV_Q8_K_P6;
+}
 
 struct act_layout {
     size_t q, d, bs, bytes;

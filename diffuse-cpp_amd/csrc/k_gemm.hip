@@ -655,6 +655,250 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
 }
 
 // ---------------------------------------------------------------------------
+// Q6_K: the same pipeline as Q4_K (register rings, A tile in LDS, chunked K)
+// ---------------------------------------------------------------------------
+// A K step is half a super-block (128 elements).  Lane (row n, half g = lane/32) holds
+// l = 16g..16g+15 of every quarter: 16 bytes of ql for quarters 0/2, 16 for quarters
+// 1/3 and 16 of qh.  MFMA kk = i + 4p takes word i of the ql bytes of quarters p / p+2
+// (low / high nibbles) and word i of qh.  q6 - 32 = lo4 + 16*(hi2 - 2) is split into two
+// exact f16 operands that go to two MFMAs into the same accumulator:
+//   sc*lo4:          (lo4 at bits 3..6) | 0x5800 = 128 + lo4,  x*sc - 128*sc
+//   16*sc*(hi2-2):   (hi2 at bits 8..9) | 0x4400 = 4 + hi2,    x*(16*sc) - 96*sc
+// (|sc| <= 128: every constant and result is an exact f16).  The activation buffer
+// stores q in the matching slot order (CONV_Q8_K_P6).  The flush of a super-block is
+// x = d_w*isum; S = fma(d_a, x, S).
+
+struct q6k_qc { uint32_t s, c, s16, c96; };
+__device__ __forceinline__ q6k_qc q6k_quarter_consts(int sc) {
+    const float f = (float)sc;
+    q6k_qc k;
+    k.s = h2pair(f);
+    k.c = h2pair(-128.0f * f);
+    k.s16 = h2pair(16.0f * f);
+    k.c96 = h2pair(-96.0f * f);
+    return k;
+}
+
+// Signed scale byte k (0..15) of the 16 scale bytes held in sc4.
+__device__ __forceinline__ int q6k_scale(const u32x4 & sc4, int k) {
+    const uint32_t w = sc4[k >> 2];
+    return (int)(int8_t)((w >> (8 * (k & 3))) & 0xFFu);
+}
+
+// Operands of MFMA kk = i + 4p: lo = sc*lo4 part, hi = 16*sc*(hi2-2) part, order
+// [qa: b0 b2 b1 b3 | qb: b0 b2 b1 b3], qa = p, qb = p + 2.
+__device__ __forceinline__ void q6k_word(int P, uint32_t w, uint32_t hw, const q6k_qc & ka, const q6k_qc & kb,
+                                         half8 & lo, half8 & hi, uint32_t m78, uint32_t mg58, uint32_t m300,
+                                         uint32_t mg44) {
+    u32x4 a, b;
+    a.x = pk_fma_h2(and_or(w << 3, m78, mg58), ka.s, ka.c);
+    a.y = pk_fma_h2(and_or(w >> 5, m78, mg58), ka.s, ka.c);
+    a.z = pk_fma_h2(and_or(w >> 1, m78, mg58), kb.s, kb.c);
+    a.w = pk_fma_h2(and_or(w >> 9, m78, mg58), kb.s, kb.c);
+    const int qa = P, qb = P + 2;    // 2-bit fields at bits 2q (+8 per byte): moved to bits 8..9 of each half
+    b.x = pk_fma_h2(and_or(hw << (8 - 2 * qa), m300, mg44), ka.s16, ka.c96);
+    b.y = pk_fma_h2(and_or(hw >> (2 * qa), m300, mg44), ka.s16, ka.c96);
+    b.z = pk_fma_h2(and_or(hw << (8 - 2 * qb), m300, mg44), kb.s16, kb.c96);
+    b.w = pk_fma_h2(and_or(hw >> (2 * qb), m300, mg44), kb.s16, kb.c96);
+    lo = __builtin_bit_cast(half8, a);
+    hi = __builtin_bit_cast(half8, b);
+}
+
+template <int TM, int TN, int D>
+__global__ void __launch_bounds__(256, TM * TN >= 4 ? 1 : 2)
+k_q6k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__ act, int M,
+      const float * __restrict__ bias, const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
+      int n_tiles, int m_tiles, float * __restrict__ ws) {
+#pragma clang fp contract(off)
+    constexpr int BM = TM * 32, BN = 4 * TN * 32;
+    constexpr int AST = 128 + 8;
+    constexpr int A_PER_T = BM * 16 / 256;
+    __shared__ __attribute__((aligned(16))) half_t As[2][BM * AST];
+    __shared__ __attribute__((aligned(16))) float Ad[2][BM];
+
+    const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
+    const int z = blockIdx.x / per_pass, L = blockIdx.x - z * per_pass, xcd = L & 7, j = L >> 3;
+    const int ty = j % m_tiles, tx = 8 * (j / m_tiles) + xcd;
+    if (tx >= n_tiles) return;
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, hl = lane >> 5, l32 = lane & 31;
+    const int n0 = tx * BN, m0 = ty * BM;
+    constexpr int SB_CHUNK = DFX_DOT_CHUNK / 256;
+    const int n_sb_all = K >> 8;
+    const int sb_first = ws ? z * SB_CHUNK : 0;
+    const int n_sb = ws ? min(SB_CHUNK, n_sb_all - sb_first) : n_sb_all;
+    const int n_kt = 2 * n_sb;
+    const uint32_t row_bytes = (uint32_t)n_sb_all * SB_Q6_K;
+    const act_layout Lay = act_layout_of(CONV_Q8_K_P6, M, K);
+    const uint8_t * Aq = act + Lay.q;
+    const uint8_t * Adg = act + Lay.d;
+
+    uint32_t off_a[A_PER_T], off_w[TN];
+#pragma unroll
+    for (int i = 0; i < A_PER_T; i++) {
+        const int c = tid + 256 * i, r = c >> 4, cc = c & 15;
+        off_a[i] = ((uint32_t)min(m0 + r, M - 1) * (uint32_t)K + (uint32_t)cc * 8u) * 2u;
+    }
+#pragma unroll
+    for (int t = 0; t < TN; t++) off_w[t] = (uint32_t)min(n0 + (wv * TN + t) * 32 + l32, N - 1) * row_bytes;
+    const uint32_t off_d = (uint32_t)min(m0 + tid % BM, M - 1) * (uint32_t)n_sb_all * 4u;
+
+    u32x4 a_st[2][A_PER_T];
+    float d_st[2];
+    u32x4 l_st[D][TN][2];            // ql bytes: quarters 0/2 and 1/3 at l = 16g..16g+15
+    u32x4 qh_st[D][TN];              // qh bytes at l = 16g..16g+15
+    u32x4 sc_st[D][TN];              // 16 scale bytes (even K steps)
+    uint32_t dw_st[D][TN];           // d (low 16 bits) (even K steps)
+
+    auto issue_w = [&](auto stage, int kt_req) __attribute__((always_inline)) {
+        constexpr int s = decltype(stage)::value, h = s & 1;
+        const int kt = 2 * sb_first + min(kt_req, n_kt - 1);
+        const int sb = kt >> 1;
+        const uint8_t * wbase = W + (size_t)sb * SB_Q6_K;
+#pragma unroll
+        for (int t = 0; t < TN; t++) {
+            const uint8_t * p = wbase + off_w[t];
+            l_st[s][t][0] = *(const u32x4 *)(p + 64 * h + 16 * hl);
+            l_st[s][t][1] = *(const u32x4 *)(p + 64 * h + 32 + 16 * hl);
+            qh_st[s][t] = *(const u32x4 *)(p + 128 + 32 * h + 16 * hl);
+            if (h == 0) {
+                sc_st[s][t] = *(const u32x4 *)(p + 192);
+                dw_st[s][t] = *(const uint32_t *)(p + 208);
+            }
+        }
+    };
+    auto issue_a = [&](auto stage, int kt_req) __attribute__((always_inline)) {
+        constexpr int s = decltype(stage)::value, h = s & 1;
+        const int kt = 2 * sb_first + min(kt_req, n_kt - 1);
+        const int sb = kt >> 1;
+        const uint8_t * abase = Aq + (size_t)kt * 256;
+#pragma unroll
+        for (int i = 0; i < A_PER_T; i++) a_st[s][i] = *(const u32x4 *)(abase + off_a[i]);
+        if (h == 0) d_st[s] = *(const float *)(Adg + (size_t)sb * 4 + off_d);
+    };
+
+    float16v P[TM][TN], S[TM][TN], T[TM][TN];
+    const float16v zero16 = {};
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int t = 0; t < TN; t++) { P[i][t] = zero16; S[i][t] = zero16; T[i][t] = zero16; }
+    u32x4 sc4[TN];
+    uint32_t dwh[TN];
+    const uint32_t M78 = 0x00780078u, MG58 = 0x58005800u, M300 = 0x03000300u, MG44 = 0x44004400u;
+
+    auto step = [&](auto stage, int kt) __attribute__((always_inline)) {
+        constexpr int s = decltype(stage)::value, h = s & 1, buf = s & 1;
+        const int mbuf = (kt >> 1) & 1;
+#pragma unroll
+        for (int i = 0; i < A_PER_T; i++) {
+            const int c = tid + 256 * i, r = c >> 4, cc = c & 15;
+            *(u32x4 *)(&As[buf][r * AST + cc * 8]) = a_st[buf][i];
+        }
+        if (h == 0) {
+            if (tid < BM) Ad[mbuf][tid] = d_st[buf];
+#pragma unroll
+            for (int t = 0; t < TN; t++) { sc4[t] = sc_st[s][t]; dwh[t] = dw_st[s][t]; }
+        }
+        __syncthreads();
+        issue_w(std::integral_constant<int, (s + D - 1) % D>{}, kt + D - 1);
+        issue_a(std::integral_constant<int, (s + 1) & 1>{}, kt + 1);
+
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            // quarters p and p+2 of this half: sub-blocks 8h + 2q + g
+            q6k_qc ka[TN], kb[TN];
+#pragma unroll
+            for (int t = 0; t < TN; t++) {
+                ka[t] = q6k_quarter_consts(q6k_scale(sc4[t], 8 * h + 2 * p + hl));
+                kb[t] = q6k_quarter_consts(q6k_scale(sc4[t], 8 * h + 2 * (p + 2) + hl));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int kk = i + 4 * p;
+                half8 blo[TN], bhi[TN];
+#pragma unroll
+                for (int t = 0; t < TN; t++)
+                    q6k_word(p, l_st[s][t][p][i], qh_st[s][t][i], ka[t], kb[t], blo[t], bhi[t], M78, MG58, M300,
+                             MG44);
+#pragma unroll
+                for (int ii = 0; ii < TM; ii++) {
+                    const half8 a = *(const half8 *)(&As[buf][(ii * 32 + l32) * AST + 64 * hl + 8 * kk]);
+#pragma unroll
+                    for (int t = 0; t < TN; t++) {
+                        P[ii][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, blo[t],
+                                                                          (h == 0 && kk == 0) ? zero16 : P[ii][t],
+                                                                          0, 0, 0);
+                        P[ii][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bhi[t], P[ii][t], 0, 0, 0);
+                    }
+                }
+            }
+        }
+
+        if (h == 1) {
+            // super-block complete: x = d_w*isum; S = fma(d_a, x, S)
+#pragma unroll
+            for (int t = 0; t < TN; t++) {
+                const float dw = h2f((uint16_t)(dwh[t] & 0xFFFFu));
+#pragma unroll
+                for (int ii = 0; ii < TM; ii++) {
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; q4++) {
+                        const float4 da = *(const float4 *)(&Ad[mbuf][ii * 32 + 8 * q4 + 4 * hl]);
+                        const float dav[4] = {da.x, da.y, da.z, da.w};
+#pragma unroll
+                        for (int rr = 0; rr < 4; rr++) {
+                            const int r = 4 * q4 + rr;
+                            S[ii][t][r] = fmaf(dav[rr], dw * P[ii][t][r], S[ii][t][r]);
+                        }
+                    }
+                }
+            }
+        }
+    };
+
+    issue_w(std::integral_constant<int, 0>{}, 0);
+    if constexpr (D == 4) {
+        issue_w(std::integral_constant<int, 1>{}, 1);
+        issue_w(std::integral_constant<int, 2>{}, 2);
+    }
+    issue_a(std::integral_constant<int, 0>{}, 0);
+    for (int c0 = 0; c0 < n_kt; c0 += 2 * SB_CHUNK) {
+        const int c1 = min(c0 + 2 * SB_CHUNK, n_kt);
+        for (int kt0 = c0; kt0 < c1; kt0 += D) {
+            step(std::integral_constant<int, 0>{}, kt0);
+            step(std::integral_constant<int, 1>{}, kt0 + 1);
+            if constexpr (D == 4) {
+                step(std::integral_constant<int, 2>{}, kt0 + 2);
+                step(std::integral_constant<int, 3>{}, kt0 + 3);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int t = 0; t < TN; t++) {
+                T[i][t] = T[i][t] + S[i][t];
+                S[i][t] = zero16;
+            }
+    }
+
+#pragma unroll
+    for (int t = 0; t < TN; t++) {
+        const int n = n0 + (wv * TN + t) * 32 + l32;
+        if (n >= N) continue;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + i * 32 + tile_row(r, lane);
+                if (m >= M) continue;
+                if (ws) ws[((int64_t)z * M + m) * N + n] = T[i][t][r];
+                else epilogue_store(T[i][t][r], m, n, bias, res, Y, ldy, ymap);
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // F16 weights
 // ---------------------------------------------------------------------------
 template <int TM>
@@ -798,6 +1042,50 @@ static int launch_q4k(const void * w, int N, int K, const void * act, int M, con
     return DFX_OK;
 }
 
+template <int TM, int TN, int D>
+static int launch_q6k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
+                      float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st) {
+    constexpr int BM = TM * 32, BN = 4 * TN * 32;
+    const int n_tiles = (N + BN - 1) / BN, m_tiles = (M + BM - 1) / BM;
+    const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
+    const int chunks = dot_chunks(K), passes = ws ? chunks : 1;
+    const int sb = K / 256, sb_last = sb - (chunks - 1) * (DFX_DOT_CHUNK / 256);
+    if ((2 * sb_last) % D || (chunks > 1 && (2 * (DFX_DOT_CHUNK / 256)) % D)) {
+        dfx_set_error("dfx_gemm q6_k: K=%d does not fit the pipeline depth %d", K, D);
+        return DFX_ERR_ARG;
+    }
+    hipLaunchKernelGGL((k_q6k<TM, TN, D>), dim3((unsigned)(per_pass * passes)), dim3(256), 0, st,
+                       (const uint8_t *)w, N, K, (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles, ws);
+    DFX_CHECK_LAUNCH("dfx_gemm q6_k");
+    if (ws) {
+        const int64_t MN = (int64_t)M * N;
+        const int64_t blocks = std::min<int64_t>((MN + 255) / 256, 8192);
+        hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)blocks), dim3(256), 0, st, (const float *)ws, chunks, MN, N,
+                           bias, res, y, ldy, ymap);
+        DFX_CHECK_LAUNCH("dfx_gemm q6_k reduce");
+    }
+    return DFX_OK;
+}
+
+// Q6_K: 64x128 workgroup tiles (2-deep weight ring), split K when the grid is small.
+// DFX_Q6K_TILE = "<TM>x<TN>[s|n]" forces a tile (tuning, tests).
+static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
+                        float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st) {
+    int tm = M > 48 ? 2 : 1, tn = 1;
+    const int chunks = dot_chunks(K);
+    const int64_t tiles = (int64_t)((M + 32 * tm - 1) / (32 * tm)) * ((N + 128 * tn - 1) / (128 * tn));
+    bool split = chunks > 1 && tiles * 4 < 2048 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
+    if (const char * f = getenv("DFX_Q6K_TILE")) {
+        int a = 0, b = 0;
+        if (sscanf(f, "%dx%d", &a, &b) == 2 && ((a == 1 || a == 2) && b == 1)) { tm = a; tn = b; }
+        if (strchr(f, 's')) split = chunks > 1 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
+        if (strchr(f, 'n')) split = false;
+    }
+    float * wsf = split ? (float *)ws : nullptr;
+    if (tm == 2) return launch_q6k<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st);
+    return launch_q6k<1, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st);
+}
+
 // Tile of the Q4_K kernel (TM x TN 32x32 tiles per wave, D = K steps in flight).
 // When the grid leaves the SIMDs short of two waves each, K is split at chunk
 // borders (workspace permitting).
@@ -881,7 +1169,7 @@ int dfx_gemm_ex(int wtype, const void * w, int64_t N, int64_t K, const void * ac
     const int n = (int)N, k = (int)K, m = (int)M;
     switch (wtype) {
         case DFX_TYPE_Q4_K: return dispatch_q4k(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st);
-        case DFX_TYPE_Q6_K: return dispatch_mmq<DFX_TYPE_Q6_K>(w, n, k, act, m, bias, residual, y, ldy, ymap, st);
+        case DFX_TYPE_Q6_K: return dispatch_q6k(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st);
         case DFX_TYPE_Q8_0: return dispatch_mmq<DFX_TYPE_Q8_0>(w, n, k, act, m, bias, residual, y, ldy, ymap, st);
         case DFX_TYPE_F16:
             switch (pick_tm(m, 4)) {

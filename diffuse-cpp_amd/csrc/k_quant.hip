@@ -127,6 +127,13 @@ __device__ __forceinline__ void convert_block256(const float v[4], int lane, int
             const int L = lane & 15;
             const uint16_t p[4] = {o[0], o[2], o[1], o[3]};
             store_q4((uint16_t *)(act + Lay.q) + m * K + b * 256 + 64 * (lane >> 4) + 8 * (L & 7) + 4 * (L >> 3), p);
+        } else if (mode == CONV_Q8_K_P6) {
+            // elements 4L..4L+3 (L = lane): half h = L/32, quarter q = (L/8)%4, l = 4(L%8);
+            // slot 64g + 8(i + 4(q%2)) + 4(q/2) + {0,2,1,3} with g = l/16, i = (l%16)/4
+            const int h = lane >> 5, q = (lane >> 3) & 3, l = 4 * (lane & 7), g = l >> 4, i = (l & 15) >> 2;
+            const uint16_t p[4] = {o[0], o[2], o[1], o[3]};
+            store_q4((uint16_t *)(act + Lay.q) + m * K + b * 256 + 128 * h + 64 * g + 8 * (i + 4 * (q & 1)) +
+                         4 * (q >> 1), p);
         } else {
             store_q4(q, o);
         }

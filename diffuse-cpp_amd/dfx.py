@@ -203,6 +203,21 @@ def q4k_slot_order():
     return np.array([(32 if s >= 4 else 0) + 4 * i + P[s % 4] for i in range(8) for s in range(8)], np.int64)
 
 
+def q6k_slot_order():
+    """Element index held by each slot of a 128-element half super-block of a Q6_K
+    activation buffer (slot 64g + 8(i + 4p) + s -> 32q + 16g + 4i + P[s % 4],
+    q = p + 2 (s >= 4), P = 0,2,1,3)."""
+    P = (0, 2, 1, 3)
+    order = np.empty(128, np.int64)
+    for g in range(2):
+        for p in range(2):
+            for i in range(4):
+                for s in range(8):
+                    q = p + (2 if s >= 4 else 0)
+                    order[64 * g + 8 * (i + 4 * p) + s] = 32 * q + 16 * g + 4 * i + P[s % 4]
+    return order
+
+
 def act_parts(act_buf, wtype, M, K):
     """Split a downloaded activation buffer (layout of dfx_act_bytes) into (q, d, bs);
     q is returned in element order."""
@@ -211,10 +226,11 @@ def act_parts(act_buf, wtype, M, K):
     def a256(x):
         return (x + 255) // 256 * 256
     q = raw[:M * K * 2].view(np.float16).reshape(M, K)
-    if wtype == TYPE_Q4_K:
-        stored = q.reshape(M, K // 64, 64)
+    if wtype in (TYPE_Q4_K, TYPE_Q6_K):
+        g = 64 if wtype == TYPE_Q4_K else 128
+        stored = q.reshape(M, K // g, g)
         q = np.empty_like(stored)
-        q[:, :, q4k_slot_order()] = stored
+        q[:, :, q4k_slot_order() if wtype == TYPE_Q4_K else q6k_slot_order()] = stored
         q = q.reshape(M, K)
     d_off = a256(M * K * 2)
     if wtype in (TYPE_Q4_K, TYPE_Q6_K):

@@ -173,6 +173,19 @@ def test_gemm_q4k_split_k_bit_exact(gpu, monkeypatch, tile, N, K, M):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
 
 
+@pytest.mark.parametrize("tile", ["2x1n", "1x1n", "2x1s", "1x1s"])
+@pytest.mark.parametrize("N,K,M", [(1000, 4096, 77), (640, 12288, 40), (300, 2304, 33)])
+def test_gemm_q6k_tiles_and_split_bit_exact(gpu, monkeypatch, tile, N, K, M):
+    """Q6_K kernel tiles, with and without split K (scales up to +-127 exercise the
+    exact f16 operand split), against the oracle bit for bit."""
+    monkeypatch.setenv("DFX_Q6K_TILE", tile)
+    raw = quant(dfx.TYPE_Q6_K, N, K)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    got = gpu_gemm(dfx.TYPE_Q6_K, raw, N, K, X)
+    ref = O.mul_mat(dfx.TYPE_Q6_K, raw, N, K, X)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
+
+
 @pytest.mark.parametrize("N,K,M", [(1000, 4096, 33), (4096, 4096, 288), (4096, 12288, 64)])
 def test_gemm_f16_matches_oracle(gpu, N, K, M):
     """F16: exact f16 products accumulated by MFMA in f32 (the oracle sums in f64)."""
