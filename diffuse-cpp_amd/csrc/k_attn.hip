@@ -12,36 +12,45 @@
 
 #include <algorithm>
 
-// One thread per (row, head of Q|K|V, rotation pair).
-__global__ void k_rope_store(const float * __restrict__ qkv, const int32_t * __restrict__ pos, int64_t M, int H,
-                             int Hkv, int hd, const float * __restrict__ tab, float * __restrict__ q_out,
-                             float * __restrict__ kc, float * __restrict__ vt, int64_t v_ld) {
+// One workgroup per (32-row tile, head of Q|K|V).  Q and K heads: one rotation pair
+// (i, i + hd/2) per thread, coalesced along i.  V heads: the tile passes through LDS
+// so that the transposed store vt[kvh][dim][p] takes consecutive positions from
+// consecutive lanes.
+#define ROPE_RT 32
+__global__ void __launch_bounds__(256) k_rope_store(const float * __restrict__ qkv, const int32_t * __restrict__ pos,
+                                                    int M, int H, int Hkv, int hd, const float * __restrict__ tab,
+                                                    float * __restrict__ q_out, float * __restrict__ kc,
+                                                    float * __restrict__ vt, int64_t v_ld) {
 #pragma clang fp contract(off)
+    extern __shared__ float vtile[];   // V heads: [ROPE_RT][hd + 1]
     const int half = hd / 2, heads = H + 2 * Hkv;
-    const int64_t total = M * heads * half;
-    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-         idx += (int64_t)gridDim.x * blockDim.x) {
-        const int i = (int)(idx % half);
-        const int64_t t = idx / half;
-        const int hh = (int)(t % heads);
-        const int64_t m = t / heads;
-        const float * src = qkv + m * heads * hd + (int64_t)hh * hd;
-        const int p = pos[m];
-        const float x0 = src[i], x1 = src[i + half];
-        if (hh < H + Hkv) {
+    const int hh = blockIdx.y, m0 = blockIdx.x * ROPE_RT;
+    const int rows = min(ROPE_RT, M - m0);
+    const int64_t ld = (int64_t)heads * hd;
+    if (hh < H + Hkv) {
+        for (int e = threadIdx.x; e < rows * half; e += blockDim.x) {
+            const int r = e / half, i = e - r * half, m = m0 + r;
+            const float * src = qkv + m * ld + (int64_t)hh * hd;
+            const int p = pos[m];
+            const float x0 = src[i], x1 = src[i + half];
             // ggml_rope_ext NEOX: rotate (i, i + n_dims/2) by theta_i(p)
-            const float c = tab[((int64_t)p * half + i) * 2 + 0];
-            const float s = tab[((int64_t)p * half + i) * 2 + 1];
-            const float y0 = x0 * c - x1 * s;
-            const float y1 = x0 * s + x1 * c;
-            float * dst = (hh < H) ? q_out + (m * H + hh) * hd
-                                   : kc + ((int64_t)p * Hkv + (hh - H)) * hd;
+            const float2 cs = *(const float2 *)(tab + ((int64_t)p * half + i) * 2);
+            const float y0 = x0 * cs.x - x1 * cs.y;
+            const float y1 = x0 * cs.y + x1 * cs.x;
+            float * dst = hh < H ? q_out + ((int64_t)m * H + hh) * hd : kc + ((int64_t)p * Hkv + (hh - H)) * hd;
             dst[i] = y0;
             dst[i + half] = y1;
-        } else {
-            float * dst = vt + (int64_t)(hh - H - Hkv) * hd * v_ld + p;
-            dst[(int64_t)i * v_ld] = x0;
-            dst[(int64_t)(i + half) * v_ld] = x1;
+        }
+    } else {
+        const int kvh = hh - H - Hkv, ls = hd + 1;
+        for (int e = threadIdx.x; e < rows * hd; e += blockDim.x) {
+            const int r = e / hd, i = e - r * hd;
+            vtile[r * ls + i] = qkv[(int64_t)(m0 + r) * ld + (int64_t)hh * hd + i];
+        }
+        __syncthreads();
+        for (int e = threadIdx.x; e < hd * ROPE_RT; e += blockDim.x) {
+            const int i = e / ROPE_RT, r = e - i * ROPE_RT;
+            if (r < rows) vt[((int64_t)kvh * hd + i) * v_ld + pos[m0 + r]] = vtile[r * ls + i];
         }
     }
 }
@@ -295,10 +304,13 @@ extern "C" int dfx_rope_store(const float * qkv, const int32_t * pos, int64_t M,
         return DFX_ERR_ARG;
     }
     if (M == 0) return DFX_OK;
-    const int64_t total = M * (H + 2 * Hkv) * (hd / 2);
-    const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
-    hipLaunchKernelGGL(k_rope_store, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, qkv, pos, M, H, Hkv,
-                       hd, tab, q_out, kc, vt, v_ld);
+    if (M > INT32_MAX - ROPE_RT || H + 2 * Hkv > 65535 || hd > 1024) {
+        dfx_set_error("dfx_rope_store: shape too large M=%lld heads=%d hd=%d", (long long)M, H + 2 * Hkv, hd);
+        return DFX_ERR_ARG;
+    }
+    const dim3 grid((unsigned)((M + ROPE_RT - 1) / ROPE_RT), (unsigned)(H + 2 * Hkv));
+    hipLaunchKernelGGL(k_rope_store, grid, dim3(256), ROPE_RT * (hd + 1) * sizeof(float), (hipStream_t)stream, qkv,
+                       pos, (int)M, H, Hkv, hd, tab, q_out, kc, vt, v_ld);
     DFX_CHECK_LAUNCH("dfx_rope_store");
     return DFX_OK;
 }

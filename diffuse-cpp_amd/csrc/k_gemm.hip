@@ -1074,7 +1074,7 @@ static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, c
     int tm = M > 48 ? 2 : 1, tn = 1;
     const int chunks = dot_chunks(K);
     const int64_t tiles = (int64_t)((M + 32 * tm - 1) / (32 * tm)) * ((N + 128 * tn - 1) / (128 * tn));
-    bool split = chunks > 1 && tiles * 4 < 2048 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
+    bool split = chunks > 1 && tiles * 4 < 1024 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
     if (const char * f = getenv("DFX_Q6K_TILE")) {
         int a = 0, b = 0;
         if (sscanf(f, "%dx%d", &a, &b) == 2 && ((a == 1 || a == 2) && b == 1)) { tm = a; tn = b; }
@@ -1105,7 +1105,7 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
         const int BM = 32 * cands[pick].tm, BN = 128 * cands[pick].tn;
         tiles = (int64_t)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     }
-    bool split = chunks > 1 && tiles * 4 < 2048 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
+    bool split = chunks > 1 && tiles * 4 < 1024 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
     // DFX_Q4K_TILE="<TM>x<TN>[x<D>][s|n]" forces a configuration (tuning, tests):
     // s = split K when possible, n = never split.
     if (const char * f = getenv("DFX_Q4K_TILE")) {

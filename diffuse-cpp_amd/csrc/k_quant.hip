@@ -171,42 +171,57 @@ __global__ void k_act_convert(int mode, const float * x, int64_t M, int64_t K, u
     convert_block256(v, lane, mode, act, Lay, m, K, b);
 }
 
-// RMSNorm + weight + conversion; one 256-thread workgroup per row.
+// RMSNorm + weight + conversion; one workgroup of up to 16 waves per row.  Wave wv
+// owns the BPW consecutive 256-element blocks from wv*BPW; x and w are loaded once,
+// before the row reduction, and kept in registers for the scaling pass.
 // GGML ggml_compute_forward_rms_norm_f32: sum += (double)(x*x); mean = (float)(sum/K);
 // scale = 1.0f/sqrtf(mean + eps); y = x*scale; then ggml_mul by w.
 // Output row m normalises input row xmap[m] (or m).
-__global__ void __launch_bounds__(256) k_rmsnorm_convert(int mode, const float * x, const int32_t * xmap,
-                                                         const float * w, int64_t M, int64_t K, float eps,
-                                                         uint8_t * act) {
+template <int BPW>
+__global__ void __launch_bounds__(1024) k_rmsnorm_convert(int mode, const float * x, const int32_t * xmap,
+                                                          const float * w, int64_t M, int64_t K, float eps,
+                                                          uint8_t * act) {
 #pragma clang fp contract(off)
-    __shared__ double red[4];
+    __shared__ double red[16];
     const int64_t m = blockIdx.x;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
+    const int nb = (int)(K >> 8);
     const float * xr = x + (int64_t)(xmap ? xmap[m] : m) * K;
+    float4 t[BPW], g[BPW];
+#pragma unroll
+    for (int j = 0; j < BPW; j++) {
+        const int b = min(wv * BPW + j, nb - 1);   // clamped: the duplicate is not summed or stored
+        t[j] = *(const float4 *)(xr + (int64_t)b * 256 + 4 * lane);
+        g[j] = *(const float4 *)(w + (int64_t)b * 256 + 4 * lane);
+    }
     double s = 0.0;
-    for (int64_t k = 4 * tid; k < K; k += 1024) {
-        const float4 t = *(const float4 *)(xr + k);
-        s += (double)(t.x * t.x);
-        s += (double)(t.y * t.y);
-        s += (double)(t.z * t.z);
-        s += (double)(t.w * t.w);
+#pragma unroll
+    for (int j = 0; j < BPW; j++) {
+        if (wv * BPW + j < nb) {
+            s += (double)(t[j].x * t[j].x);
+            s += (double)(t[j].y * t[j].y);
+            s += (double)(t[j].z * t[j].z);
+            s += (double)(t[j].w * t[j].w);
+        }
     }
     s = wave_sum_d(s);
     if (lane == 0) red[wv] = s;
     __syncthreads();
-    const double tot = red[0] + red[1] + red[2] + red[3];
+    double tot = 0.0;
+    for (int i = 0; i < nw; i++) tot += red[i];
     const float mean = (float)(tot / (double)K);
     // correctly rounded sqrtf and division (double rounding is exact for these ops)
     const float root = (float)sqrt((double)(mean + eps));
     const float scale = (float)(1.0 / (double)root);
     const act_layout Lay = act_layout_of(mode, M, K);
-    const int64_t nb = K >> 8;
-    for (int64_t b = wv; b < nb; b += 4) {
-        const int64_t k = b * 256 + 4 * lane;
-        const float4 t = *(const float4 *)(xr + k);
-        const float4 g = *(const float4 *)(w + k);
-        const float v[4] = {(t.x * scale) * g.x, (t.y * scale) * g.y, (t.z * scale) * g.z, (t.w * scale) * g.w};
-        convert_block256(v, lane, mode, act, Lay, m, K, b);
+#pragma unroll
+    for (int j = 0; j < BPW; j++) {
+        const int b = wv * BPW + j;
+        if (b < nb) {
+            const float v[4] = {(t[j].x * scale) * g[j].x, (t[j].y * scale) * g[j].y, (t[j].z * scale) * g[j].z,
+                                (t[j].w * scale) * g[j].w};
+            convert_block256(v, lane, mode, act, Lay, m, K, b);
+        }
     }
 }
 
@@ -292,9 +307,19 @@ int dfx_rmsnorm_convert_ex(int wtype, const float * x, const int32_t * xmap, con
         dfx_set_error("dfx_rmsnorm_convert: unsupported type %d or K %lld", wtype, (long long)K);
         return DFX_ERR_UNSUPPORTED;
     }
+    const int64_t nb = K >> 8;
+    if (nb > 128) {
+        dfx_set_error("dfx_rmsnorm_convert: K %lld above 32768", (long long)K);
+        return DFX_ERR_UNSUPPORTED;
+    }
     if (M == 0) return DFX_OK;
-    hipLaunchKernelGGL(k_rmsnorm_convert, dim3((unsigned)M), dim3(256), 0, (hipStream_t)stream,
-                       conv_mode(wtype), x, xmap, w, M, K, eps, (uint8_t *)act);
+    // blocks per wave: the fewest that keep the row within 16 waves
+    const int bpw = nb <= 16 ? 1 : nb <= 32 ? 2 : nb <= 64 ? 4 : 8;
+    const dim3 block((unsigned)(64 * ((nb + bpw - 1) / bpw)));
+    auto kern = bpw == 1 ? k_rmsnorm_convert<1> : bpw == 2 ? k_rmsnorm_convert<2>
+              : bpw == 4 ? k_rmsnorm_convert<4> : k_rmsnorm_convert<8>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)M), block, 0, (hipStream_t)stream, conv_mode(wtype), x, xmap, w, M, K,
+                       eps, (uint8_t *)act);
     DFX_CHECK_LAUNCH("dfx_rmsnorm_convert");
     return DFX_OK;
 }

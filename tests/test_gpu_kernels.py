@@ -98,11 +98,12 @@ def test_act_convert_matches_oracle(gpu, typ):
     check_act(ab, typ, oracle_act(typ, x), M, K)
 
 
-def test_rmsnorm_convert_matches_oracle(gpu):
-    M, K, eps = 29, 4096, 1e-5
+@pytest.mark.parametrize("K", [4096, 1280, 5120, 9472])   # 1, 1, 2 and 4 blocks per wave
+def test_rmsnorm_convert_matches_oracle(gpu, K):
+    M, eps = 29, 1e-5
     x = (rng.standard_normal((M, K)) * 3).astype(np.float32)
     w = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
-    for typ in (dfx.TYPE_Q4_K, dfx.TYPE_Q8_0, dfx.TYPE_F16):
+    for typ in (dfx.TYPE_Q4_K, dfx.TYPE_Q6_K, dfx.TYPE_Q8_0, dfx.TYPE_F16):
         xb, wb, ab = dfx.Buf.of(x), dfx.Buf.of(w), dfx.Buf(L().dfx_act_bytes(typ, M, K))
         dfx.check(L().dfx_rmsnorm_convert(typ, xb.ptr, wb.ptr, M, K, eps, ab.ptr, None), "rmsnorm")
         check_act(ab, typ, oracle_act(typ, O.rms_norm_mul(x, w, eps)), M, K)
@@ -218,8 +219,8 @@ def test_gemm_bias_and_residual_epilogue(gpu):
 
 
 # ---------------------------------------------------------------- RoPE + attention
-def test_rope_store_matches_oracle(gpu):
-    M, H, Hkv, hd, n_ctx = 23, 8, 2, 128, 64
+@pytest.mark.parametrize("M,H,Hkv,hd,n_ctx", [(23, 8, 2, 128, 64), (77, 4, 4, 64, 96), (65, 28, 4, 128, 300)])
+def test_rope_store_matches_oracle(gpu, M, H, Hkv, hd, n_ctx):
     qkv = rng.standard_normal((M, (H + 2 * Hkv) * hd)).astype(np.float32)
     pos = rng.permutation(n_ctx)[:M].astype(np.int32)
     tab = O.rope_table(n_ctx, hd, 1000000.0)
