@@ -85,15 +85,33 @@ __host__ __device__ inline bool conv_is_q8k(int mode) {
     return mode == CONV_Q8_K || mode == CONV_Q8_K_P4 || mode == CONV_Q8_K_P6;
 }
 
+// For both permuted modes q is stored in MFMA fragment order, rows padded to a
+// multiple of 32.  The slot sl = 256*sb + 128*h + 64*hl + 8*kk + j (slot order as
+// above) of row m is at half index
+//   (((m/32) * (K/128) + 2*sb + h) * 8 + kk) * 512 + (m%32 + 32*hl) * 8 + j
+// so that the eight A operands (32 rows x 16 slots, 1 KB each) of one 128-slot K
+// step of a 32-row tile are 8 KB of consecutive memory, the 16 bytes of MFMA lane
+// m%32 + 32*hl at byte 16*lane of operand kk.
+__host__ __device__ inline bool conv_is_frag(int mode) { return mode == CONV_Q8_K_P4 || mode == CONV_Q8_K_P6; }
+__host__ __device__ inline int64_t act_q_rows(int mode, int64_t M) { return conv_is_frag(mode) ? (M + 31) & ~(int64_t)31 : M; }
+__host__ __device__ inline int64_t act_frag_off(int64_t m, int64_t sl, int64_t K) {
+    const int64_t step = sl >> 7, w = sl & 127, hl = w >> 6, kk = (w >> 3) & 7, j = w & 7;
+    return ((((m >> 5) * (K >> 7) + step) * 8 + kk) * 64 + (m & 31) + 32 * hl) * 8 + j;
+}
+
+// The d of the permuted modes is stored super-block major, d[K/256][ceil(M/32)*32]
+// (the scales of consecutive rows of one super-block are adjacent).
 struct act_layout {
     size_t q, d, bs, bytes;
+    int64_t mq;   // rows of q (and, for the permuted modes, the row stride of d)
 };
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 __host__ __device__ inline act_layout act_layout_of(int mode, int64_t M, int64_t K) {
     act_layout L;
     L.q = 0;
-    L.d = align256((size_t)M * K * 2);
-    const size_t nd = conv_is_q8k(mode) ? (size_t)M * (K / 256) : mode == CONV_Q8_0 ? (size_t)M * (K / 32) : 0;
+    L.mq = act_q_rows(mode, M);
+    L.d = align256((size_t)L.mq * K * 2);
+    const size_t nd = conv_is_q8k(mode) ? (size_t)L.mq * (K / 256) : mode == CONV_Q8_0 ? (size_t)M * (K / 32) : 0;
     L.bs = align256(L.d + nd * 4);
     const size_t nbs = conv_is_q8k(mode) ? (size_t)M * (K / 16) : 0;
     L.bytes = align256(L.bs + nbs * 2);

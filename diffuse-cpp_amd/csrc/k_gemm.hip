@@ -381,10 +381,13 @@ __device__ __forceinline__ uint32_t h2pair(float v) {
 }
 
 // v_and_or_b32 (x & m) | o; the masks live in VGPRs (gfx9 VOP3 takes no literals).
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(o));
-    return r;
+// (x & m) | o for an o with no bits inside m, written as (x & m) | (o & ~m) so that it
+// becomes one v_bfi_b32.  m and o must reach it as register values (opaque()):
+// with literal constants the compiler folds o & ~m and emits an and and an or.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) { return (x & m) | (o & ~m); }
+__device__ __forceinline__ uint32_t opaque(uint32_t x) {
+    asm volatile("" : "+v"(x));
+    return x;
 }
 
 // Q4_K header of one super-block held in registers: x = {d, dmin}, y/z/w = scales[0..11].
@@ -444,10 +447,10 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
       int n_tiles, int m_tiles, float * __restrict__ ws) {
 #pragma clang fp contract(off)
     constexpr int BM = TM * 32, BN = 4 * TN * 32;
-    constexpr int AST = 128 + 8;             // LDS halves per activation row and K step
     constexpr int BST = 24;                  // LDS halves per row of 16 block sums
     constexpr int A_PER_T = BM * 16 / 256;   // 16-byte chunks of the A tile per thread
-    __shared__ __attribute__((aligned(16))) half_t As[2][BM * AST];
+    // A tile of one K step in fragment order: operand kk of row tile i at half (8i + kk) * 512
+    __shared__ __attribute__((aligned(16))) half_t As[2][BM * 128];
     __shared__ __attribute__((aligned(16))) float Ad[2][BM];
     __shared__ __attribute__((aligned(16))) half_t Abs[2][BM * BST];
 
@@ -468,6 +471,7 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
     const int n_kt = 2 * n_sb;
     const uint32_t row_bytes = (uint32_t)n_sb_all * SB_Q4_K;
     const act_layout Lay = act_layout_of(CONV_Q8_K_P4, M, K);
+    const int m_pad = (int)act_q_rows(CONV_Q8_K_P4, M);
     const uint8_t * Aq = act + Lay.q;
     const uint8_t * Adg = act + Lay.d;
     const uint8_t * Absg = act + Lay.bs;
@@ -479,12 +483,13 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
     uint32_t off_a[A_PER_T], off_w[TN];
 #pragma unroll
     for (int i = 0; i < A_PER_T; i++) {
-        const int c = tid + 256 * i, r = c >> 4, cc = c & 15;
-        off_a[i] = ((uint32_t)min(m0 + r, M - 1) * (uint32_t)K + (uint32_t)cc * 8u) * 2u;
+        // chunk c of the step: row tile c / 512 (clamped to the padded rows), 16 bytes c % 512
+        const int c = tid + 256 * i, mt = min(m0 / 32 + (c >> 9), m_pad / 32 - 1);
+        off_a[i] = (uint32_t)mt * (uint32_t)(K / 128) * 8192u + (uint32_t)(c & 511) * 16u;
     }
 #pragma unroll
     for (int t = 0; t < TN; t++) off_w[t] = (uint32_t)min(n0 + (wv * TN + t) * 32 + l32, N - 1) * row_bytes;
-    const uint32_t off_d = (uint32_t)min(m0 + tid % BM, M - 1) * (uint32_t)n_sb_all * 4u;
+    const uint32_t off_d = (uint32_t)min(m0 + tid % BM, M - 1) * 4u;   // d is [sb][m_pad]
     const uint32_t off_b = ((uint32_t)min(m0 + (tid >> 1) % BM, M - 1) * (uint32_t)(K / 16) + (tid & 1) * 8u) * 2u;
 
     // Register rings: weight stage s holds the nibbles (and header) of K step kt with
@@ -516,11 +521,11 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
         constexpr int s = decltype(stage)::value, h = s & 1;
         const int kt = 2 * sb_first + min(kt_req, n_kt - 1);
         const int sb = kt >> 1;
-        const uint8_t * abase = Aq + (size_t)kt * 256;
+        const uint8_t * abase = Aq + (size_t)kt * 8192;
 #pragma unroll
         for (int i = 0; i < A_PER_T; i++) a_st[s][i] = *(const u32x4 *)(abase + off_a[i]);
         if (h == 0) {
-            d_st[s] = *(const float *)(Adg + (size_t)sb * 4 + off_d);
+            d_st[s] = *(const float *)(Adg + (size_t)sb * m_pad * 4 + off_d);
             b_st[s] = *(const u32x4 *)(Absg + (size_t)sb * 32 + off_b);
         }
     };
@@ -533,20 +538,26 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
         for (int t = 0; t < TN; t++) { P[i][t] = zero16; S[i][t] = zero16; T[i][t] = zero16; }
     u32x4 hdr[TN];
     q4k_sm sm[TN];
-    const uint32_t MASK_LO = 0x000F000Fu, MASK_HI = 0x00F000F0u, MAGIC = 0x64006400u;
+    const uint32_t MASK_LO = opaque(0x000F000Fu), MASK_HI = opaque(0x00F000F0u), MAGIC = opaque(0x64006400u);
 
     auto step = [&](auto stage, int kt) __attribute__((always_inline)) {
         constexpr int s = decltype(stage)::value, h = s & 1, buf = s & 1;
         const int mbuf = (kt >> 1) & 1;
+        // The step's phases are fenced from the scheduler: loads moved below the
+        // fence after the issue block would be waited for right after issue, and
+        // ring registers refilled before their last use would need copies (and
+        // waits) at the loop back-edge.
+        __builtin_amdgcn_sched_barrier(0);
         // activation stage -> LDS
 #pragma unroll
         for (int i = 0; i < A_PER_T; i++) {
-            const int c = tid + 256 * i, r = c >> 4, cc = c & 15;
-            *(u32x4 *)(&As[buf][r * AST + cc * 8]) = a_st[buf][i];
+            *(u32x4 *)(&As[buf][(tid + 256 * i) * 8]) = a_st[buf][i];
         }
         if (h == 0) {
-            if (tid < BM) Ad[mbuf][tid] = d_st[buf];
-            if (tid < 2 * BM) *(u32x4 *)(&Abs[mbuf][(tid >> 1) * BST + (tid & 1) * 8]) = b_st[buf];
+            // every thread stores (threads of the same row store the same value), so
+            // no branch lets the compiler sink the scale loads next to these stores
+            Ad[mbuf][tid % BM] = d_st[buf];
+            *(u32x4 *)(&Abs[mbuf][((tid >> 1) % BM) * BST + (tid & 1) * 8]) = b_st[buf];
 #pragma unroll
             for (int t = 0; t < TN; t++) {
                 hdr[t] = h_st[s][t];
@@ -554,9 +565,12 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
             }
         }
         __syncthreads();
-        // weights D-1 K steps ahead, activations one
-        issue_w(std::integral_constant<int, (s + D - 1) % D>{}, kt + D - 1);
+        // activations one K step ahead, then weights D-1 steps ahead.  Loads complete
+        // in issue order, so the wait for the next step's activations (at the top of
+        // that step) never waits for the weight loads issued here.
         issue_a(std::integral_constant<int, (s + 1) & 1>{}, kt + 1);
+        issue_w(std::integral_constant<int, (s + D - 1) % D>{}, kt + D - 1);
+        __builtin_amdgcn_sched_barrier(0);
 
         // group g = 2h + hl: scales of sub-blocks 4h + 2hl and 4h + 2hl + 1
         q4k_consts kc[TN];
@@ -568,7 +582,7 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
         for (int kk = 0; kk < 8; kk++)
 #pragma unroll
             for (int i = 0; i < TM; i++)
-                afr[kk][i] = *(const half8 *)(&As[buf][(i * 32 + l32) * AST + 64 * hl + 8 * kk]);
+                afr[kk][i] = *(const half8 *)(&As[buf][(8 * i + kk) * 512 + 8 * lane]);
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) {
             half8 b[TN];
@@ -609,12 +623,13 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
         }
     };
 
+    // same issue order as the steady state: activations, then weights
+    issue_a(std::integral_constant<int, 0>{}, 0);
     issue_w(std::integral_constant<int, 0>{}, 0);
     if constexpr (D == 4) {
         issue_w(std::integral_constant<int, 1>{}, 1);
         issue_w(std::integral_constant<int, 2>{}, 2);
     }
-    issue_a(std::integral_constant<int, 0>{}, 0);
     // chunks of SB_CHUNK super-blocks (the first at sb_first, a multiple of SB_CHUNK);
     // every chunk's K steps are a multiple of D
     for (int c0 = 0; c0 < n_kt; c0 += 2 * SB_CHUNK) {
@@ -638,6 +653,289 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
     }
 
     // split K: the chunk sum goes to ws[z][m][n]; the reduction adds the chunks in order
+#pragma unroll
+    for (int t = 0; t < TN; t++) {
+        const int n = n0 + (wv * TN + t) * 32 + l32;
+        if (n >= N) continue;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + i * 32 + tile_row(r, lane);
+                if (m >= M) continue;
+                if (ws) ws[((int64_t)z * M + m) * N + n] = T[i][t][r];
+                else epilogue_store(T[i][t][r], m, n, bias, res, Y, ldy, ymap);
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Q4_K, many rows: each wave computes 64 x 64 outputs (2 x 2 MFMA tiles, every A
+// operand feeds two MFMAs), four waves side by side make a 64 x 256 workgroup tile,
+// one workgroup per CU.  Everything a K step (128 elements) needs is requested
+// DEPTH-1 steps ahead, nine loads per wave and step, in this order:
+//   4 copies global -> LDS of the step's fragment-ordered A (16 KB per workgroup);
+//   1 copy global -> LDS: even steps the super-block headers of the wave's 64
+//     weight rows, odd steps the super-block's activation scales (d_a by waves 0
+//     and 3, the block sums of rows 0-31 / 32-63 by waves 1 / 2);
+//   4 copies global -> LDS of the wave's packed nibbles (32 bytes per lane and row).
+// All rings (DEPTH slots) are in LDS; registers carry only the sums from one step to
+// the next, which leaves room for every A operand of a step to be in flight at once.
+// Loads complete in issue order, so "this wave's copies for step kt are done" is a
+// wait for all but the 4 + 9*(DEPTH-2) loads issued after them; a barrier then makes
+// every wave's copies visible.  Sums and their order: as k_q4k.
+__host__ __device__ constexpr int waitcnt_vm_lgkm(int vm, int lgkm) {
+    return (vm & 15) | (7 << 4) | ((lgkm & 15) << 8) | ((vm >> 4) << 14);
+}
+// Workgroup barrier without the memory fence of __syncthreads (whose release would
+// wait for every outstanding load, the copies to LDS included); the empty asm with a
+// memory clobber keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void barrier_only() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+typedef __attribute__((address_space(3))) void * lds_ptr;
+
+template <int TN, int DEPTH>
+__global__ void __launch_bounds__(256, TN == 1 ? 2 : 1)
+k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__ act, int M,
+        const float * __restrict__ bias, const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
+        int n_tiles, int m_tiles, float * __restrict__ ws) {
+#pragma clang fp contract(off)
+    constexpr int TM = 2, BM = 64, BN = 128 * TN, WSZ = 2048 * TN;   // WSZ: nibble bytes per wave and step
+    static_assert(DEPTH == 2 || DEPTH == 4, "ring depth 2 or 4");
+    static_assert(TN == 1 || TN == 2, "one or two column tiles per wave");
+    // Separate arrays per ring slot: the compiler then knows that reading one slot
+    // does not have to wait for the copies in flight into the others.
+    __shared__ __attribute__((aligned(1024))) half_t As0[BM * 128], As1[BM * 128], As2[DEPTH > 2 ? BM * 128 : 8],
+        As3[DEPTH > 2 ? BM * 128 : 8];
+    // nibble slots: [wave][t][j][lane][16 B], j = the two 16-byte halves of a lane's 32 bytes
+    __shared__ __attribute__((aligned(1024))) uint8_t Ws0[4 * WSZ], Ws1[4 * WSZ], Ws2[DEPTH > 2 ? 4 * WSZ : 16],
+        Ws3[DEPTH > 2 ? 4 * WSZ : 16];
+    // header slots: [wave][lane][16 B] (TN 2: lane = t*32 + row; TN 1: rows repeat in both halves)
+    __shared__ __attribute__((aligned(1024))) uint8_t Hs0[4 * 1024], Hs1[DEPTH > 2 ? 4 * 1024 : 16];
+    // scale slots: [0, 2 KB) block sums [row][16], [2 KB, 3 KB) d of rows m0.. (64 used)
+    __shared__ __attribute__((aligned(1024))) uint8_t Sc0[3 * 1024], Sc1[DEPTH > 2 ? 3 * 1024 : 16];
+    auto aslot = [&](auto stage) __attribute__((always_inline)) -> half_t * {
+        constexpr int s = decltype(stage)::value;
+        if constexpr (s == 0) return As0;
+        else if constexpr (s == 1) return As1;
+        else if constexpr (s == 2) return As2;
+        else return As3;
+    };
+    auto wslot = [&](auto stage) __attribute__((always_inline)) -> uint8_t * {
+        constexpr int s = decltype(stage)::value;
+        if constexpr (s == 0) return Ws0;
+        else if constexpr (s == 1) return Ws1;
+        else if constexpr (s == 2) return Ws2;
+        else return Ws3;
+    };
+
+    const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
+    const int z = blockIdx.x / per_pass, L = blockIdx.x - z * per_pass, xcd = L & 7, j = L >> 3;
+    const int ty = j % m_tiles, tx = 8 * (j / m_tiles) + xcd;
+    if (tx >= n_tiles) return;
+
+    const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n0 = tx * BN, m0 = ty * BM;
+    constexpr int SB_CHUNK = DFX_DOT_CHUNK / 256;
+    const int n_sb_all = K >> 8;
+    const int sb_first = ws ? z * SB_CHUNK : 0;
+    const int n_sb = ws ? min(SB_CHUNK, n_sb_all - sb_first) : n_sb_all;
+    const int n_kt = 2 * n_sb;
+    const uint32_t row_bytes = (uint32_t)n_sb_all * SB_Q4_K;
+    const act_layout Lay = act_layout_of(CONV_Q8_K_P4, M, K);
+    const int m_pad = (int)act_q_rows(CONV_Q8_K_P4, M);
+
+    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void *)W, 0, 0xFFFFFFFF, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc((void *)act, 0, (int)Lay.bytes, 0x00020000);
+
+    // per-lane byte offsets (fixed); the step moves only the scalar offsets
+    uint32_t off_a[4];   // this wave copies A operands 4wv..4wv+3 of the step: row tile f/8, operand f%8
+#pragma unroll
+    for (int f = 0; f < 4; f++) {
+        const int ff = 4 * wv + f, mt = min(m0 / 32 + (ff >> 3), m_pad / 32 - 1);
+        off_a[f] = (uint32_t)Lay.q + (uint32_t)mt * (uint32_t)(K / 128) * 8192u + (uint32_t)(ff & 7) * 1024u +
+                   (uint32_t)lane * 16u;
+    }
+    // (fixed size: this clang drops the host stub of a kernel template whose lambdas
+    // capture a local array sized by a template parameter)
+    uint32_t off_w[2];
+#pragma unroll
+    for (int t = 0; t < TN; t++) off_w[t] = (uint32_t)min(n0 + (wv * TN + t) * 32 + l32, N - 1) * row_bytes;
+    const uint32_t off_h = (uint32_t)min(n0 + 32 * TN * wv + (TN == 2 ? lane : l32), N - 1) * row_bytes;
+    // scale copies (16 bytes a lane): waves 1, 2 the block sums of rows 32(wv-1) + lane/2,
+    // waves 0, 3 the same 1 KB of d from row m0 on (d is [sb][m_pad]; 64 of those rows
+    // are used; lanes past the buffer's end read nothing: the buffer's extent is set)
+    const bool bs_wave = wv == 1 || wv == 2;
+    const uint32_t off_s = bs_wave
+        ? (uint32_t)Lay.bs + ((uint32_t)min(m0 + 32 * (wv - 1) + (lane >> 1), M - 1) * (uint32_t)(K / 16) +
+                              (lane & 1) * 8u) * 2u
+        : (uint32_t)Lay.d + (uint32_t)m0 * 4u + (uint32_t)lane * 16u;
+    const int s_step = bs_wave ? 32 : m_pad * 4;   // bytes per super-block
+
+    // Header and scale slots alternate with the super-block (DEPTH 4: the slot of the
+    // steps of stage s is (s / 2) % 2, as every chunk starts at an even super-block and
+    // on a multiple of 4 steps); with DEPTH 2 one slot each suffices.
+    auto hslot = [&](auto stage) __attribute__((always_inline)) -> uint8_t * {
+        constexpr int s = decltype(stage)::value;
+        if constexpr (DEPTH == 4 && ((s >> 1) & 1)) return Hs1;
+        else return Hs0;
+    };
+    auto sslot = [&](auto stage) __attribute__((always_inline)) -> uint8_t * {
+        constexpr int s = decltype(stage)::value;
+        if constexpr (DEPTH == 4 && ((s >> 1) & 1)) return Sc1;
+        else return Sc0;
+    };
+    const int sc_dst = bs_wave ? 1024 * (wv - 1) : 2048;   // this wave's copy within a scale slot
+
+    auto issue = [&](auto stage, int kt_req) __attribute__((always_inline)) {
+        constexpr int s = decltype(stage)::value, h = s & 1;
+        const int kt = 2 * sb_first + min(kt_req, n_kt - 1);
+        const int sb = kt >> 1;
+#pragma unroll
+        for (int f = 0; f < 4; f++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_ptr)(aslot(stage) + (4 * wv + f) * 512), 16, off_a[f],
+                                                     kt * 8192, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (h == 0)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, (lds_ptr)(hslot(stage) + 1024 * wv), 16, off_h, sb * SB_Q4_K,
+                                                     0, 0);
+        else
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_ptr)(sslot(stage) + sc_dst), 16, off_s,
+                                                     sb * s_step, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < TN; t++)
+#pragma unroll
+            for (int jj = 0; jj < 2; jj++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, (lds_ptr)(wslot(stage) + WSZ * wv + 1024 * (2 * t + jj)), 16,
+                                                         off_w[t] + 16 + 16 * jj + 32 * hl, sb * SB_Q4_K + 64 * h, 0, 0);
+    };
+    // per step: 4 + 1 + 2*TN loads; after a step's copies of A and its header / scale
+    // copy come its 2*TN nibble copies and DEPTH-2 whole steps
+    constexpr int WAIT_TOP = waitcnt_vm_lgkm(2 * TN + (5 + 2 * TN) * (DEPTH - 2), 0);
+
+    float16v P[TM][TN], S[TM][TN], T[TM][TN];
+    const float16v zero16 = {};
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int t = 0; t < TN; t++) { P[i][t] = zero16; S[i][t] = zero16; T[i][t] = zero16; }
+    q4k_sm sm[TN];
+    float dw[TN], dmw[TN];
+    const uint32_t MASK_LO = opaque(0x000F000Fu), MASK_HI = opaque(0x00F000F0u), MAGIC = opaque(0x64006400u);
+
+    auto step = [&](auto stage, int kt) __attribute__((always_inline)) {
+        constexpr int s = decltype(stage)::value, h = s & 1;
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(WAIT_TOP);
+        barrier_only();
+        __builtin_amdgcn_sched_barrier(0);
+        issue(std::integral_constant<int, (s + DEPTH - 1) % DEPTH>{}, kt + DEPTH - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        if (h == 0) {
+#pragma unroll
+            for (int t = 0; t < TN; t++) {
+                const u32x4 hdr = *(const u32x4 *)(hslot(stage) + 1024 * wv + 16 * (32 * t + l32));
+                sm[t] = q4k_unpack(hdr);
+                dw[t] = h2f((uint16_t)(hdr.x & 0xFFFFu));
+                dmw[t] = h2f((uint16_t)(hdr.x >> 16));
+            }
+        }
+        // every A operand and nibble word of the step requested at once (one LDS latency)
+        half8 afr[8][TM];
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++)
+#pragma unroll
+            for (int i = 0; i < TM; i++) afr[kk][i] = *(const half8 *)(aslot(stage) + (8 * i + kk) * 512 + 8 * lane);
+        u32x4 qw[TN][2];
+#pragma unroll
+        for (int t = 0; t < TN; t++)
+#pragma unroll
+            for (int jj = 0; jj < 2; jj++) qw[t][jj] = *(const u32x4 *)(wslot(stage) + WSZ * wv + 1024 * (2 * t + jj) + 16 * lane);
+        __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the MFMAs
+        q4k_consts kc[TN];
+#pragma unroll
+        for (int t = 0; t < TN; t++) kc[t] = q4k_group_consts(h == 0 ? sm[t].sc_lo : sm[t].sc_hi, 16 * hl);
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) {
+            half8 b[TN];
+#pragma unroll
+            for (int t = 0; t < TN; t++) b[t] = q4k_word(qw[t][kk >> 2][kk & 3], kc[t], MASK_LO, MASK_HI, MAGIC);
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int t = 0; t < TN; t++)
+                    P[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afr[kk][i], b[t],
+                                                                     (h == 0 && kk == 0) ? zero16 : P[i][t], 0, 0, 0);
+        }
+#ifdef DFX_W_INTERLEAVE
+        // interleave: every MFMA followed by a few VALU instructions (the next
+        // operands' dequantisation), so that the VALU work runs under the MFMAs
+#pragma unroll
+        for (int g = 0; g < 8 * TM * TN; g++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);              // 1 MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, DFX_W_INTERLEAVE, 0);   // VALU
+        }
+#endif
+
+        if (h == 1) {
+            // super-block complete: x = d_w*isum; x = fma(-dmin_w, msum, x); S = fma(d_a, x, S)
+            const half_t * Abs = (const half_t *)sslot(stage);
+            const float * Ad = (const float *)(sslot(stage) + 2048);
+#pragma unroll
+            for (int t = 0; t < TN; t++) {
+                const half8 bm = mins_half8(hl ? sm[t].mn_hi : sm[t].mn_lo);
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+                    const half8 av = *(const half8 *)(Abs + (i * 32 + l32) * 16 + 8 * hl);
+                    const float16v Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bm, zero16, 0, 0, 0);
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; q4++) {
+                        const float4 da = *(const float4 *)(Ad + i * 32 + 8 * q4 + 4 * hl);
+                        const float dav[4] = {da.x, da.y, da.z, da.w};
+#pragma unroll
+                        for (int rr = 0; rr < 4; rr++) {
+                            const int r = 4 * q4 + rr;
+                            const float x = fmaf(-dmw[t], Q[r], dw[t] * P[i][t][r]);
+                            S[i][t][r] = fmaf(dav[rr], x, S[i][t][r]);
+                        }
+                    }
+                }
+            }
+        }
+    };
+
+    issue(std::integral_constant<int, 0>{}, 0);
+    issue(std::integral_constant<int, 1>{}, 1);
+    if constexpr (DEPTH == 4) {
+        issue(std::integral_constant<int, 2>{}, 2);
+    }
+    for (int c0 = 0; c0 < n_kt; c0 += 2 * SB_CHUNK) {
+        const int c1 = min(c0 + 2 * SB_CHUNK, n_kt);
+        for (int kt0 = c0; kt0 < c1; kt0 += DEPTH) {
+            step(std::integral_constant<int, 0>{}, kt0);
+            step(std::integral_constant<int, 1>{}, kt0 + 1);
+            if constexpr (DEPTH == 4) {
+                step(std::integral_constant<int, 2>{}, kt0 + 2);
+                step(std::integral_constant<int, 3>{}, kt0 + 3);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int t = 0; t < TN; t++) {
+                T[i][t] = T[i][t] + S[i][t];
+                S[i][t] = zero16;
+            }
+    }
+    // the copies issued past the last step still land in this workgroup's LDS: let
+    // them finish before the workgroup (and its LDS) can end
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm(0, 0));
+
 #pragma unroll
     for (int t = 0; t < TN; t++) {
         const int n = n0 + (wv * TN + t) * 32 + l32;
@@ -711,9 +1009,8 @@ k_q6k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
       int n_tiles, int m_tiles, float * __restrict__ ws) {
 #pragma clang fp contract(off)
     constexpr int BM = TM * 32, BN = 4 * TN * 32;
-    constexpr int AST = 128 + 8;
     constexpr int A_PER_T = BM * 16 / 256;
-    __shared__ __attribute__((aligned(16))) half_t As[2][BM * AST];
+    __shared__ __attribute__((aligned(16))) half_t As[2][BM * 128];   // fragment order, as in k_q4k
     __shared__ __attribute__((aligned(16))) float Ad[2][BM];
 
     const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
@@ -730,18 +1027,20 @@ k_q6k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
     const int n_kt = 2 * n_sb;
     const uint32_t row_bytes = (uint32_t)n_sb_all * SB_Q6_K;
     const act_layout Lay = act_layout_of(CONV_Q8_K_P6, M, K);
+    const int m_pad = (int)act_q_rows(CONV_Q8_K_P6, M);
     const uint8_t * Aq = act + Lay.q;
     const uint8_t * Adg = act + Lay.d;
 
     uint32_t off_a[A_PER_T], off_w[TN];
 #pragma unroll
     for (int i = 0; i < A_PER_T; i++) {
-        const int c = tid + 256 * i, r = c >> 4, cc = c & 15;
-        off_a[i] = ((uint32_t)min(m0 + r, M - 1) * (uint32_t)K + (uint32_t)cc * 8u) * 2u;
+        // chunk c of the step: row tile c / 512 (clamped to the padded rows), 16 bytes c % 512
+        const int c = tid + 256 * i, mt = min(m0 / 32 + (c >> 9), m_pad / 32 - 1);
+        off_a[i] = (uint32_t)mt * (uint32_t)(K / 128) * 8192u + (uint32_t)(c & 511) * 16u;
     }
 #pragma unroll
     for (int t = 0; t < TN; t++) off_w[t] = (uint32_t)min(n0 + (wv * TN + t) * 32 + l32, N - 1) * row_bytes;
-    const uint32_t off_d = (uint32_t)min(m0 + tid % BM, M - 1) * (uint32_t)n_sb_all * 4u;
+    const uint32_t off_d = (uint32_t)min(m0 + tid % BM, M - 1) * 4u;   // d is [sb][m_pad]
 
     u32x4 a_st[2][A_PER_T];
     float d_st[2];
@@ -771,10 +1070,10 @@ k_q6k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
         constexpr int s = decltype(stage)::value, h = s & 1;
         const int kt = 2 * sb_first + min(kt_req, n_kt - 1);
         const int sb = kt >> 1;
-        const uint8_t * abase = Aq + (size_t)kt * 256;
+        const uint8_t * abase = Aq + (size_t)kt * 8192;
 #pragma unroll
         for (int i = 0; i < A_PER_T; i++) a_st[s][i] = *(const u32x4 *)(abase + off_a[i]);
-        if (h == 0) d_st[s] = *(const float *)(Adg + (size_t)sb * 4 + off_d);
+        if (h == 0) d_st[s] = *(const float *)(Adg + (size_t)sb * m_pad * 4 + off_d);
     };
 
     float16v P[TM][TN], S[TM][TN], T[TM][TN];
@@ -785,24 +1084,26 @@ k_q6k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
         for (int t = 0; t < TN; t++) { P[i][t] = zero16; S[i][t] = zero16; T[i][t] = zero16; }
     u32x4 sc4[TN];
     uint32_t dwh[TN];
-    const uint32_t M78 = 0x00780078u, MG58 = 0x58005800u, M300 = 0x03000300u, MG44 = 0x44004400u;
+    const uint32_t M78 = opaque(0x00780078u), MG58 = opaque(0x58005800u), M300 = opaque(0x03000300u),
+                   MG44 = opaque(0x44004400u);
 
     auto step = [&](auto stage, int kt) __attribute__((always_inline)) {
         constexpr int s = decltype(stage)::value, h = s & 1, buf = s & 1;
         const int mbuf = (kt >> 1) & 1;
+        __builtin_amdgcn_sched_barrier(0);     // phases fenced as in k_q4k
 #pragma unroll
         for (int i = 0; i < A_PER_T; i++) {
-            const int c = tid + 256 * i, r = c >> 4, cc = c & 15;
-            *(u32x4 *)(&As[buf][r * AST + cc * 8]) = a_st[buf][i];
+            *(u32x4 *)(&As[buf][(tid + 256 * i) * 8]) = a_st[buf][i];
         }
         if (h == 0) {
-            if (tid < BM) Ad[mbuf][tid] = d_st[buf];
+            Ad[mbuf][tid % BM] = d_st[buf];     // duplicates store the same value
 #pragma unroll
             for (int t = 0; t < TN; t++) { sc4[t] = sc_st[s][t]; dwh[t] = dw_st[s][t]; }
         }
         __syncthreads();
-        issue_w(std::integral_constant<int, (s + D - 1) % D>{}, kt + D - 1);
         issue_a(std::integral_constant<int, (s + 1) & 1>{}, kt + 1);
+        issue_w(std::integral_constant<int, (s + D - 1) % D>{}, kt + D - 1);
+        __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
         for (int p = 0; p < 2; p++) {
@@ -823,7 +1124,7 @@ k_q6k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
                              MG44);
 #pragma unroll
                 for (int ii = 0; ii < TM; ii++) {
-                    const half8 a = *(const half8 *)(&As[buf][(ii * 32 + l32) * AST + 64 * hl + 8 * kk]);
+                    const half8 a = *(const half8 *)(&As[buf][(8 * ii + kk) * 512 + 8 * lane]);
 #pragma unroll
                     for (int t = 0; t < TN; t++) {
                         P[ii][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, blo[t],
@@ -857,12 +1158,13 @@ k_q6k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
         }
     };
 
+    // same issue order as the steady state: activations, then weights
+    issue_a(std::integral_constant<int, 0>{}, 0);
     issue_w(std::integral_constant<int, 0>{}, 0);
     if constexpr (D == 4) {
         issue_w(std::integral_constant<int, 1>{}, 1);
         issue_w(std::integral_constant<int, 2>{}, 2);
     }
-    issue_a(std::integral_constant<int, 0>{}, 0);
     for (int c0 = 0; c0 < n_kt; c0 += 2 * SB_CHUNK) {
         const int c1 = min(c0 + 2 * SB_CHUNK, n_kt);
         for (int kt0 = c0; kt0 < c1; kt0 += D) {
@@ -1042,6 +1344,30 @@ static int launch_q4k(const void * w, int N, int K, const void * act, int M, con
     return DFX_OK;
 }
 
+template <int TN, int DEPTH>
+static int launch_q4k_w(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
+                        float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st) {
+    const int n_tiles = (N + 128 * TN - 1) / (128 * TN), m_tiles = (M + 63) / 64;
+    const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
+    const int chunks = dot_chunks(K), passes = ws ? chunks : 1;
+    const int sb = K / 256, sb_last = sb - (chunks - 1) * (DFX_DOT_CHUNK / 256);
+    if ((2 * sb_last) % DEPTH || (chunks > 1 && (2 * (DFX_DOT_CHUNK / 256)) % DEPTH)) {
+        dfx_set_error("dfx_gemm q4_k: K=%d does not fit the pipeline depth %d", K, DEPTH);
+        return DFX_ERR_ARG;
+    }
+    hipLaunchKernelGGL((k_q4k_w<TN, DEPTH>), dim3((unsigned)(per_pass * passes)), dim3(256), 0, st, (const uint8_t *)w, N,
+                       K, (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles, ws);
+    DFX_CHECK_LAUNCH("dfx_gemm q4_k");
+    if (ws) {
+        const int64_t MN = (int64_t)M * N;
+        const int64_t blocks = std::min<int64_t>((MN + 255) / 256, 8192);
+        hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)blocks), dim3(256), 0, st, (const float *)ws, chunks, MN, N,
+                           bias, res, y, ldy, ymap);
+        DFX_CHECK_LAUNCH("dfx_gemm q4_k reduce");
+    }
+    return DFX_OK;
+}
+
 template <int TM, int TN, int D>
 static int launch_q6k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                       float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st) {
@@ -1075,15 +1401,24 @@ static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, c
     const int chunks = dot_chunks(K);
     const int64_t tiles = (int64_t)((M + 32 * tm - 1) / (32 * tm)) * ((N + 128 * tn - 1) / (128 * tn));
     bool split = chunks > 1 && tiles * 4 < 1024 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
+    int d = 2;
     if (const char * f = getenv("DFX_Q6K_TILE")) {
-        int a = 0, b = 0;
-        if (sscanf(f, "%dx%d", &a, &b) == 2 && ((a == 1 || a == 2) && b == 1)) { tm = a; tn = b; }
+        int a = 0, b = 0, c = 0;
+        const int got = sscanf(f, "%dx%dx%d", &a, &b, &c);
+        if (got >= 2 && ((a == 1 || a == 2) && b == 1)) { tm = a; tn = b; }
+        if (got == 3 && (c == 2 || c == 4)) d = c;
         if (strchr(f, 's')) split = chunks > 1 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
         if (strchr(f, 'n')) split = false;
     }
+    // a 4-deep ring needs a multiple of 4 K steps in every workgroup
+    const int sb = K / 256, sb_last = sb - (chunks - 1) * (DFX_DOT_CHUNK / 256);
+    if (sb_last % 2) d = 2;
     float * wsf = split ? (float *)ws : nullptr;
-    if (tm == 2) return launch_q6k<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st);
-    return launch_q6k<1, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st);
+    if (tm == 2)
+        return d == 4 ? launch_q6k<2, 1, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st)
+                      : launch_q6k<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st);
+    return d == 4 ? launch_q6k<1, 1, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st)
+                  : launch_q6k<1, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st);
 }
 
 // Tile of the Q4_K kernel (TM x TN 32x32 tiles per wave, D = K steps in flight).
@@ -1093,8 +1428,8 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
                         float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st) {
     struct cand { int tm, tn, d; };
     static const cand cands[] = {{2, 2, 2}, {4, 1, 2}, {3, 1, 2}, {2, 1, 2}, {1, 2, 2}, {1, 1, 4},
-                                 {1, 1, 2}};
-    constexpr int n_cand = 7;
+                                 {1, 1, 2}, {2, 1, 4}, {2, 2, 4}};
+    constexpr int n_cand = 9;
     // measured on MI355X for the LLaDA-8B shapes (N 4096..24576, K 4096/12288,
     // M 50..288): 64x128 workgroup tiles with a 2-deep ring win from M ~ 100 up,
     // 32x128 tiles with a 4-deep ring below
@@ -1119,6 +1454,13 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
     }
     // a 4-deep ring needs a multiple of 4 K steps in every workgroup
     const int sb = K / 256, sb_last = sb - (chunks - 1) * (DFX_DOT_CHUNK / 256);
+    if (const char * f = getenv("DFX_Q4K_TILE"); f && strchr(f, 'w')) {
+        // "w": 64 x 64 per wave; "w1": 64 x 32 per wave, two workgroups per CU
+        float * wsw = split ? (float *)ws : nullptr;
+        if (strstr(f, "w1")) return launch_q4k_w<1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st);
+        if (sb_last % 2) return launch_q4k_w<2, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st);
+        return launch_q4k_w<2, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st);
+    }
     if (cands[pick].d == 4 && (sb_last % 2))
         for (int c = 0; c < n_cand; c++)
             if (cands[c].tm == cands[pick].tm && cands[c].tn == cands[pick].tn && cands[c].d == 2) { pick = c; break; }
@@ -1127,7 +1469,7 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
     case c: return launch_q4k<TM_, TN_, D_>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st);
     switch (pick) {
         Q4K_CASE(0, 2, 2, 2) Q4K_CASE(1, 4, 1, 2) Q4K_CASE(2, 3, 1, 2) Q4K_CASE(3, 2, 1, 2) Q4K_CASE(4, 1, 2, 2)
-        Q4K_CASE(5, 1, 1, 4)
+        Q4K_CASE(5, 1, 1, 4) Q4K_CASE(7, 2, 1, 4) Q4K_CASE(8, 2, 2, 4)
         default: return launch_q4k<1, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st);
     }
 #undef Q4K_CASE

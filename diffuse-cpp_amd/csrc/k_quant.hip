@@ -126,14 +126,15 @@ __device__ __forceinline__ void convert_block256(const float v[4], int lane, int
             // elements 4L..4L+3 of a 64-group (L = lane % 16) go to slots 8(L%8) + 4(L/8) + {0,2,1,3}
             const int L = lane & 15;
             const uint16_t p[4] = {o[0], o[2], o[1], o[3]};
-            store_q4((uint16_t *)(act + Lay.q) + m * K + b * 256 + 64 * (lane >> 4) + 8 * (L & 7) + 4 * (L >> 3), p);
+            const int64_t sl = b * 256 + 64 * (lane >> 4) + 8 * (L & 7) + 4 * (L >> 3);
+            store_q4((uint16_t *)(act + Lay.q) + act_frag_off(m, sl, K), p);
         } else if (mode == CONV_Q8_K_P6) {
             // elements 4L..4L+3 (L = lane): half h = L/32, quarter q = (L/8)%4, l = 4(L%8);
             // slot 64g + 8(i + 4(q%2)) + 4(q/2) + {0,2,1,3} with g = l/16, i = (l%16)/4
             const int h = lane >> 5, q = (lane >> 3) & 3, l = 4 * (lane & 7), g = l >> 4, i = (l & 15) >> 2;
             const uint16_t p[4] = {o[0], o[2], o[1], o[3]};
-            store_q4((uint16_t *)(act + Lay.q) + m * K + b * 256 + 128 * h + 64 * g + 8 * (i + 4 * (q & 1)) +
-                         4 * (q >> 1), p);
+            const int64_t sl = b * 256 + 128 * h + 64 * g + 8 * (i + 4 * (q & 1)) + 4 * (q >> 1);
+            store_q4((uint16_t *)(act + Lay.q) + act_frag_off(m, sl, K), p);
         } else {
             store_q4(q, o);
         }
@@ -141,7 +142,7 @@ __device__ __forceinline__ void convert_block256(const float v[4], int lane, int
         s += __shfl_xor(s, 1, WAVE);
         s += __shfl_xor(s, 2, WAVE);
         if ((lane & 3) == 0) ((uint16_t *)(act + Lay.bs))[m * (K / 16) + b * 16 + (lane >> 2)] = f2h((float)s);
-        if (lane == 0) ((float *)(act + Lay.d))[m * (K / 256) + b] = d;
+        if (lane == 0) ((float *)(act + Lay.d))[conv_is_frag(mode) ? b * Lay.mq + m : m * (K / 256) + b] = d;
     } else if (mode == CONV_Q8_0) {
         // GGML quantize_row_q8_0_ref over 32-element blocks (8 lanes each):
         // d = amax/127, q = roundf(x * (1/d)), stored d rounded to f16.

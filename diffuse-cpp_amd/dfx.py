@@ -218,6 +218,17 @@ def q6k_slot_order():
     return order
 
 
+def act_frag_index(M, K):
+    """Half index of (row m, slot sl) in the fragment-ordered q of Q4_K / Q6_K
+    activation buffers: sl = 128*step + 64*hl + 8*kk + j goes to
+    (((m/32) * (K/128) + step) * 8 + kk) * 512 + (m%32 + 32*hl) * 8 + j."""
+    m = np.arange(M, dtype=np.int64)[:, None]
+    sl = np.arange(K, dtype=np.int64)[None, :]
+    step, w = sl >> 7, sl & 127
+    hl, kk, j = w >> 6, (w >> 3) & 7, w & 7
+    return ((((m >> 5) * (K >> 7) + step) * 8 + kk) * 64 + (m & 31) + 32 * hl) * 8 + j
+
+
 def act_parts(act_buf, wtype, M, K):
     """Split a downloaded activation buffer (layout of dfx_act_bytes) into (q, d, bs);
     q is returned in element order."""
@@ -225,21 +236,29 @@ def act_parts(act_buf, wtype, M, K):
 
     def a256(x):
         return (x + 255) // 256 * 256
-    q = raw[:M * K * 2].view(np.float16).reshape(M, K)
+    m_q = (M + 31) // 32 * 32 if wtype in (TYPE_Q4_K, TYPE_Q6_K) else M
     if wtype in (TYPE_Q4_K, TYPE_Q6_K):
+        allq = raw[:m_q * K * 2].view(np.float16)
+        stored = allq[act_frag_index(M, K)]             # [M][K] in slot order
         g = 64 if wtype == TYPE_Q4_K else 128
-        stored = q.reshape(M, K // g, g)
+        stored = stored.reshape(M, K // g, g)
         q = np.empty_like(stored)
         q[:, :, q4k_slot_order() if wtype == TYPE_Q4_K else q6k_slot_order()] = stored
         q = q.reshape(M, K)
-    d_off = a256(M * K * 2)
+    else:
+        q = raw[:M * K * 2].view(np.float16).reshape(M, K)
+    d_off = a256(m_q * K * 2)
     if wtype in (TYPE_Q4_K, TYPE_Q6_K):
         nd, nbs = M * (K // 256), M * (K // 16)
     elif wtype == TYPE_Q8_0:
         nd, nbs = M * (K // 32), 0
     else:
         return q, None, None
-    d = raw[d_off:d_off + nd * 4].view(np.float32).reshape(M, -1)
+    if wtype in (TYPE_Q4_K, TYPE_Q6_K):   # super-block major over the padded rows
+        d = raw[d_off:d_off + (K // 256) * m_q * 4].view(np.float32).reshape(K // 256, m_q)[:, :M].T.copy()
+        nd = (K // 256) * m_q
+    else:
+        d = raw[d_off:d_off + nd * 4].view(np.float32).reshape(M, -1)
     bs_off = a256(d_off + nd * 4)
     bs = raw[bs_off:bs_off + nbs * 2].view(np.float16).reshape(M, -1) if nbs else None
     return q, d, bs

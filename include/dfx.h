@@ -92,7 +92,10 @@ int dfx_embed(int type, const void * table, int64_t n_embd, const int32_t * toke
  *   q   f16 [M][K]      int8 quants as exact f16 integers (F16: the f16 values)
  *   d   f32 [M][K/blk]  block scales (Q8_K: blk 256; Q8_0: blk 32, the f16 scale)
  *   bs  f16 [M][K/16]   Q8_K only: sums of q over 16 elements
- * each part starting at a 256-byte boundary, in this order. */
+ * each part starting at a 256-byte boundary, in this order.  For Q4_K and Q6_K
+ * weights q holds ceil(M/32)*32 rows in the GEMM's matrix-core operand order: each
+ * 128-element K step of a 32-row tile is 8 KB of consecutive memory (the order is
+ * spelled out next to act_frag_off in the library's device header). */
 size_t dfx_act_bytes(int wtype, int64_t M, int64_t K);
 int dfx_act_convert(int wtype, const float * x, int64_t M, int64_t K, void * act, void * stream);
 
