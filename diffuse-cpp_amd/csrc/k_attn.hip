@@ -12,45 +12,83 @@
 
 #include <algorithm>
 
-// One workgroup per (32-row tile, head of Q|K|V).  Q and K heads: one rotation pair
-// (i, i + hd/2) per thread, coalesced along i.  V heads: the tile passes through LDS
-// so that the transposed store vt[kvh][dim][p] takes consecutive positions from
-// consecutive lanes.
+// One workgroup per (32-row tile, head of Q|K|V), head size HD.  Q and K heads: wave
+// w rotates rows w, w+4, .., w+28 of the tile, lane i the pairs (i, i + HD/2) (HD/2
+// pairs split over the wave's lanes); all rows' loads are issued before any
+// arithmetic.  V heads: the tile passes through LDS so that the transposed store
+// vt[kvh][dim][p] takes consecutive positions from consecutive lanes.
 #define ROPE_RT 32
+template <int HD>
 __global__ void __launch_bounds__(256) k_rope_store(const float * __restrict__ qkv, const int32_t * __restrict__ pos,
-                                                    int M, int H, int Hkv, int hd, const float * __restrict__ tab,
+                                                    int M, int H, int Hkv, const float * __restrict__ tab,
                                                     float * __restrict__ q_out, float * __restrict__ kc,
                                                     float * __restrict__ vt, int64_t v_ld) {
 #pragma clang fp contract(off)
-    extern __shared__ float vtile[];   // V heads: [ROPE_RT][hd + 1]
-    const int half = hd / 2, heads = H + 2 * Hkv;
+    constexpr int HALF = HD / 2, PPL = (HALF + 63) / 64;   // pairs per lane
+    constexpr int RPW = ROPE_RT / 4;                        // rows per wave
+    __shared__ float vtile[ROPE_RT * (HD + 1)];
+    const int heads = H + 2 * Hkv;
     const int hh = blockIdx.y, m0 = blockIdx.x * ROPE_RT;
     const int rows = min(ROPE_RT, M - m0);
-    const int64_t ld = (int64_t)heads * hd;
+    const int64_t ld = (int64_t)heads * HD;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     if (hh < H + Hkv) {
-        for (int e = threadIdx.x; e < rows * half; e += blockDim.x) {
-            const int r = e / half, i = e - r * half, m = m0 + r;
-            const float * src = qkv + m * ld + (int64_t)hh * hd;
-            const int p = pos[m];
-            const float x0 = src[i], x1 = src[i + half];
-            // ggml_rope_ext NEOX: rotate (i, i + n_dims/2) by theta_i(p)
-            const float2 cs = *(const float2 *)(tab + ((int64_t)p * half + i) * 2);
-            const float y0 = x0 * cs.x - x1 * cs.y;
-            const float y1 = x0 * cs.y + x1 * cs.x;
-            float * dst = hh < H ? q_out + ((int64_t)m * H + hh) * hd : kc + ((int64_t)p * Hkv + (hh - H)) * hd;
-            dst[i] = y0;
-            dst[i + half] = y1;
+        int p[RPW];
+        float x0[RPW][PPL], x1[RPW][PPL];
+        float2 cs[RPW][PPL];
+#pragma unroll
+        for (int r = 0; r < RPW; r++) {
+            const int m = m0 + min(wv + 4 * r, rows - 1);    // clamped: duplicates are not stored
+            p[r] = pos[m];
+#pragma unroll
+            for (int u = 0; u < PPL; u++) {
+                const int i = min(lane + 64 * u, HALF - 1);
+                const float * src = qkv + m * ld + (int64_t)hh * HD;
+                x0[r][u] = src[i];
+                x1[r][u] = src[i + HALF];
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; r++)
+#pragma unroll
+            for (int u = 0; u < PPL; u++) {
+                const int i = min(lane + 64 * u, HALF - 1);
+                cs[r][u] = *(const float2 *)(tab + ((int64_t)p[r] * HALF + i) * 2);
+            }
+#pragma unroll
+        for (int r = 0; r < RPW; r++) {
+            const int m = m0 + wv + 4 * r;
+            if (wv + 4 * r >= rows) continue;
+#pragma unroll
+            for (int u = 0; u < PPL; u++) {
+                const int i = lane + 64 * u;
+                if (i >= HALF) continue;
+                // ggml_rope_ext NEOX: rotate (i, i + n_dims/2) by theta_i(p)
+                const float y0 = x0[r][u] * cs[r][u].x - x1[r][u] * cs[r][u].y;
+                const float y1 = x0[r][u] * cs[r][u].y + x1[r][u] * cs[r][u].x;
+                float * dst = hh < H ? q_out + ((int64_t)m * H + hh) * HD : kc + ((int64_t)p[r] * Hkv + (hh - H)) * HD;
+                dst[i] = y0;
+                dst[i + HALF] = y1;
+            }
         }
     } else {
-        const int kvh = hh - H - Hkv, ls = hd + 1;
-        for (int e = threadIdx.x; e < rows * hd; e += blockDim.x) {
-            const int r = e / hd, i = e - r * hd;
-            vtile[r * ls + i] = qkv[(int64_t)(m0 + r) * ld + (int64_t)hh * hd + i];
+        const int kvh = hh - H - Hkv;
+        constexpr int LS = HD + 1;
+#pragma unroll
+        for (int k = 0; k < ROPE_RT * HD / 256; k++) {
+            const int e = threadIdx.x + 256 * k, r = e / HD, i = e % HD;
+            if (r < rows) vtile[r * LS + i] = qkv[(int64_t)(m0 + r) * ld + (int64_t)hh * HD + i];
         }
         __syncthreads();
-        for (int e = threadIdx.x; e < hd * ROPE_RT; e += blockDim.x) {
-            const int i = e / ROPE_RT, r = e - i * ROPE_RT;
-            if (r < rows) vt[((int64_t)kvh * hd + i) * v_ld + pos[m0 + r]] = vtile[r * ls + i];
+        // thread -> position r = tid % 32 (fixed), dimensions i = tid / 32 + 8k
+        const int r = threadIdx.x & 31;
+        if (r < rows) {
+            const int p = pos[m0 + r];
+#pragma unroll
+            for (int k = 0; k < HD / 8; k++) {
+                const int i = (threadIdx.x >> 5) + 8 * k;
+                vt[((int64_t)kvh * HD + i) * v_ld + p] = vtile[r * LS + i];
+            }
         }
     }
 }
@@ -304,13 +342,21 @@ extern "C" int dfx_rope_store(const float * qkv, const int32_t * pos, int64_t M,
         return DFX_ERR_ARG;
     }
     if (M == 0) return DFX_OK;
-    if (M > INT32_MAX - ROPE_RT || H + 2 * Hkv > 65535 || hd > 1024) {
+    if (M > INT32_MAX - ROPE_RT || H + 2 * Hkv > 65535) {
         dfx_set_error("dfx_rope_store: shape too large M=%lld heads=%d hd=%d", (long long)M, H + 2 * Hkv, hd);
         return DFX_ERR_ARG;
     }
     const dim3 grid((unsigned)((M + ROPE_RT - 1) / ROPE_RT), (unsigned)(H + 2 * Hkv));
-    hipLaunchKernelGGL(k_rope_store, grid, dim3(256), ROPE_RT * (hd + 1) * sizeof(float), (hipStream_t)stream, qkv,
-                       pos, (int)M, H, Hkv, hd, tab, q_out, kc, vt, v_ld);
+    if (hd == 128)
+        hipLaunchKernelGGL(k_rope_store<128>, grid, dim3(256), 0, (hipStream_t)stream, qkv, pos, (int)M, H, Hkv, tab,
+                           q_out, kc, vt, v_ld);
+    else if (hd == 64)
+        hipLaunchKernelGGL(k_rope_store<64>, grid, dim3(256), 0, (hipStream_t)stream, qkv, pos, (int)M, H, Hkv, tab,
+                           q_out, kc, vt, v_ld);
+    else {
+        dfx_set_error("dfx_rope_store: head size %d (64 or 128 supported)", hd);
+        return DFX_ERR_UNSUPPORTED;
+    }
     DFX_CHECK_LAUNCH("dfx_rope_store");
     return DFX_OK;
 }
