@@ -102,6 +102,17 @@ __global__ void __launch_bounds__(256) k_rope_store(const float * __restrict__ q
 // depend on the summation order.  exp is correctly rounded.
 
 typedef double double4v __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte load at an always valid address; `keep` false gives zeros.  Written without
+// a branch around the load: a conditional load compiles to four predicated dword loads
+// under their own branches, each waited for on its own.
+__device__ __forceinline__ float4 ld4_or0(const float * p, bool keep) {
+    const f32x4 v = *(const f32x4 *)p;
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    const f32x4 r = keep ? v : z;
+    return make_float4(r.x, r.y, r.z, r.w);
+}
 
 // v_mfma_f64_16x16x4f64: D[16][16] += A[16][4] B[4][16].
 // Lane l supplies A[l%16][l/16] and B[l/16][l%16]; it holds D[l/16 + 4i][l%16], i < 4.
@@ -138,7 +149,6 @@ __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q,
     const int64_t kvstride = (int64_t)Hkv * HD;
     const float scale = 1.0f / sqrtf((float)HD);
     const int ntiles = (n_keys + 15) >> 4;
-    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
 
     // ---- phase 1
     float4 qf[SS];
@@ -146,23 +156,23 @@ __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q,
         const int row = q0 + li;
         const float * qr = q + ((int64_t)min(row, M - 1) * H + h) * HD + 4 * lg;
 #pragma unroll
-        for (int s = 0; s < SS; s++) qf[s] = (row < M) ? *(const float4 *)(qr + 16 * s) : zero4;
+        for (int s = 0; s < SS; s++) qf[s] = ld4_or0(qr + 16 * s, row < M);
     }
     const float * kbase = kc + (int64_t)kvh * HD + 4 * lg;
     auto load_k = [&](float4 (&kf)[SS], int t) {
         const int n = 16 * t + li;
         const float * kr = kbase + (int64_t)min(n, n_keys - 1) * kvstride;
 #pragma unroll
-        for (int s = 0; s < SS; s++) kf[s] = (n < n_keys) ? *(const float4 *)(kr + 16 * s) : zero4;
+        for (int s = 0; s < SS; s++) kf[s] = ld4_or0(kr + 16 * s, n < n_keys);
     };
-    float4 kcur[SS], knext[SS];
-    if (wv < ntiles) load_k(kcur, wv);
-    for (int t = wv; t < ntiles; t += 4) {
-        if (t + 4 < ntiles) load_k(knext, t + 4);
+    // key tiles t = wv + 4j in a three-slot register ring, two tiles in flight ahead
+    // of the one being multiplied (slot roles fixed by unrolling, so no copies)
+    float4 kr[3][SS];
+    auto tile = [&](float4 (&kf)[SS], int t) __attribute__((always_inline)) {
         double4v a[4] = {0.0, 0.0, 0.0, 0.0};      // four independent chains: MFMA c of each step
 #pragma unroll
         for (int s = 0; s < SS; s++) {
-            const float kb[4] = {kcur[s].x, kcur[s].y, kcur[s].z, kcur[s].w};
+            const float kb[4] = {kf[s].x, kf[s].y, kf[s].z, kf[s].w};
             const float qa[4] = {qf[s].x, qf[s].y, qf[s].z, qf[s].w};
 #pragma unroll
             for (int c = 0; c < 4; c++) a[c] = mfma_f64((double)qa[c], (double)kb[c], a[c]);
@@ -170,8 +180,19 @@ __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q,
         const double4v acc = (a[0] + a[1]) + (a[2] + a[3]);
 #pragma unroll
         for (int i = 0; i < 4; i++) S[(lg + 4 * i) * sstride + 16 * t + li] = (float)acc[i] * scale;
+    };
 #pragma unroll
-        for (int s = 0; s < SS; s++) kcur[s] = knext[s];
+    for (int u = 0; u < 3; u++)
+        if (wv + 4 * u < ntiles) load_k(kr[u], wv + 4 * u);
+    for (int t0 = wv; t0 < ntiles; t0 += 12) {
+#pragma unroll
+        for (int u = 0; u < 3; u++) {
+            const int t = t0 + 4 * u;
+            if (t < ntiles) {
+                tile(kr[u], t);
+                if (t + 12 < ntiles) load_k(kr[u], t + 12);
+            }
+        }
     }
     __syncthreads();
 
@@ -205,16 +226,14 @@ __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q,
 #pragma unroll
         for (int ct = 0; ct < CT; ct++) {
             const float * p = vb + (int64_t)64 * ct * v_ld + 16 * min(s, ntiles - 1);
-            // v_ld and n are multiples of 4 and n_keys <= v_ld: the load stays in the row
-            vf[ct] = (n < n_keys) ? *(const float4 *)p : zero4;
-            if (n + 4 > n_keys) {        // keys past the end of the sequence count as 0
-                if (n + 1 >= n_keys) vf[ct].y = 0.0f;
-                if (n + 2 >= n_keys) vf[ct].z = 0.0f;
-                if (n + 3 >= n_keys) vf[ct].w = 0.0f;
-            }
+            // v_ld and n are multiples of 4 and n_keys <= v_ld: the load stays in the row;
+            // keys past the end of the sequence count as 0
+            const f32x4 v = *(const f32x4 *)p;
+            vf[ct] = make_float4(n < n_keys ? v.x : 0.0f, n + 1 < n_keys ? v.y : 0.0f, n + 2 < n_keys ? v.z : 0.0f,
+                                 n + 3 < n_keys ? v.w : 0.0f);
         }
     };
-    constexpr int PV = 2;                           // value steps in flight
+    constexpr int PV = 4;                           // value steps in flight
     float4 vq[PV][CT];
 #pragma unroll
     for (int u = 0; u < PV; u++) load_v(vq[u], u);

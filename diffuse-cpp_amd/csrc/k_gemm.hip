@@ -134,12 +134,50 @@ __device__ __forceinline__ half8 to_half8(const int v[8]) {
 // Row of register r of a 32x32 MFMA tile held by `lane` (its column is lane % 32).
 __device__ __forceinline__ int tile_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
-__device__ __forceinline__ void epilogue_store(float v, int m, int n, const float * bias, const float * res, float * Y,
-                                               int64_t ldy, const int32_t * ymap) {
-    const int64_t o = (int64_t)(ymap ? ymap[m] : m) * ldy + n;
-    if (bias) v = v + bias[n];
-    if (res) v = v + res[o];
-    Y[o] = v;
+// Epilogue of one 32x32 MFMA tile held by `lane`: register r is row m0 + tile_row(r, lane),
+// column n.  Every read (row map, bias, residual) is issued before any is used, at clamped
+// (always valid) addresses, so the wave waits once per kind of read rather than once per
+// element; rows >= M and columns >= N are not stored.  With ws (split K) the tile's chunk
+// sum goes to ws[z][m][n] instead.  y = (v + bias) + residual, written to Y[ymap[m] * ldy + n]
+// (Y[m * ldy + n] without a row map).
+template <typename V16>
+__device__ __forceinline__ void epilogue_tile(const V16 & acc, int m0, int n, int M, int N, const float * bias,
+                                              const float * res, float * Y, int64_t ldy, const int32_t * ymap,
+                                              float * ws, int z, int lane) {
+    if (ws) {
+        if (n < N)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + tile_row(r, lane);
+                if (m < M) ws[((int64_t)z * M + m) * N + n] = acc[r];
+            }
+        return;
+    }
+    const int nc = min(n, N - 1);
+    int64_t o[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int m = min(m0 + tile_row(r, lane), M - 1);
+        o[r] = (int64_t)(ymap ? ymap[m] : m) * ldy + nc;
+    }
+    float rv[16];
+    if (res)
+#pragma unroll
+        for (int r = 0; r < 16; r++) rv[r] = res[o[r]];
+    const float b = bias ? bias[nc] : 0.0f;
+    // All sums are formed before the first store: a sum sunk into its store's branch would make
+    // each store wait for the one before it to complete.
+    float v[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        v[r] = acc[r];
+        if (bias) v[r] = v[r] + b;
+        if (res) v[r] = v[r] + rv[r];
+        asm volatile("" : "+v"(v[r]));
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++)
+        if (n < N && m0 + tile_row(r, lane) < M) Y[o[r]] = v[r];
 }
 
 // ---------------------------------------------------------------------------
@@ -338,16 +376,8 @@ k_mmq(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
     }
 
     const int n = n0 + wn * 32 + (lane & 31);
-    if (n >= N) return;
 #pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int m = m0 + i * 32 + tile_row(r, lane);
-            if (m >= M) continue;
-            const float v = T1[i][r];
-            epilogue_store(v, m, n, bias, res, Y, ldy, ymap);
-        }
+    for (int i = 0; i < TM; i++) epilogue_tile(T1[i], m0 + i * 32, n, M, N, bias, res, Y, ldy, ymap, nullptr, 0, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -654,19 +684,11 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
 
     // split K: the chunk sum goes to ws[z][m][n]; the reduction adds the chunks in order
 #pragma unroll
-    for (int t = 0; t < TN; t++) {
-        const int n = n0 + (wv * TN + t) * 32 + l32;
-        if (n >= N) continue;
+    for (int t = 0; t < TN; t++)
 #pragma unroll
         for (int i = 0; i < TM; i++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + i * 32 + tile_row(r, lane);
-                if (m >= M) continue;
-                if (ws) ws[((int64_t)z * M + m) * N + n] = T[i][t][r];
-                else epilogue_store(T[i][t][r], m, n, bias, res, Y, ldy, ymap);
-            }
-    }
+            epilogue_tile(T[i][t], m0 + i * 32, n0 + (wv * TN + t) * 32 + l32, M, N, bias, res, Y, ldy, ymap, ws, z,
+                          lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -937,19 +959,11 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
     __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm(0, 0));
 
 #pragma unroll
-    for (int t = 0; t < TN; t++) {
-        const int n = n0 + (wv * TN + t) * 32 + l32;
-        if (n >= N) continue;
+    for (int t = 0; t < TN; t++)
 #pragma unroll
         for (int i = 0; i < TM; i++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + i * 32 + tile_row(r, lane);
-                if (m >= M) continue;
-                if (ws) ws[((int64_t)z * M + m) * N + n] = T[i][t][r];
-                else epilogue_store(T[i][t][r], m, n, bias, res, Y, ldy, ymap);
-            }
-    }
+            epilogue_tile(T[i][t], m0 + i * 32, n0 + (wv * TN + t) * 32 + l32, M, N, bias, res, Y, ldy, ymap, ws, z,
+                          lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -1185,19 +1199,11 @@ k_q6k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
     }
 
 #pragma unroll
-    for (int t = 0; t < TN; t++) {
-        const int n = n0 + (wv * TN + t) * 32 + l32;
-        if (n >= N) continue;
+    for (int t = 0; t < TN; t++)
 #pragma unroll
         for (int i = 0; i < TM; i++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + i * 32 + tile_row(r, lane);
-                if (m >= M) continue;
-                if (ws) ws[((int64_t)z * M + m) * N + n] = T[i][t][r];
-                else epilogue_store(T[i][t][r], m, n, bias, res, Y, ldy, ymap);
-            }
-    }
+            epilogue_tile(T[i][t], m0 + i * 32, n0 + (wv * TN + t) * 32 + l32, M, N, bias, res, Y, ldy, ymap, ws, z,
+                          lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -1243,27 +1249,59 @@ k_gemm_f16(const uint8_t * __restrict__ W, int N, int K, const half_t * __restri
     }
     const bool split = gridDim.z > 1;
     const int n = n0 + wn * 32 + (lane & 31);
-    if (n >= N) return;
 #pragma unroll
     for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int m = m0 + i * 32 + tile_row(r, lane);
-            if (m >= M) continue;
-            if (split) ws[((int64_t)blockIdx.z * M + m) * N + n] = acc[i][r];
-            else epilogue_store(acc[i][r], m, n, bias, res, Y, ldy, ymap);
-        }
+        epilogue_tile(acc[i], m0 + i * 32, n, M, N, bias, res, Y, ldy, ymap, split ? ws : nullptr, (int)blockIdx.z,
+                      lane);
 }
 
-// Fixed-order reduction of split-K partials plus epilogue.
+// Fixed-order reduction of split-K partials plus epilogue: y = ((0 + p_0) + p_1 ...) + bias + res.
+// Each thread takes REDUCE_R elements spaced one grid apart, so the partial loads of one chunk,
+// the row-map reads and the residual reads are each issued as one batch at clamped (valid)
+// addresses; elements past MN are not stored.
+#define REDUCE_R 4
 __global__ void k_gemm_reduce(const float * __restrict__ ws, int S, int64_t MN, int N, const float * bias,
                               const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap) {
-    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < MN;
-         idx += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t m = idx / N, n = idx - m * N;
-        float v = 0.0f;
-        for (int s = 0; s < S; s++) v = v + ws[(int64_t)s * MN + idx];
-        epilogue_store(v, (int)m, (int)n, bias, res, Y, ldy, ymap);
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i0 < MN; i0 += REDUCE_R * stride) {
+        int64_t idx[REDUCE_R];
+        float v[REDUCE_R];
+#pragma unroll
+        for (int j = 0; j < REDUCE_R; j++) {
+            idx[j] = min(i0 + j * stride, MN - 1);
+            v[j] = 0.0f;
+        }
+        for (int s = 0; s < S; s++) {
+            float p[REDUCE_R];
+#pragma unroll
+            for (int j = 0; j < REDUCE_R; j++) p[j] = ws[(int64_t)s * MN + idx[j]];
+#pragma unroll
+            for (int j = 0; j < REDUCE_R; j++) v[j] = v[j] + p[j];
+        }
+        int64_t o[REDUCE_R];
+        int n[REDUCE_R];
+#pragma unroll
+        for (int j = 0; j < REDUCE_R; j++) {
+            const int64_t m = idx[j] / N;
+            n[j] = (int)(idx[j] - m * N);
+            o[j] = (int64_t)(ymap ? ymap[m] : m) * ldy + n[j];
+        }
+        float b[REDUCE_R], rv[REDUCE_R];
+        if (bias)
+#pragma unroll
+            for (int j = 0; j < REDUCE_R; j++) b[j] = bias[n[j]];
+        if (res)
+#pragma unroll
+            for (int j = 0; j < REDUCE_R; j++) rv[j] = res[o[j]];
+#pragma unroll
+        for (int j = 0; j < REDUCE_R; j++) {
+            if (bias) v[j] = v[j] + b[j];
+            if (res) v[j] = v[j] + rv[j];
+            asm volatile("" : "+v"(v[j]));
+        }
+#pragma unroll
+        for (int j = 0; j < REDUCE_R; j++)
+            if (i0 + j * stride < MN) Y[o[j]] = v[j];
     }
 }
 
@@ -1297,7 +1335,7 @@ static int launch_f16(const void * w, int N, int K, const void * act, int M, con
     DFX_CHECK_LAUNCH("dfx_gemm f16");
     if (S > 1) {
         const int64_t MN = (int64_t)M * N;
-        const int64_t blocks = std::min<int64_t>((MN + 255) / 256, 8192);
+        const int64_t blocks = std::min<int64_t>((MN + 256 * REDUCE_R - 1) / (256 * REDUCE_R), 8192);
         hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)blocks), dim3(256), 0, st, (const float *)ws, S, MN, N,
                            bias, res, y, ldy, ymap);
         DFX_CHECK_LAUNCH("dfx_gemm reduce");
@@ -1336,7 +1374,7 @@ static int launch_q4k(const void * w, int N, int K, const void * act, int M, con
     DFX_CHECK_LAUNCH("dfx_gemm q4_k");
     if (ws) {
         const int64_t MN = (int64_t)M * N;
-        const int64_t blocks = std::min<int64_t>((MN + 255) / 256, 8192);
+        const int64_t blocks = std::min<int64_t>((MN + 256 * REDUCE_R - 1) / (256 * REDUCE_R), 8192);
         hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)blocks), dim3(256), 0, st, (const float *)ws, chunks, MN, N,
                            bias, res, y, ldy, ymap);
         DFX_CHECK_LAUNCH("dfx_gemm q4_k reduce");
@@ -1360,7 +1398,7 @@ static int launch_q4k_w(const void * w, int N, int K, const void * act, int M, c
     DFX_CHECK_LAUNCH("dfx_gemm q4_k");
     if (ws) {
         const int64_t MN = (int64_t)M * N;
-        const int64_t blocks = std::min<int64_t>((MN + 255) / 256, 8192);
+        const int64_t blocks = std::min<int64_t>((MN + 256 * REDUCE_R - 1) / (256 * REDUCE_R), 8192);
         hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)blocks), dim3(256), 0, st, (const float *)ws, chunks, MN, N,
                            bias, res, y, ldy, ymap);
         DFX_CHECK_LAUNCH("dfx_gemm q4_k reduce");
@@ -1385,7 +1423,7 @@ static int launch_q6k(const void * w, int N, int K, const void * act, int M, con
     DFX_CHECK_LAUNCH("dfx_gemm q6_k");
     if (ws) {
         const int64_t MN = (int64_t)M * N;
-        const int64_t blocks = std::min<int64_t>((MN + 255) / 256, 8192);
+        const int64_t blocks = std::min<int64_t>((MN + 256 * REDUCE_R - 1) / (256 * REDUCE_R), 8192);
         hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)blocks), dim3(256), 0, st, (const float *)ws, chunks, MN, N,
                            bias, res, y, ldy, ymap);
         DFX_CHECK_LAUNCH("dfx_gemm q6_k reduce");
