@@ -1469,9 +1469,11 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
                                  {1, 1, 2}, {2, 1, 4}, {2, 2, 4}};
     constexpr int n_cand = 9;
     // measured on MI355X for the LLaDA-8B shapes (N 4096..24576, K 4096/12288,
-    // M 50..288): 64x128 workgroup tiles with a 2-deep ring win from M ~ 100 up,
-    // 32x128 tiles with a 4-deep ring below
+    // M 50..288): 64x128 workgroup tiles win from M ~ 100 up, 32x128 tiles with a
+    // 4-deep register ring below.  Of the 64x128 kernels, the one fed by LDS DMA
+    // (k_q4k_w<1, 2>) beats the register-ring one by 0-4% at those shapes.
     int pick = M > 96 ? 3 : 5;
+    bool dma = M > 96;
     const int chunks = dot_chunks(K);
     int64_t tiles;
     {
@@ -1484,9 +1486,11 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
     if (const char * f = getenv("DFX_Q4K_TILE")) {
         int tm = 0, tn = 0, d = 0;
         const int got = sscanf(f, "%dx%dx%d", &tm, &tn, &d);
-        if (got >= 2)
+        if (got >= 2) {
+            dma = false;
             for (int c = n_cand - 1; c >= 0; c--)
                 if (cands[c].tm == tm && cands[c].tn == tn && (got < 3 || cands[c].d == d)) pick = c;
+        }
         if (strchr(f, 's')) split = chunks > 1 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
         if (strchr(f, 'n')) split = false;
     }
@@ -1499,6 +1503,7 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
         if (sb_last % 2) return launch_q4k_w<2, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st);
         return launch_q4k_w<2, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st);
     }
+    if (dma) return launch_q4k_w<1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, split ? (float *)ws : nullptr, st);
     if (cands[pick].d == 4 && (sb_last % 2))
         for (int c = 0; c < n_cand; c++)
             if (cands[c].tm == cands[pick].tm && cands[c].tn == cands[pick].tn && cands[c].d == 2) { pick = c; break; }

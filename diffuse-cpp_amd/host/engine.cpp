@@ -46,15 +46,16 @@ struct dims {
 
 void free_buffers(diffuse_context * c) {
     void * bufs[] = {c->x, c->act, c->qkv, c->qr, c->att, c->gu, c->logits, c->kc, c->vc, c->rope_tab,
-                     c->d_tok, c->d_pos, c->d_hrows, c->d_hmap, c->d_srows, c->d_spos, c->ws, c->d_stats,
-                     c->d_cand, c->d_order, c->d_nun};
+                     c->d_ints, c->ws, c->d_stats, c->d_out};
     for (void * p : bufs)
         if (p) (void)hipFree(p);
     if (c->h_pin) (void)hipHostFree(c->h_pin);
+    if (c->h_out) (void)hipHostFree(c->h_out);
     c->x = c->qkv = c->qr = c->att = c->gu = c->logits = c->kc = c->vc = c->rope_tab = nullptr;
     c->act = nullptr;
-    c->d_tok = c->d_pos = c->d_hrows = c->d_hmap = c->d_srows = c->d_spos = c->d_order = c->d_nun = nullptr;
-    c->ws = nullptr;
+    c->d_ints = c->d_tok = c->d_pos = c->d_hrows = c->d_hmap = c->d_srows = c->d_spos = c->d_order = c->d_nun = nullptr;
+    c->ws = c->d_out = c->h_out = nullptr;
+    c->out_bytes = 0;
     c->d_stats = nullptr;
     c->d_cand = nullptr;
     c->h_pin = nullptr;
@@ -97,22 +98,26 @@ int ensure_capacity(diffuse_context * c, int N) {
     TRY(A((void **)&c->kc, D.L * n * D.dkv * 4));
     TRY(A((void **)&c->vc, D.L * n * D.dkv * 4));
     TRY(A((void **)&c->rope_tab, n * D.hd * 4));
-    TRY(A((void **)&c->d_tok, n * 4));
-    TRY(A((void **)&c->d_pos, n * 4));
-    TRY(A((void **)&c->d_hrows, n * 4));
-    TRY(A((void **)&c->d_hmap, n * 4));
-    TRY(A((void **)&c->d_srows, n * 4));
-    TRY(A((void **)&c->d_spos, n * 4));
+    TRY(A((void **)&c->d_ints, 6 * n * 4));
+    c->d_tok = c->d_ints;
+    c->d_pos = c->d_ints + n;
+    c->d_hrows = c->d_ints + 2 * n;
+    c->d_hmap = c->d_ints + 3 * n;
+    c->d_srows = c->d_ints + 4 * n;
+    c->d_spos = c->d_ints + 5 * n;
     // split-K workspace for the GEMMs with few output tiles (Q|K|V, O, down); gate|up
     // (N = 2F) always has enough tiles and gets whatever fits
     c->ws_bytes = std::max(std::max(dfx_gemm_ws_bytes(n, D.nqkv, D.d), dfx_gemm_ws_bytes(n, D.d, D.d)),
                            dfx_gemm_ws_bytes(n, D.d, D.F));
     TRY(A(&c->ws, c->ws_bytes));
     TRY(A((void **)&c->d_stats, n * sizeof(dfx_row_stat)));
-    TRY(A((void **)&c->d_cand, n * sizeof(dfx_candidate)));
-    TRY(A((void **)&c->d_order, n * 4));
-    TRY(A((void **)&c->d_nun, 4));
+    c->out_bytes = n * sizeof(dfx_candidate) + n * 4 + 16;
+    TRY(A(&c->d_out, c->out_bytes));
+    c->d_cand = (dfx_candidate *)c->d_out;
+    c->d_order = (int32_t *)(c->d_cand + n);
+    c->d_nun = c->d_order + n;
     TRY(hip_ok(hipHostMalloc((void **)&c->h_pin, n * 8 * 4, hipHostMallocDefault), "hipHostMalloc"));
+    TRY(hip_ok(hipHostMalloc(&c->h_out, c->out_bytes, hipHostMallocDefault), "hipHostMalloc"));
     // caches start at zero like diffuse_step_cache::init (src/diffuse-cache.h:43-49)
     TRY(hip_ok(hipMemsetAsync(c->kc, 0, D.L * n * D.dkv * 4, c->stream), "memset"));
     TRY(hip_ok(hipMemsetAsync(c->vc, 0, D.L * n * D.dkv * 4, c->stream), "memset"));
@@ -223,6 +228,15 @@ int upload_i32(diffuse_context * c, int32_t * dst, const int32_t * src, int n, i
     return hip_ok(hipMemcpyAsync(dst, stage, (size_t)n * 4, hipMemcpyHostToDevice, c->stream), "H2D");
 }
 
+// Stage n values into slot `slot` of h_pin; upload_slots sends slots 0..n_slots-1 to d_ints.
+void stage_i32(diffuse_context * c, const int32_t * src, int n, int slot) {
+    if (n > 0) memcpy(c->h_pin + (size_t)slot * c->cap, src, (size_t)n * 4);
+}
+int upload_slots(diffuse_context * c, int n_slots) {
+    return hip_ok(hipMemcpyAsync(c->d_ints, c->h_pin, (size_t)n_slots * c->cap * 4, hipMemcpyHostToDevice, c->stream),
+                  "H2D");
+}
+
 // src/diffuse-sampler.cpp:12-31 (t * M_PI is a double product narrowed for cosf)
 int tokens_to_unmask(int step, int total_steps, int total_masked, int schedule) {
     const float t0 = (float)step / total_steps;
@@ -255,6 +269,7 @@ int engine_context_new(const diffuse_model * m, int n_ctx, int n_threads, diffus
     int rc = hip_ok(hipStreamCreate(&c->stream), "hipStreamCreate");
     if (rc == DFX_OK) rc = hip_ok(hipEventCreate(&c->ev0), "hipEventCreate");
     if (rc == DFX_OK) rc = hip_ok(hipEventCreate(&c->ev1), "hipEventCreate");
+    if (rc == DFX_OK) rc = hip_ok(hipEventCreate(&c->ev2), "hipEventCreate");
     if (rc == DFX_OK) rc = ensure_capacity(c, std::max(n_ctx, 1));
     if (rc != DFX_OK) {
         engine_context_free(c);
@@ -271,6 +286,7 @@ void engine_context_free(diffuse_context * c) {
     free_buffers(c);
     if (c->ev0) (void)hipEventDestroy(c->ev0);
     if (c->ev1) (void)hipEventDestroy(c->ev1);
+    if (c->ev2) (void)hipEventDestroy(c->ev2);
     for (hipEvent_t e : c->prof_pool) (void)hipEventDestroy(e);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
@@ -414,24 +430,7 @@ int engine_generate(diffuse_context * c, const int32_t * prompt, int n_prompt, i
                 hmap.push_back(act[a]);
             }
         }
-        TRY(upload_i32(c, c->d_tok, tok.data(), M, 0));
-        TRY(upload_i32(c, c->d_pos, act.data(), M, 1));
-        TRY(upload_i32(c, c->d_hrows, hrows.data(), (int)hrows.size(), 2));
-        TRY(upload_i32(c, c->d_hmap, hmap.data(), (int)hmap.size(), 3));
-        TRY(hip_ok(hipEventRecord(c->ev0, c->stream), "event"));
-        TRY(forward_pass(c, M, N, (int)hrows.size()));
-        TRY(hip_ok(hipEventRecord(c->ev1, c->stream), "event"));
-        if (use_cache) {   // update_seq right after the forward (src/diffuse-sampler.cpp:154, 171, 194)
-            prev_seq = seq;
-            cache_init = true;
-        }
-        TRY(hip_ok(hipEventSynchronize(c->ev1), "forward"));
-        const auto t1 = clk::now();
-        const double fwd_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
-        total_fwd += fwd_ms;
-
-        // ---- candidates (src/diffuse-sampler.cpp:222-270) ----
-        const auto t2 = clk::now();
+        // rows the sampler scans: every masked position (its left neighbour's row for Dream)
         srows.clear();
         spos.clear();
         for (int i = 0; i < N; i++)
@@ -440,31 +439,64 @@ int engine_generate(diffuse_context * c, const int32_t * prompt, int n_prompt, i
                 spos.push_back(i);
             }
         const int n_cand = (int)spos.size();
-        TRY(upload_i32(c, c->d_srows, srows.data(), n_cand, 4));
-        TRY(upload_i32(c, c->d_spos, spos.data(), n_cand, 5));
+        // The step's six index arrays go up in one copy; the forward, the row statistics,
+        // candidates and selection are queued behind it, and the host waits once, for the
+        // copy of the selection back.
+        stage_i32(c, tok.data(), M, 0);
+        stage_i32(c, act.data(), M, 1);
+        stage_i32(c, hrows.data(), (int)hrows.size(), 2);
+        stage_i32(c, hmap.data(), (int)hmap.size(), 3);
+        stage_i32(c, srows.data(), n_cand, 4);
+        stage_i32(c, spos.data(), n_cand, 5);
+        const double prep_ms = std::chrono::duration<double, std::milli>(clk::now() - t0).count();
+        TRY(upload_slots(c, 6));
+        TRY(hip_ok(hipEventRecord(c->ev0, c->stream), "event"));
+        TRY(forward_pass(c, M, N, (int)hrows.size()));
+        TRY(hip_ok(hipEventRecord(c->ev1, c->stream), "event"));
+        if (use_cache) {   // update_seq right after the forward (src/diffuse-sampler.cpp:154, 171, 194)
+            prev_seq = seq;
+            cache_init = true;
+        }
+
+        // ---- candidates (src/diffuse-sampler.cpp:222-270) ----
         TRY(dfx_row_stats(c->logits, V, c->d_srows, n_cand, V, c->d_stats, c->stream));
         const int n_sched = tokens_to_unmask(step, p.n_steps, n_masked, p.schedule);
         int n_unmask = n_sched;
         cand.resize(n_cand);
         order.resize(n_cand);
-        if (p.temperature <= 0.0f) {
+        const bool greedy = p.temperature <= 0.0f;
+        if (greedy) {
             TRY(dfx_make_candidates(c->d_stats, c->d_spos, n_cand, p.remasking == 4 ? 1 : 0, c->d_cand, c->stream));
-            if (p.remasking != 1) {
+            if (p.remasking != 1)
                 TRY(dfx_select(c->d_cand, n_cand, p.remasking, p.entropy_threshold, n_sched, c->d_order, c->d_nun,
                                c->stream));
-                TRY(hip_ok(hipMemcpyAsync(order.data(), c->d_order, (size_t)n_cand * 4, hipMemcpyDeviceToHost, c->stream), "D2H"));
-                TRY(hip_ok(hipMemcpyAsync(&n_unmask, c->d_nun, 4, hipMemcpyDeviceToHost, c->stream), "D2H"));
+            TRY(hip_ok(hipEventRecord(c->ev2, c->stream), "event"));
+            TRY(hip_ok(hipMemcpyAsync(c->h_out, c->d_out, c->out_bytes, hipMemcpyDeviceToHost, c->stream), "D2H"));
+        } else {
+            TRY(hip_ok(hipEventRecord(c->ev2, c->stream), "event"));
+        }
+        TRY(hip_ok(hipStreamSynchronize(c->stream), "step"));
+        const auto t2 = clk::now();
+        float gpu_fwd_ms = 0.0f, gpu_smp_ms = 0.0f;
+        TRY(hip_ok(hipEventElapsedTime(&gpu_fwd_ms, c->ev0, c->ev1), "event"));
+        TRY(hip_ok(hipEventElapsedTime(&gpu_smp_ms, c->ev1, c->ev2), "event"));
+        const double fwd_ms = prep_ms + gpu_fwd_ms;
+        total_fwd += fwd_ms;
+        total_sample += gpu_smp_ms;
+        if (greedy) {
+            const auto * hc = (const dfx_candidate *)c->h_out;
+            std::copy(hc, hc + n_cand, cand.begin());
+            if (p.remasking != 1) {
+                const auto * ho = (const int32_t *)(hc + c->cap);
+                std::copy(ho, ho + n_cand, order.begin());
+                n_unmask = ho[c->cap];
             }
-            TRY(hip_ok(hipMemcpyAsync(cand.data(), c->d_cand, (size_t)n_cand * sizeof(dfx_candidate),
-                                      hipMemcpyDeviceToHost, c->stream), "D2H"));
-            TRY(hip_ok(hipStreamSynchronize(c->stream), "sampler"));
         } else {
             // Stochastic path stays on the host like the reference (src/diffuse-sampler.cpp:256-269).
             std::vector<dfx_row_stat> st(n_cand);
             std::vector<float> rowbuf((size_t)V);
-            TRY(hip_ok(hipMemcpyAsync(st.data(), c->d_stats, (size_t)n_cand * sizeof(dfx_row_stat),
-                                      hipMemcpyDeviceToHost, c->stream), "D2H"));
-            TRY(hip_ok(hipStreamSynchronize(c->stream), "sampler"));
+            TRY(hip_ok(hipMemcpy(st.data(), c->d_stats, (size_t)n_cand * sizeof(dfx_row_stat), hipMemcpyDeviceToHost),
+                       "D2H"));
             std::vector<float> probs((size_t)V);
             for (int j = 0; j < n_cand; j++) {
                 TRY(hip_ok(hipMemcpy(rowbuf.data(), c->logits + (size_t)srows[j] * V, (size_t)V * 4,
@@ -482,7 +514,7 @@ int engine_generate(diffuse_context * c, const int32_t * prompt, int n_prompt, i
             }
         }
         const auto t3 = clk::now();
-        total_sample += std::chrono::duration<double, std::milli>(t3 - t2).count();
+        total_sample += std::chrono::duration<double, std::milli>(t3 - t2).count();   // host part
 
         // ---- ordering (src/diffuse-sampler.cpp:277-308) ----
         const auto t4 = clk::now();

@@ -77,20 +77,28 @@ struct diffuse_context {
     float *      kc = nullptr;       // [L][cap][dkv]        inter-step key cache
     float *      vc = nullptr;       // [L][Hkv][hd][cap]    inter-step value cache, transposed
     float *      rope_tab = nullptr; // [cap][hd/2][2]
-    int32_t *    d_tok = nullptr;    // [cap] tokens of this pass
-    int32_t *    d_pos = nullptr;    // [cap] positions of this pass
-    int32_t *    d_hrows = nullptr;  // [cap] pass rows that need logits
-    int32_t *    d_hmap = nullptr;   // [cap] logits row of each of them
-    int32_t *    d_srows = nullptr;  // [cap] logits rows scanned by the sampler
-    int32_t *    d_spos = nullptr;   // [cap] masked position of each scanned row
+    // The six index arrays of a step are slots 0..5 of one allocation d_ints [6][cap],
+    // staged in the same order in h_pin, so one copy uploads them all.
+    int32_t *    d_ints = nullptr;
+    int32_t *    d_tok = nullptr;    // slot 0: tokens of this pass
+    int32_t *    d_pos = nullptr;    // slot 1: positions of this pass
+    int32_t *    d_hrows = nullptr;  // slot 2: pass rows that need logits
+    int32_t *    d_hmap = nullptr;   // slot 3: logits row of each of them
+    int32_t *    d_srows = nullptr;  // slot 4: logits rows scanned by the sampler
+    int32_t *    d_spos = nullptr;   // slot 5: masked position of each scanned row
     void *       ws = nullptr;       // split-K workspace
     size_t       ws_bytes = 0;
     dfx_row_stat *  d_stats = nullptr;
+    // Sampler results, one allocation d_out = [cand: cap][order: cap][n_unmask], read back
+    // with one copy into the pinned h_out.
+    void *       d_out = nullptr;
     dfx_candidate * d_cand = nullptr;
     int32_t *    d_order = nullptr;
     int32_t *    d_nun = nullptr;
+    void *       h_out = nullptr;
+    size_t       out_bytes = 0;
     int32_t *    h_pin = nullptr;    // pinned staging, 8 * cap int32
-    hipEvent_t   ev0 = nullptr, ev1 = nullptr;
+    hipEvent_t   ev0 = nullptr, ev1 = nullptr, ev2 = nullptr;
 
     // Optional per-GEMM timing: a pair of events around every GEMM launch on `stream`.
     struct gemm_rec { hipEvent_t a, b; int type; double flops, bytes; };
