@@ -118,7 +118,19 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 3 device-to-device copies of 512 MiB (reference kernel for the "
+                         "FETCH_SIZE / WRITE_SIZE counter scale) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        n = 512 << 20
+        a, b = dfx.Buf(n), dfx.Buf(n)
+        a.zero()
+        for _ in range(3):
+            dfx.check(dfx.lib().dfx_memcpy_d2d(b.ptr, a.ptr, n, None), "copy")
+        dfx.sync()
+        print(json.dumps({"copy_calibration_bytes": n, "copies": 3}))
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: --gpus {args.gpus} is not supported (the denoising path is "
               f"single-GPU; see the sharding design notes)", file=sys.stderr)
@@ -157,6 +169,8 @@ def main():
     dfx.sync()
     elapsed_prof = time.perf_counter() - t0
     prof = {t: ctx.profile_read(t) for t in (dfx.TYPE_Q4_K, dfx.TYPE_Q6_K)}
+    q4_big = ctx.profile_read(dfx.TYPE_Q4_K, 1)     # M > 96: k_q4k_w<1, 2>, the dominant kernel
+    q4_small = ctx.profile_read(dfx.TYPE_Q4_K, 2)   # M <= 96: k_q4k<1, 1, 4>, HBM-bound shapes
     ctx.profile(False)
 
     steps_done = stats.actual_steps
@@ -164,7 +178,9 @@ def main():
     step_ms = [round(stats.step_ms[i], 3) for i in range(steps_done)]
     ms_per_gen = 1000 * elapsed / args.steps
     q4 = prof[dfx.TYPE_Q4_K]
-    achieved = q4["flops"] / (q4["ms"] * 1e-3) / 1e12 if q4["ms"] > 0 else 0.0
+    achieved = q4_big["flops"] / (q4_big["ms"] * 1e-3) / 1e12 if q4_big["ms"] > 0 else 0.0
+    achieved_all = q4["flops"] / (q4["ms"] * 1e-3) / 1e12 if q4["ms"] > 0 else 0.0
+    small_gbs = q4_small["bytes"] / (q4_small["ms"] * 1e-3) / 1e9 if q4_small["ms"] > 0 else 0.0
 
     # the reference runs the vocab head over every active row; its row counts per step
     masked, head_plan = B, []
@@ -200,17 +216,22 @@ def main():
         "ms_per_denoise_step_cached_mean": round(float(np.mean(step_ms[1:])), 3) if len(step_ms) > 1 else None,
         "step_forward_ms": step_ms,
         "roofline": {
-            "kernel": "k_q4k (exact dequant-fused MFMA GEMM on Q4_K weights, every tile variant, split-K "
-                      "reduction included)",
+            "kernel": "k_q4k_w<1, 2> (exact dequant-fused MFMA GEMM on Q4_K weights, every call over more "
+                      "than 96 rows; split-K reduction included when launched)",
             "bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": committed_traffic(),
             "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
-            "algorithmic_bytes_per_launch": round(q4["bytes"] / max(q4["launches"], 1)),
-            "launches": q4["launches"],
-            "avg_launch_us": round(1000 * q4["ms"] / max(q4["launches"], 1), 3),
-            "flops_per_launch": round(q4["flops"] / max(q4["launches"], 1), 1),
+            "algorithmic_bytes_per_launch": round(q4_big["bytes"] / max(q4_big["launches"], 1)),
+            "launches": q4_big["launches"],
+            "avg_launch_us": round(1000 * q4_big["ms"] / max(q4_big["launches"], 1), 3),
+            "flops_per_launch": round(q4_big["flops"] / max(q4_big["launches"], 1), 1),
             "gemm_share_of_time": round((q4["ms"] + prof[dfx.TYPE_Q6_K]["ms"]) / (1000 * elapsed_prof), 4),
             "events_pass_tok_s": round(B * args.steps / elapsed_prof, 2),
+            "all_q4k_calls_tflops": round(achieved_all, 2),
+            "small_rows": {"kernel": "k_q4k<1, 1, 4> (calls over at most 96 rows)", "bound": "hbm",
+                           "achieved": round(small_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": round(small_gbs / HBM_PEAK_GBS, 4), "launches": q4_small["launches"],
+                           "avg_launch_us": round(1000 * q4_small["ms"] / max(q4_small["launches"], 1), 3)},
         },
         "cpu_baseline": cpu,
     }

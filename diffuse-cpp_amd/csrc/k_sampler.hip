@@ -2,16 +2,20 @@
 //
 // Row statistics restate the reference's per-masked-position scan
 // (src/diffuse-sampler.cpp:34-57 compute_entropy, 241-252 top-1/top-2) as
-// workgroup reductions over a logits row:
-//   pass 1  argmax (strict >, lowest index on ties) and top-2
-//   pass 2  sum of expf(x - max)
-//   pass 3  entropy = -sum p*log_p over p = expf((x - max) - logf(sum)) > 1e-10
-// Rows are read three times; passes 2 and 3 hit the caches behind HBM.
+// workgroup reductions over a logits row, in two reads of the row:
+//   pass 1  argmax (strict >, lowest index on ties), top-2, and sum = sum of exp(x - max),
+//           each thread keeping its sum relative to its own running maximum (rescaled when
+//           that maximum grows) until the row maximum is known
+//   pass 2  entropy = -sum p*log_p over p = exp((x - max) - log(sum)) > 1e-10
+// The top-2 values are exact.  exp is the transcendental unit's 2^(x log2 e) (about 1 ulp);
+// per-thread partial sums are float, the sums across threads double.  The reference adds
+// 126464 floats one after another, so its own sum carries a larger rounding error.
 #include "dfx_device.h"
 
 #include <algorithm>
 
 #define RS_THREADS 1024
+#define RS_UNROLL 4
 
 struct top2_t { float best; int idx; float second; };
 
@@ -33,6 +37,14 @@ __device__ __forceinline__ top2_t top2_shfl(top2_t v, int off) {
     return o;
 }
 
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
+// running top-2 of one element (elements arrive in increasing index order per thread)
+__device__ __forceinline__ void top2_push(top2_t & t, float e, int i) {
+    if (e > t.best) { t.second = fmaxf(t.second, t.best); t.best = e; t.idx = i; }
+    else t.second = fmaxf(t.second, e);
+}
+
 __global__ void __launch_bounds__(RS_THREADS) k_row_stats(const float * __restrict__ logits, int64_t ld,
                                                           const int32_t * __restrict__ rows, int V,
                                                           dfx_row_stat * __restrict__ out) {
@@ -42,25 +54,52 @@ __global__ void __launch_bounds__(RS_THREADS) k_row_stats(const float * __restri
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int nw = RS_THREADS / 64;
     const float * x = logits + (int64_t)rows[blockIdx.x] * ld;
-
-    // pass 1: per thread, elements in increasing index order
-    top2_t t = {-INFINITY, 0x7fffffff, -INFINITY};
     const bool vec = ((V & 3) == 0) && ((((uintptr_t)x) & 15) == 0);
+
+    // pass 1: top-2 and the exp sum relative to this thread's running maximum m
+    top2_t t = {-INFINITY, 0x7fffffff, -INFINITY};
+    float m = -INFINITY, s = 0.0f;
     if (vec) {
-        for (int i = 4 * tid; i < V; i += 4 * RS_THREADS) {
-            const float4 v = *(const float4 *)(x + i);
-            const float e[4] = {v.x, v.y, v.z, v.w};
+        // RS_UNROLL float4 loads in flight per thread, from clamped addresses; elements past
+        // the row end read as -inf (no effect on top-2, exp(-inf) = 0)
+        for (int i0 = 4 * tid; i0 < V; i0 += 4 * RS_UNROLL * RS_THREADS) {
+            float4 v[RS_UNROLL];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                if (e[j] > t.best) { t.second = fmaxf(t.second, t.best); t.best = e[j]; t.idx = i + j; }
-                else t.second = fmaxf(t.second, e[j]);
+            for (int u = 0; u < RS_UNROLL; u++) v[u] = *(const float4 *)(x + min(i0 + 4 * u * RS_THREADS, V - 4));
+#pragma unroll
+            for (int u = 0; u < RS_UNROLL; u++) {
+                const int i = i0 + 4 * u * RS_THREADS;
+                if (i >= V) v[u] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+                const float g = fmaxf(fmaxf(v[u].x, v[u].y), fmaxf(v[u].z, v[u].w));
+                // elements <= the running second change neither the best nor the second
+                if (g > t.second) {
+                    top2_push(t, v[u].x, i);
+                    top2_push(t, v[u].y, i + 1);
+                    top2_push(t, v[u].z, i + 2);
+                    top2_push(t, v[u].w, i + 3);
+                }
+                const float m4 = fmaxf(g, m);
+                if (m4 > m) {
+                    s = m == -INFINITY ? 0.0f : s * exp_fast(m - m4);
+                    m = m4;
+                }
+                if (m != -INFINITY) {
+                    s = s + exp_fast(v[u].x - m);
+                    s = s + exp_fast(v[u].y - m);
+                    s = s + exp_fast(v[u].z - m);
+                    s = s + exp_fast(v[u].w - m);
+                }
             }
         }
     } else {
         for (int i = tid; i < V; i += RS_THREADS) {
             const float e = x[i];
-            if (e > t.best) { t.second = fmaxf(t.second, t.best); t.best = e; t.idx = i; }
-            else t.second = fmaxf(t.second, e);
+            top2_push(t, e, i);
+            if (e > m) {
+                s = m == -INFINITY ? 0.0f : s * exp_fast(m - e);
+                m = e;
+            }
+            s = s + exp_fast(e - m);
         }
     }
     for (int off = 32; off > 0; off >>= 1) t = top2_merge(t, top2_shfl(t, off));
@@ -74,27 +113,43 @@ __global__ void __launch_bounds__(RS_THREADS) k_row_stats(const float * __restri
     float second = t.second;
     if (t.idx == 0) second = fmaxf(second, -1e30f);
 
-    // pass 2: sum of exp
-    double s = 0.0;
-    for (int i = tid; i < V; i += RS_THREADS) s += (double)(float)exp((double)(x[i] - mx));
-    s = wave_sum_d(s);
-    __syncthreads();
-    if (lane == 0) red_d[wv] = s;
+    double sd = m == -INFINITY ? 0.0 : (double)(s * exp_fast(m - mx));
+    sd = wave_sum_d(sd);
+    if (lane == 0) red_d[wv] = sd;
     __syncthreads();
     double tot = 0.0;
     for (int w = 0; w < nw; w++) tot += red_d[w];
     const float log_sum = logf((float)tot);
-
-    // pass 3: entropy
-    double ent = 0.0;
-    for (int i = tid; i < V; i += RS_THREADS) {
-        const float lp = (x[i] - mx) - log_sum;
-        const float p = (float)exp((double)lp);
-        if (p > 1e-10f) ent -= (double)(p * lp);
-    }
-    ent = wave_sum_d(ent);
     __syncthreads();
-    if (lane == 0) red_d[wv] = ent;
+
+    // pass 2: entropy
+    float ent = 0.0f;
+    if (vec) {
+        for (int i0 = 4 * tid; i0 < V; i0 += 4 * RS_UNROLL * RS_THREADS) {
+            float4 v[RS_UNROLL];
+#pragma unroll
+            for (int u = 0; u < RS_UNROLL; u++) v[u] = *(const float4 *)(x + min(i0 + 4 * u * RS_THREADS, V - 4));
+#pragma unroll
+            for (int u = 0; u < RS_UNROLL; u++) {
+                if (i0 + 4 * u * RS_THREADS >= V) continue;
+                const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float lp = (e[j] - mx) - log_sum;
+                    const float p = exp_fast(lp);
+                    if (p > 1e-10f) ent = ent - p * lp;
+                }
+            }
+        }
+    } else {
+        for (int i = tid; i < V; i += RS_THREADS) {
+            const float lp = (x[i] - mx) - log_sum;
+            const float p = exp_fast(lp);
+            if (p > 1e-10f) ent = ent - p * lp;
+        }
+    }
+    double ed = wave_sum_d((double)ent);
+    if (lane == 0) red_d[wv] = ed;
     __syncthreads();
     if (tid == 0) {
         double e = 0.0;

@@ -123,6 +123,8 @@ def _declare(L):
         "dfx_generate": (I32, [P, P, I32, I32, C.POINTER(SamplerParams), P, C.POINTER(GenStats)]),
         "dfx_generate_trace": (I32, [P, P, I32, I32, C.POINTER(SamplerParams), P, C.POINTER(GenStats), P]),
         "dfx_context_profile": (I32, [P, I32]),
+        "dfx_context_profile_read_rows": (I32, [P, I32, I32, C.POINTER(C.c_int64), C.POINTER(C.c_double),
+                                                C.POINTER(C.c_double), C.POINTER(C.c_double)]),
         "dfx_context_profile_read": (I32, [P, I32, C.POINTER(C.c_int64), C.POINTER(C.c_double),
                                            C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     }
@@ -354,11 +356,12 @@ class Context:
     def profile(self, enable=True):
         check(lib().dfx_context_profile(self.h, 1 if enable else 0), "dfx_context_profile")
 
-    def profile_read(self, wtype):
-        """{launches, ms, flops, bytes} of the GEMMs on weights of type wtype since profiling began."""
+    def profile_read(self, wtype, rows_class=0):
+        """{launches, ms, flops, bytes} of the GEMMs on weights of type wtype since profiling began;
+        rows_class 1 = launches over more than 96 rows, 2 = at most 96, 0 = all."""
         n, ms, fl, by = C.c_int64(), C.c_double(), C.c_double(), C.c_double()
-        check(lib().dfx_context_profile_read(self.h, wtype, C.byref(n), C.byref(ms), C.byref(fl), C.byref(by)),
-              "dfx_context_profile_read")
+        check(lib().dfx_context_profile_read_rows(self.h, wtype, rows_class, C.byref(n), C.byref(ms), C.byref(fl),
+                                                  C.byref(by)), "dfx_context_profile_read_rows")
         return dict(launches=n.value, ms=ms.value, flops=fl.value, bytes=by.value)
 
     def close(self):

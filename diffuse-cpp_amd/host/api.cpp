@@ -86,7 +86,13 @@ extern "C" int dfx_context_profile(dfx_context * c, int enable) {
 extern "C" int dfx_context_profile_read(dfx_context * c, int wtype, int64_t * launches, double * ms, double * flops,
                                         double * bytes) {
     if (!c) return DFX_ERR_ARG;
-    return engine_profile_read(c, wtype, launches, ms, flops, bytes);
+    return engine_profile_read(c, wtype, 0, launches, ms, flops, bytes);
+}
+
+extern "C" int dfx_context_profile_read_rows(dfx_context * c, int wtype, int rows_class, int64_t * launches,
+                                             double * ms, double * flops, double * bytes) {
+    if (!c) return DFX_ERR_ARG;
+    return engine_profile_read(c, wtype, rows_class, launches, ms, flops, bytes);
 }
 
 // ---- C++ API (include/diffuse.h) ----

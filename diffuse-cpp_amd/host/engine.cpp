@@ -150,6 +150,7 @@ int gemm(diffuse_context * c, const dev_matrix & w, int64_t N, int64_t K, int64_
     r.a = take_event(c);
     r.b = take_event(c);
     r.type = w.type;
+    r.M = M;
     r.flops = 2.0 * (double)M * N * K;
     r.bytes = (double)dfx_device_row_bytes(w.type, K) * N + (double)M * K * 2 + (double)M * N * 4;
     if (!r.a || !r.b) return hip_ok(hipErrorOutOfMemory, "hipEventCreate");
@@ -164,13 +165,14 @@ int gemm(diffuse_context * c, const dev_matrix & w, int64_t N, int64_t K, int64_
 void prof_collect(diffuse_context * c) {
     for (auto & r : c->prof_pending) {
         float ms = 0.0f;
-        if (hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess && r.type >= 0 && r.type < 32) {
-            auto & t = c->prof_tot[r.type];
-            t.launches++;
-            t.ms += ms;
-            t.flops += r.flops;
-            t.bytes += r.bytes;
-        }
+        if (hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess && r.type >= 0 && r.type < 32)
+            for (int cls : {0, r.M > 96 ? 1 : 2}) {
+                auto & t = c->prof_tot[cls][r.type];
+                t.launches++;
+                t.ms += ms;
+                t.flops += r.flops;
+                t.bytes += r.bytes;
+            }
         c->prof_pool.push_back(r.a);
         c->prof_pool.push_back(r.b);
     }
@@ -296,16 +298,17 @@ int engine_profile(diffuse_context * c, bool enable) {
     if (c->stream) TRY(hip_ok(hipStreamSynchronize(c->stream), "profile"));
     prof_collect(c);
     c->prof = enable;
-    for (auto & t : c->prof_tot) t = diffuse_context::prof_total();
+    for (auto & cls : c->prof_tot)
+        for (auto & t : cls) t = diffuse_context::prof_total();
     return DFX_OK;
 }
 
-int engine_profile_read(diffuse_context * c, int wtype, int64_t * launches, double * ms, double * flops,
-                        double * bytes) {
-    if (wtype < 0 || wtype >= 32) return DFX_ERR_ARG;
+int engine_profile_read(diffuse_context * c, int wtype, int rows_class, int64_t * launches, double * ms,
+                        double * flops, double * bytes) {
+    if (wtype < 0 || wtype >= 32 || rows_class < 0 || rows_class > 2) return DFX_ERR_ARG;
     TRY(hip_ok(hipStreamSynchronize(c->stream), "profile"));
     prof_collect(c);
-    const auto & t = c->prof_tot[wtype];
+    const auto & t = c->prof_tot[rows_class][wtype];
     if (launches) *launches = t.launches;
     if (ms) *ms = t.ms;
     if (flops) *flops = t.flops;

@@ -101,12 +101,13 @@ struct diffuse_context {
     hipEvent_t   ev0 = nullptr, ev1 = nullptr, ev2 = nullptr;
 
     // Optional per-GEMM timing: a pair of events around every GEMM launch on `stream`.
-    struct gemm_rec { hipEvent_t a, b; int type; double flops, bytes; };
+    struct gemm_rec { hipEvent_t a, b; int type; int64_t M; double flops, bytes; };
     bool                  prof = false;
     std::vector<gemm_rec> prof_pending;      // launched, not yet read
     std::vector<hipEvent_t> prof_pool;       // reusable events
     struct prof_total { long launches = 0; double ms = 0, flops = 0, bytes = 0; };
-    prof_total            prof_tot[32];      // by weight type id
+    // by row class (0 every launch, 1 M > 96, 2 M <= 96) and weight type id
+    prof_total            prof_tot[3][32];
 };
 
 // model.cpp
@@ -118,8 +119,8 @@ int  engine_context_new(const diffuse_model * m, int n_ctx, int n_threads, diffu
 void engine_context_free(diffuse_context * c);
 int  engine_forward(diffuse_context * c, const int32_t * tokens, int n, float * logits_out);
 int  engine_profile(diffuse_context * c, bool enable);
-int  engine_profile_read(diffuse_context * c, int wtype, int64_t * launches, double * ms, double * flops,
-                         double * bytes);
+int  engine_profile_read(diffuse_context * c, int wtype, int rows_class, int64_t * launches, double * ms,
+                         double * flops, double * bytes);
 int  engine_generate(diffuse_context * c, const int32_t * prompt, int n_prompt, int n_generate,
                      const dfx_sampler_params & p, int32_t * out, dfx_gen_stats * stats,
                      const diffuse_step_callback * callback, int32_t * unmask_step = nullptr);

@@ -232,6 +232,11 @@ int  dfx_generate(dfx_context * c, const int32_t * prompt, int n_prompt, int n_g
 int  dfx_context_profile(dfx_context * c, int enable);
 int  dfx_context_profile_read(dfx_context * c, int wtype, int64_t * launches, double * ms, double * flops,
                               double * bytes);
+/* The same totals for one class of row counts: rows_class 1 = GEMMs over M > 96 rows (the
+ * 64-row-tile Q4_K kernel's range), 2 = M <= 96, 0 = all (as dfx_context_profile_read).
+ * Build-defined instrumentation; no counterpart in the reference. */
+int  dfx_context_profile_read_rows(dfx_context * c, int wtype, int rows_class, int64_t * launches, double * ms,
+                                   double * flops, double * bytes);
 /* dfx_generate that also records, for each generated position, the step (0-based)
  * at which it was unmasked (-1 if still masked at the end).  Stands in for the
  * per-step callback of include/diffuse.h:67-68 for C callers. */
