@@ -1468,19 +1468,47 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
     static const cand cands[] = {{2, 2, 2}, {4, 1, 2}, {3, 1, 2}, {2, 1, 2}, {1, 2, 2}, {1, 1, 4},
                                  {1, 1, 2}, {2, 1, 4}, {2, 2, 4}};
     constexpr int n_cand = 9;
-    // measured on MI355X for the LLaDA-8B shapes (N 4096..24576, K 4096/12288,
-    // M 50..288): 64x128 workgroup tiles win from M ~ 100 up, 32x128 tiles with a
-    // 4-deep register ring below.  Of the 64x128 kernels, the one fed by LDS DMA
-    // (k_q4k_w<1, 2>) beats the register-ring one by 0-4% at those shapes.
-    int pick = M > 96 ? 3 : 5;
-    bool dma = M > 96;
+    // Kernel and split choice, from a warmed-up sweep of every variant on MI355X over
+    // the LLaDA-8B shapes (N 4096 / 12288 / 24576, K 4096 / 12288) and the row counts
+    // of a 16-step, 256-mask generation (M 50..288), kept where the whole generation
+    // got faster too.  "Narrow" GEMMs (at most 32
+    // column tiles of 128) give few workgroups; "wide" ones many.
+    //   default: the 64x128 LDS-DMA kernel k_q4k_w<1, 2>, K split at chunk borders
+    //     when K spans more than two chunks or the grid has under 160 workgroups;
+    //   M in (128, 150): 64-row tiles leave most of the last tile empty, and the
+    //     32x128 register-ring kernel (4-deep ring; 2-deep and split for narrow GEMMs
+    //     over many chunks) is 6-19% faster;
+    //   narrow, at most two chunks, M <= 128: 32x128 with a 2-deep ring and split K
+    //     (8-17% faster than the default);
+    //   narrow, many chunks, M in (64, 80]: 32x128, 2-deep ring, split K;
+    //   M <= 48 (outside the sweep, weight-bandwidth-bound): 32x128, 4-deep ring, split
+    //     K while the grid leaves the SIMDs short of a wave each.
+    // The choice only changes speed: every variant gives the same bits.
     const int chunks = dot_chunks(K);
-    int64_t tiles;
-    {
-        const int BM = 32 * cands[pick].tm, BN = 128 * cands[pick].tn;
-        tiles = (int64_t)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    const int n_col = (N + 127) / 128;
+    const bool narrow = n_col <= 32;
+    const bool can_split = chunks > 1 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
+    int pick = 3;   // register-ring 64x128 (when the DMA kernel is not used)
+    bool dma = true, split = false;
+    if (M <= 48) {
+        dma = false;
+        pick = 5;
+        split = can_split && (int64_t)n_col * ((M + 31) / 32) * 4 < 1024;
+    } else if (M > 128 && M < 150) {
+        dma = false;
+        pick = narrow && chunks > 2 ? 6 : 5;
+        split = narrow && chunks > 2 && can_split;
+    } else if (narrow && chunks <= 2 && M <= 128) {
+        dma = false;
+        pick = 6;
+        split = can_split;
+    } else if (narrow && chunks > 2 && M > 64 && M <= 80) {
+        dma = false;
+        pick = 6;
+        split = can_split;
+    } else {
+        split = can_split && (chunks > 2 || (int64_t)n_col * ((M + 63) / 64) < 160);
     }
-    bool split = chunks > 1 && tiles * 4 < 1024 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
     // DFX_Q4K_TILE="<TM>x<TN>[x<D>][s|n]" forces a configuration (tuning, tests):
     // s = split K when possible, n = never split.
     if (const char * f = getenv("DFX_Q4K_TILE")) {

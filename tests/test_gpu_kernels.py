@@ -123,7 +123,9 @@ def test_swiglu_convert_matches_oracle(gpu):
 GEMM_CASES = [(dfx.TYPE_Q4_K, 4096, 4096, m) for m in (1, 5, 50, 96, 128, 255, 288)] + [
     (dfx.TYPE_Q4_K, 12288, 4096, 288), (dfx.TYPE_Q6_K, 4096, 4096, 64), (dfx.TYPE_Q6_K, 2048, 12288, 100),
     (dfx.TYPE_Q6_K, 1000, 4096, 288), (dfx.TYPE_Q8_0, 4096, 4096, 77), (dfx.TYPE_Q4_K, 4096, 12288, 288),
-    (dfx.TYPE_Q8_0, 1024, 4096, 300)]
+    (dfx.TYPE_Q8_0, 1024, 4096, 300),
+    # batched long-context workload: one 512 + 256 sequence's step-0 rows on Q8_0 weights
+    (dfx.TYPE_Q8_0, 4096, 4096, 768), (dfx.TYPE_Q8_0, 4096, 12288, 768)]
 
 
 def gpu_gemm(typ, raw, N, K, X, ws=True):
@@ -187,7 +189,7 @@ def test_gemm_q6k_tiles_and_split_bit_exact(gpu, monkeypatch, tile, N, K, M):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
 
 
-@pytest.mark.parametrize("N,K,M", [(1000, 4096, 33), (4096, 4096, 288), (4096, 12288, 64)])
+@pytest.mark.parametrize("N,K,M", [(1000, 4096, 33), (4096, 4096, 288), (4096, 12288, 64), (4096, 4096, 768)])
 def test_gemm_f16_matches_oracle(gpu, N, K, M):
     """F16: exact f16 products accumulated by MFMA in f32 (the oracle sums in f64)."""
     raw = quant(dfx.TYPE_F16, N, K)
@@ -245,7 +247,8 @@ def test_rope_store_matches_oracle(gpu, M, H, Hkv, hd, n_ctx):
 
 @pytest.mark.parametrize("M,n_keys,H,Hkv,hd", [(288, 288, 32, 32, 128), (50, 288, 32, 32, 128),
                                                (128, 128, 28, 4, 128), (7, 768, 8, 2, 64), (3, 2000, 4, 4, 128),
-                                               (2, 3000, 2, 1, 128), (17, 1, 4, 4, 128), (33, 21, 4, 2, 64)])
+                                               (2, 3000, 2, 1, 128), (17, 1, 4, 4, 128), (33, 21, 4, 2, 64),
+                                               (768, 768, 32, 32, 128), (256, 768, 32, 32, 128)])
 def test_attention_matches_oracle_and_f64(gpu, M, n_keys, H, Hkv, hd):
     """Bit-exact with the oracle (f64 accumulation of exact products, correctly rounded
     exp), and within 1e-6 of an independent f64 evaluation.  Covers the matrix-core
