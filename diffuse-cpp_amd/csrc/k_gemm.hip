@@ -1313,9 +1313,26 @@ extern "C" size_t dfx_gemm_ws_bytes(int64_t M, int64_t N, int64_t K) {
     return (size_t)slices * M * N * sizeof(float);
 }
 
+// Split-K epilogue: sums the S partial slices in ws (slice order) plus bias and residual
+// into Y, or, with defer, leaves the slices for the consumer of Y (the next RMSNorm,
+// which then adds them and the residual itself) and reports S.
+static int reduce_or_defer(const void * ws, int S, int M, int N, const float * bias, const float * res, float * y,
+                           int64_t ldy, const int32_t * ymap, hipStream_t st, int * defer) {
+    if (defer) {
+        *defer = S;
+        return DFX_OK;
+    }
+    const int64_t MN = (int64_t)M * N;
+    const int64_t blocks = std::min<int64_t>((MN + 256 * REDUCE_R - 1) / (256 * REDUCE_R), 8192);
+    hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)blocks), dim3(256), 0, st, (const float *)ws, S, MN, N, bias, res,
+                       y, ldy, ymap);
+    DFX_CHECK_LAUNCH("dfx_gemm reduce");
+    return DFX_OK;
+}
+
 template <int TM>
 static int launch_f16(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                      float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st) {
+                      float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer) {
     constexpr int BM = TM * 32, BN = 128;
     const int gx = (N + BN - 1) / BN, gy = (M + BM - 1) / BM;
     const int n_kt = K / BK;
@@ -1333,13 +1350,7 @@ static int launch_f16(const void * w, int N, int K, const void * act, int M, con
     hipLaunchKernelGGL((k_gemm_f16<TM>), dim3(gx, gy, S), dim3(256), 0, st, (const uint8_t *)w, N, K,
                        (const half_t *)act, M, bias, res, y, ldy, ymap, (float *)ws, per);
     DFX_CHECK_LAUNCH("dfx_gemm f16");
-    if (S > 1) {
-        const int64_t MN = (int64_t)M * N;
-        const int64_t blocks = std::min<int64_t>((MN + 256 * REDUCE_R - 1) / (256 * REDUCE_R), 8192);
-        hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)blocks), dim3(256), 0, st, (const float *)ws, S, MN, N,
-                           bias, res, y, ldy, ymap);
-        DFX_CHECK_LAUNCH("dfx_gemm reduce");
-    }
+    if (S > 1) return reduce_or_defer(ws, S, M, N, bias, res, y, ldy, ymap, st, defer);
     return DFX_OK;
 }
 
@@ -1356,7 +1367,7 @@ static int launch_mmq(const void * w, int N, int K, const void * act, int M, con
 
 template <int TM, int TN, int D>
 static int launch_q4k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                      float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st) {
+                      float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st, int * defer) {
     constexpr int BM = TM * 32, BN = 4 * TN * 32;
     const int n_tiles = (N + BN - 1) / BN, m_tiles = (M + BM - 1) / BM;
     const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
@@ -1372,19 +1383,13 @@ static int launch_q4k(const void * w, int N, int K, const void * act, int M, con
     hipLaunchKernelGGL((k_q4k<TM, TN, D>), dim3((unsigned)(per_pass * passes)), dim3(256), 0, st,
                        (const uint8_t *)w, N, K, (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles, ws);
     DFX_CHECK_LAUNCH("dfx_gemm q4_k");
-    if (ws) {
-        const int64_t MN = (int64_t)M * N;
-        const int64_t blocks = std::min<int64_t>((MN + 256 * REDUCE_R - 1) / (256 * REDUCE_R), 8192);
-        hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)blocks), dim3(256), 0, st, (const float *)ws, chunks, MN, N,
-                           bias, res, y, ldy, ymap);
-        DFX_CHECK_LAUNCH("dfx_gemm q4_k reduce");
-    }
+    if (ws) return reduce_or_defer(ws, chunks, M, N, bias, res, y, ldy, ymap, st, defer);
     return DFX_OK;
 }
 
 template <int TN, int DEPTH>
 static int launch_q4k_w(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                        float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st) {
+                        float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st, int * defer) {
     const int n_tiles = (N + 128 * TN - 1) / (128 * TN), m_tiles = (M + 63) / 64;
     const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
     const int chunks = dot_chunks(K), passes = ws ? chunks : 1;
@@ -1396,19 +1401,13 @@ static int launch_q4k_w(const void * w, int N, int K, const void * act, int M, c
     hipLaunchKernelGGL((k_q4k_w<TN, DEPTH>), dim3((unsigned)(per_pass * passes)), dim3(256), 0, st, (const uint8_t *)w, N,
                        K, (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles, ws);
     DFX_CHECK_LAUNCH("dfx_gemm q4_k");
-    if (ws) {
-        const int64_t MN = (int64_t)M * N;
-        const int64_t blocks = std::min<int64_t>((MN + 256 * REDUCE_R - 1) / (256 * REDUCE_R), 8192);
-        hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)blocks), dim3(256), 0, st, (const float *)ws, chunks, MN, N,
-                           bias, res, y, ldy, ymap);
-        DFX_CHECK_LAUNCH("dfx_gemm q4_k reduce");
-    }
+    if (ws) return reduce_or_defer(ws, chunks, M, N, bias, res, y, ldy, ymap, st, defer);
     return DFX_OK;
 }
 
 template <int TM, int TN, int D>
 static int launch_q6k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                      float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st) {
+                      float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st, int * defer) {
     constexpr int BM = TM * 32, BN = 4 * TN * 32;
     const int n_tiles = (N + BN - 1) / BN, m_tiles = (M + BM - 1) / BM;
     const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
@@ -1421,20 +1420,14 @@ static int launch_q6k(const void * w, int N, int K, const void * act, int M, con
     hipLaunchKernelGGL((k_q6k<TM, TN, D>), dim3((unsigned)(per_pass * passes)), dim3(256), 0, st,
                        (const uint8_t *)w, N, K, (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles, ws);
     DFX_CHECK_LAUNCH("dfx_gemm q6_k");
-    if (ws) {
-        const int64_t MN = (int64_t)M * N;
-        const int64_t blocks = std::min<int64_t>((MN + 256 * REDUCE_R - 1) / (256 * REDUCE_R), 8192);
-        hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)blocks), dim3(256), 0, st, (const float *)ws, chunks, MN, N,
-                           bias, res, y, ldy, ymap);
-        DFX_CHECK_LAUNCH("dfx_gemm q6_k reduce");
-    }
+    if (ws) return reduce_or_defer(ws, chunks, M, N, bias, res, y, ldy, ymap, st, defer);
     return DFX_OK;
 }
 
 // Q6_K: 64x128 workgroup tiles (2-deep weight ring), split K when the grid is small.
 // DFX_Q6K_TILE = "<TM>x<TN>[s|n]" forces a tile (tuning, tests).
 static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                        float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st) {
+                        float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer) {
     int tm = M > 48 ? 2 : 1, tn = 1;
     const int chunks = dot_chunks(K);
     const int64_t tiles = (int64_t)((M + 32 * tm - 1) / (32 * tm)) * ((N + 128 * tn - 1) / (128 * tn));
@@ -1453,17 +1446,17 @@ static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, c
     if (sb_last % 2) d = 2;
     float * wsf = split ? (float *)ws : nullptr;
     if (tm == 2)
-        return d == 4 ? launch_q6k<2, 1, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st)
-                      : launch_q6k<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st);
-    return d == 4 ? launch_q6k<1, 1, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st)
-                  : launch_q6k<1, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st);
+        return d == 4 ? launch_q6k<2, 1, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer)
+                      : launch_q6k<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer);
+    return d == 4 ? launch_q6k<1, 1, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer)
+                  : launch_q6k<1, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer);
 }
 
 // Tile of the Q4_K kernel (TM x TN 32x32 tiles per wave, D = K steps in flight).
 // When the grid leaves the SIMDs short of two waves each, K is split at chunk
 // borders (workspace permitting).
 static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                        float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st) {
+                        float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer) {
     struct cand { int tm, tn, d; };
     static const cand cands[] = {{2, 2, 2}, {4, 1, 2}, {3, 1, 2}, {2, 1, 2}, {1, 2, 2}, {1, 1, 4},
                                  {1, 1, 2}, {2, 1, 4}, {2, 2, 4}};
@@ -1527,21 +1520,21 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
     if (const char * f = getenv("DFX_Q4K_TILE"); f && strchr(f, 'w')) {
         // "w": 64 x 64 per wave; "w1": 64 x 32 per wave, two workgroups per CU
         float * wsw = split ? (float *)ws : nullptr;
-        if (strstr(f, "w1")) return launch_q4k_w<1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st);
-        if (sb_last % 2) return launch_q4k_w<2, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st);
-        return launch_q4k_w<2, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st);
+        if (strstr(f, "w1")) return launch_q4k_w<1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
+        if (sb_last % 2) return launch_q4k_w<2, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
+        return launch_q4k_w<2, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
     }
-    if (dma) return launch_q4k_w<1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, split ? (float *)ws : nullptr, st);
+    if (dma) return launch_q4k_w<1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, split ? (float *)ws : nullptr, st, defer);
     if (cands[pick].d == 4 && (sb_last % 2))
         for (int c = 0; c < n_cand; c++)
             if (cands[c].tm == cands[pick].tm && cands[c].tn == cands[pick].tn && cands[c].d == 2) { pick = c; break; }
     float * wsf = split ? (float *)ws : nullptr;
 #define Q4K_CASE(c, TM_, TN_, D_) \
-    case c: return launch_q4k<TM_, TN_, D_>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st);
+    case c: return launch_q4k<TM_, TN_, D_>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer);
     switch (pick) {
         Q4K_CASE(0, 2, 2, 2) Q4K_CASE(1, 4, 1, 2) Q4K_CASE(2, 3, 1, 2) Q4K_CASE(3, 2, 1, 2) Q4K_CASE(4, 1, 2, 2)
         Q4K_CASE(5, 1, 1, 4) Q4K_CASE(7, 2, 1, 4) Q4K_CASE(8, 2, 2, 4)
-        default: return launch_q4k<1, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st);
+        default: return launch_q4k<1, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer);
     }
 #undef Q4K_CASE
 }
@@ -1567,11 +1560,16 @@ static int dispatch_mmq(const void * w, int N, int K, const void * act, int M, c
 }
 
 // Internal form: output row m goes to row ymap[m] (or m) of Y with leading dimension
-// ldy; the residual is read at the same place it is written.  Split-K (F16 only)
-// uses ws when it is large enough.
+// ldy; the residual is read at the same place it is written.  Split K uses ws when it
+// is large enough.
 int dfx_gemm_ex(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
                 const float * bias, const float * residual, float * y, int64_t ldy, const int32_t * ymap,
-                void * ws, size_t ws_bytes, void * stream) {
+                void * ws, size_t ws_bytes, void * stream, int * n_partials) {
+    // n_partials: if K gets split, leave the partial slices ws[s][m][n] for the caller
+    // to add (calls without bias or row map, ldy = N) and report their number; 0 = Y
+    // was written
+    if (n_partials) *n_partials = 0;
+    int * defer = n_partials && !bias && !ymap && ldy == N ? n_partials : nullptr;
     if (N <= 0 || K <= 0 || M < 0 || (K % 256) || N > INT32_MAX || M > INT32_MAX || K > INT32_MAX || ldy < N) {
         dfx_set_error("dfx_gemm: bad shape M=%lld N=%lld K=%lld ldy=%lld (K must be a multiple of 256)",
                       (long long)M, (long long)N, (long long)K, (long long)ldy);
@@ -1581,15 +1579,15 @@ int dfx_gemm_ex(int wtype, const void * w, int64_t N, int64_t K, const void * ac
     hipStream_t st = (hipStream_t)stream;
     const int n = (int)N, k = (int)K, m = (int)M;
     switch (wtype) {
-        case DFX_TYPE_Q4_K: return dispatch_q4k(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st);
-        case DFX_TYPE_Q6_K: return dispatch_q6k(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st);
+        case DFX_TYPE_Q4_K: return dispatch_q4k(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer);
+        case DFX_TYPE_Q6_K: return dispatch_q6k(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer);
         case DFX_TYPE_Q8_0: return dispatch_mmq<DFX_TYPE_Q8_0>(w, n, k, act, m, bias, residual, y, ldy, ymap, st);
         case DFX_TYPE_F16:
             switch (pick_tm(m, 4)) {
-                case 1: return launch_f16<1>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st);
-                case 2: return launch_f16<2>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st);
-                case 3: return launch_f16<3>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st);
-                default: return launch_f16<4>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st);
+                case 1: return launch_f16<1>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer);
+                case 2: return launch_f16<2>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer);
+                case 3: return launch_f16<3>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer);
+                default: return launch_f16<4>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer);
             }
     }
     dfx_set_error("dfx_gemm: unsupported weight type %d", wtype);
@@ -1599,5 +1597,5 @@ int dfx_gemm_ex(int wtype, const void * w, int64_t N, int64_t K, const void * ac
 extern "C" int dfx_gemm(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
                         const float * bias, const float * residual, float * y, void * ws, void * stream) {
     return dfx_gemm_ex(wtype, w, N, K, act, M, bias, residual, y, N, nullptr, ws,
-                       ws ? dfx_gemm_ws_bytes(M, N, K) : 0, stream);
+                       ws ? dfx_gemm_ws_bytes(M, N, K) : 0, stream, nullptr);
 }

@@ -177,23 +177,44 @@ __global__ void k_act_convert(int mode, const float * x, int64_t M, int64_t K, u
 // before the row reduction, and kept in registers for the scaling pass.
 // GGML ggml_compute_forward_rms_norm_f32: sum += (double)(x*x); mean = (float)(sum/K);
 // scale = 1.0f/sqrtf(mean + eps); y = x*scale; then ggml_mul by w.
-// Output row m normalises input row xmap[m] (or m).
+// Output row m normalises input row r = xmap[m] (or m).  With n_part > 0 the row is first
+// completed with a deferred split-K result, exactly as the GEMM's own reduction would:
+// x[r] = ((0 + part[0][r]) + part[1][r] + ...) + x[r], written back to x.
 template <int BPW>
-__global__ void __launch_bounds__(1024) k_rmsnorm_convert(int mode, const float * x, const int32_t * xmap,
+__global__ void __launch_bounds__(1024) k_rmsnorm_convert(int mode, float * x, const int32_t * xmap,
                                                           const float * w, int64_t M, int64_t K, float eps,
-                                                          uint8_t * act) {
+                                                          uint8_t * act, const float * part, int n_part,
+                                                          int64_t part_stride) {
 #pragma clang fp contract(off)
     __shared__ double red[16];
     const int64_t m = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
     const int nb = (int)(K >> 8);
-    const float * xr = x + (int64_t)(xmap ? xmap[m] : m) * K;
+    const int64_t r = xmap ? xmap[m] : m;
+    float * xr = x + r * K;
     float4 t[BPW], g[BPW];
 #pragma unroll
     for (int j = 0; j < BPW; j++) {
         const int b = min(wv * BPW + j, nb - 1);   // clamped: the duplicate is not summed or stored
         t[j] = *(const float4 *)(xr + (int64_t)b * 256 + 4 * lane);
         g[j] = *(const float4 *)(w + (int64_t)b * 256 + 4 * lane);
+    }
+    if (n_part > 0) {
+        const float * pr = part + r * K + 4 * lane;
+#pragma unroll
+        for (int j = 0; j < BPW; j++) {
+            const int b = min(wv * BPW + j, nb - 1);
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            for (int s = 0; s < n_part; s++) {
+                const float4 p = *(const float4 *)(pr + s * part_stride + (int64_t)b * 256);
+                v.x = v.x + p.x;
+                v.y = v.y + p.y;
+                v.z = v.z + p.z;
+                v.w = v.w + p.w;
+            }
+            t[j] = make_float4(v.x + t[j].x, v.y + t[j].y, v.z + t[j].z, v.w + t[j].w);
+            if (wv * BPW + j < nb) *(float4 *)(xr + (int64_t)b * 256 + 4 * lane) = t[j];
+        }
     }
     double s = 0.0;
 #pragma unroll
@@ -302,8 +323,8 @@ extern "C" int dfx_act_convert(int wtype, const float * x, int64_t M, int64_t K,
     return DFX_OK;
 }
 
-int dfx_rmsnorm_convert_ex(int wtype, const float * x, const int32_t * xmap, const float * w, int64_t M, int64_t K,
-                           float eps, void * act, void * stream) {
+static int rmsnorm_launch(int wtype, float * x, const int32_t * xmap, const float * w, int64_t M, int64_t K,
+                          float eps, void * act, const float * part, int n_part, int64_t part_stride, void * stream) {
     if (!dev_type_ok(wtype) || K <= 0 || (K & 255) || M < 0) {
         dfx_set_error("dfx_rmsnorm_convert: unsupported type %d or K %lld", wtype, (long long)K);
         return DFX_ERR_UNSUPPORTED;
@@ -320,9 +341,25 @@ int dfx_rmsnorm_convert_ex(int wtype, const float * x, const int32_t * xmap, con
     auto kern = bpw == 1 ? k_rmsnorm_convert<1> : bpw == 2 ? k_rmsnorm_convert<2>
               : bpw == 4 ? k_rmsnorm_convert<4> : k_rmsnorm_convert<8>;
     hipLaunchKernelGGL(kern, dim3((unsigned)M), block, 0, (hipStream_t)stream, conv_mode(wtype), x, xmap, w, M, K,
-                       eps, (uint8_t *)act);
+                       eps, (uint8_t *)act, part, n_part, part_stride);
     DFX_CHECK_LAUNCH("dfx_rmsnorm_convert");
     return DFX_OK;
+}
+
+int dfx_rmsnorm_convert_ex(int wtype, const float * x, const int32_t * xmap, const float * w, int64_t M, int64_t K,
+                           float eps, void * act, void * stream) {
+    // x is only read when no partial sums are added
+    return rmsnorm_launch(wtype, const_cast<float *>(x), xmap, w, M, K, eps, act, nullptr, 0, 0, stream);
+}
+
+int dfx_rmsnorm_convert_add(int wtype, float * x, const int32_t * xmap, const float * part, int n_part,
+                            int64_t part_rows, const float * w, int64_t M, int64_t K, float eps, void * act,
+                            void * stream) {
+    if (n_part < 0 || (n_part > 0 && (!part || part_rows < 1))) {
+        dfx_set_error("dfx_rmsnorm_convert_add: bad partial sums (%d slices)", n_part);
+        return DFX_ERR_ARG;
+    }
+    return rmsnorm_launch(wtype, x, xmap, w, M, K, eps, act, part, n_part, part_rows * K, stream);
 }
 
 extern "C" int dfx_rmsnorm_convert(int wtype, const float * x, const float * w, int64_t M, int64_t K, float eps,

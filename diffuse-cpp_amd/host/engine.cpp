@@ -141,11 +141,15 @@ hipEvent_t take_event(diffuse_context * c) {
 
 // Every GEMM of the forward goes through here; with profiling on, a pair of events
 // brackets the launch on the context stream (read back by prof_collect).
+// With n_partials, a split-K GEMM may leave its chunk sums in c->ws (see dfx_gemm_ex)
+// for the next RMSNorm to add.
 int gemm(diffuse_context * c, const dev_matrix & w, int64_t N, int64_t K, int64_t M, const float * bias,
-         const float * res, float * y, int64_t ldy, const int32_t * ymap, bool split_ok) {
+         const float * res, float * y, int64_t ldy, const int32_t * ymap, bool split_ok, int * n_partials = nullptr) {
     void * ws = split_ok ? c->ws : nullptr;
     const size_t wsb = split_ok ? c->ws_bytes : 0;
-    if (!c->prof || M == 0) return dfx_gemm_ex(w.type, w.data, N, K, c->act, M, bias, res, y, ldy, ymap, ws, wsb, c->stream);
+    if (n_partials) *n_partials = 0;
+    if (!c->prof || M == 0)
+        return dfx_gemm_ex(w.type, w.data, N, K, c->act, M, bias, res, y, ldy, ymap, ws, wsb, c->stream, n_partials);
     diffuse_context::gemm_rec r;
     r.a = take_event(c);
     r.b = take_event(c);
@@ -155,7 +159,7 @@ int gemm(diffuse_context * c, const dev_matrix & w, int64_t N, int64_t K, int64_
     r.bytes = (double)dfx_device_row_bytes(w.type, K) * N + (double)M * K * 2 + (double)M * N * 4;
     if (!r.a || !r.b) return hip_ok(hipErrorOutOfMemory, "hipEventCreate");
     TRY(hip_ok(hipEventRecord(r.a, c->stream), "event"));
-    TRY(dfx_gemm_ex(w.type, w.data, N, K, c->act, M, bias, res, y, ldy, ymap, ws, wsb, c->stream));
+    TRY(dfx_gemm_ex(w.type, w.data, N, K, c->act, M, bias, res, y, ldy, ymap, ws, wsb, c->stream, n_partials));
     TRY(hip_ok(hipEventRecord(r.b, c->stream), "event"));
     c->prof_pending.push_back(r);
     return DFX_OK;
@@ -180,15 +184,25 @@ void prof_collect(diffuse_context * c) {
 }
 
 // GEMMs of a projection group into out[M][g.n_out]; input rows already in x.
-int run_group(diffuse_context * c, const proj_group & g, const float * norm, int64_t M, int64_t K, float * out) {
+// RMSNorm of x + conversion, then the group's GEMM(s).  `pending` split-K partial sums of
+// the GEMM that produced x (left in c->ws) are added to x by the first RMSNorm.
+int run_group(diffuse_context * c, const proj_group & g, const float * norm, int64_t M, int64_t K, float * out,
+              int & pending) {
     const float eps = c->model->hparams.rms_norm_eps;
+    auto norm_convert = [&](int type) -> int {
+        if (pending == 0) return dfx_rmsnorm_convert_ex(type, c->x, nullptr, norm, M, K, eps, c->act, c->stream);
+        const int np = pending;
+        pending = 0;
+        return dfx_rmsnorm_convert_add(type, c->x, nullptr, (const float *)c->ws, np, M, norm, M, K, eps, c->act,
+                                       c->stream);
+    };
     if (g.fused) {
-        TRY(dfx_rmsnorm_convert_ex(g.all.type, c->x, nullptr, norm, M, K, eps, c->act, c->stream));
+        TRY(norm_convert(g.all.type));
         return gemm(c, g.all, g.n_out, K, M, g.bias, nullptr, out, g.n_out, nullptr, true);
     }
     for (size_t i = 0; i < g.parts.size(); i++) {
         const dev_matrix & p = g.parts[i];
-        TRY(dfx_rmsnorm_convert_ex(p.type, c->x, nullptr, norm, M, K, eps, c->act, c->stream));
+        TRY(norm_convert(p.type));
         TRY(gemm(c, p, p.rows, K, M, g.bias ? g.bias + g.col_off[i] : nullptr, nullptr, out + g.col_off[i], g.n_out,
                  nullptr, true));
     }
@@ -202,22 +216,31 @@ int forward_pass(diffuse_context * c, int M, int n_keys, int n_head) {
     const dims D(m.hparams);
     const float eps = m.hparams.rms_norm_eps;
     TRY(dfx_embed(m.tok_embd.type, m.tok_embd.data, D.d, c->d_tok, M, c->x, c->stream));
+    // split-K partial sums of the last O / down projection, still to be added to x (by
+    // the RMSNorm that reads x next)
+    int pending = 0;
     for (int64_t il = 0; il < D.L; il++) {
         const dev_layer & L = m.layers[il];
         float * kc = c->kc + il * (int64_t)c->cap * D.dkv;
         float * vc = c->vc + il * (int64_t)c->cap * D.dkv;
-        TRY(run_group(c, L.qkv, L.attn_norm, M, D.d, c->qkv));
+        TRY(run_group(c, L.qkv, L.attn_norm, M, D.d, c->qkv, pending));
         TRY(dfx_rope_store(c->qkv, c->d_pos, M, (int)D.H, (int)D.Hkv, (int)D.hd, c->rope_tab, c->qr, kc, vc,
                            c->cap, c->stream));
         TRY(dfx_attention(c->qr, kc, vc, c->cap, M, n_keys, (int)D.H, (int)D.Hkv, (int)D.hd, c->att, c->stream));
         TRY(dfx_act_convert(L.o.type, c->att, M, D.d, c->act, c->stream));
-        TRY(gemm(c, L.o, D.d, D.d, M, nullptr, c->x, c->x, D.d, nullptr, true));
-        TRY(run_group(c, L.gu, L.ffn_norm, M, D.d, c->gu));
+        TRY(gemm(c, L.o, D.d, D.d, M, nullptr, c->x, c->x, D.d, nullptr, true, &pending));
+        TRY(run_group(c, L.gu, L.ffn_norm, M, D.d, c->gu, pending));
         TRY(dfx_swiglu_convert(L.down.type, c->gu, M, D.F, c->act, c->stream));
-        TRY(gemm(c, L.down, D.d, D.F, M, nullptr, c->x, c->x, D.d, nullptr, true));
+        TRY(gemm(c, L.down, D.d, D.F, M, nullptr, c->x, c->x, D.d, nullptr, true, &pending));
     }
     if (n_head > 0) {
-        TRY(dfx_rmsnorm_convert_ex(m.output.type, c->x, c->d_hrows, m.output_norm, n_head, D.d, eps, c->act, c->stream));
+        // rows without logits never need the last layer's x
+        if (pending)
+            TRY(dfx_rmsnorm_convert_add(m.output.type, c->x, c->d_hrows, (const float *)c->ws, pending, M,
+                                        m.output_norm, n_head, D.d, eps, c->act, c->stream));
+        else
+            TRY(dfx_rmsnorm_convert_ex(m.output.type, c->x, c->d_hrows, m.output_norm, n_head, D.d, eps, c->act,
+                                       c->stream));
         TRY(gemm(c, m.output, D.V, D.d, n_head, nullptr, nullptr, c->logits, D.V, c->d_hmap, false));
     }
     return DFX_OK;

@@ -14,9 +14,16 @@
 // Internal kernel entry points with row maps (k_gemm.hip, k_quant.hip, k_sampler.hip).
 int dfx_gemm_ex(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M, const float * bias,
                 const float * residual, float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes,
-                void * stream);
+                void * stream, int * n_partials);
 int dfx_rmsnorm_convert_ex(int wtype, const float * x, const int32_t * xmap, const float * w, int64_t M, int64_t K,
                            float eps, void * act, void * stream);
+// RMSNorm + conversion of x after adding a deferred split-K result: row r (= xmap[m] or m)
+// becomes x[r] = (sum over s < n_part of part[s][r]) + x[r] (written back), then is
+// normalised and converted like dfx_rmsnorm_convert_ex.  part rows are K floats, slices
+// part_rows rows apart.
+int dfx_rmsnorm_convert_add(int wtype, float * x, const int32_t * xmap, const float * part, int n_part,
+                            int64_t part_rows, const float * w, int64_t M, int64_t K, float eps, void * act,
+                            void * stream);
 int dfx_make_candidates(const dfx_row_stat * stats, const int32_t * pos, int n, int margin, dfx_candidate * out,
                         void * stream);
 extern "C" void dfx_set_error(const char * fmt, ...);

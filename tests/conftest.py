@@ -21,6 +21,10 @@ TINY_LLADA = dict(n_vocab=1536, n_embd=512, n_head=4, n_head_kv=4, n_layer=3, n_
                   rope_theta=500000.0, rms_norm_eps=1e-5, mask_token_id=1500, is_dream=0)
 TINY_DREAM = dict(n_vocab=1280, n_embd=512, n_head=8, n_head_kv=2, n_layer=3, n_ff=768,
                   rope_theta=1000000.0, rms_norm_eps=1e-6, mask_token_id=1270, is_dream=1)
+# K spans several 2048-element chunks (O: 2304 = 2048 + 256, down: 4608 = 3 chunks), so the
+# O / down GEMMs split K and hand their chunk sums to the next RMSNorm.
+TINY_LLADA_LONGK = dict(n_vocab=1024, n_embd=2304, n_head=18, n_head_kv=18, n_layer=2, n_ff=4608,
+                        rope_theta=500000.0, rms_norm_eps=1e-5, mask_token_id=1000, is_dream=0)
 
 
 @pytest.fixture(scope="session")
@@ -39,6 +43,18 @@ def tiny_models(model_dir):
             p = model_dir / f"{arch_name}-{scheme}.gguf"
             dfx.synth_model(p, arch, scheme=scheme, seed=seed, sigma=0.05, n_threads=4)
             out[(arch_name, scheme)] = str(p)
+    return out
+
+
+@pytest.fixture(scope="session")
+def longk_models(model_dir):
+    """GGUF files of TINY_LLADA_LONGK: {("llada_longk", scheme): path}."""
+    import dfx
+    out = {}
+    for scheme in ("q4_k_m", "f16"):
+        p = model_dir / f"llada_longk-{scheme}.gguf"
+        dfx.synth_model(p, TINY_LLADA_LONGK, scheme=scheme, seed=13, sigma=0.05, n_threads=8)
+        out[("llada_longk", scheme)] = str(p)
     return out
 
 

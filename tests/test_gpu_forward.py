@@ -14,10 +14,11 @@ LOGITS_REL_L2 = 1e-2
 ARGMAX_AGREE = 0.99
 
 
-@pytest.mark.parametrize("arch", ["llada", "dream"])
-@pytest.mark.parametrize("scheme", ["q4_k_m", "q8_0", "f16"])
-def test_forward_logits_match_oracle(gpu, tiny_models, arch, scheme):
-    path = tiny_models[(arch, scheme)]
+@pytest.mark.parametrize("arch,scheme", [(a, s) for a in ("llada", "dream") for s in ("q4_k_m", "q8_0", "f16")] +
+                         [("llada_longk", "q4_k_m"), ("llada_longk", "f16")])
+def test_forward_logits_match_oracle(gpu, request, arch, scheme):
+    models = request.getfixturevalue("longk_models" if arch == "llada_longk" else "tiny_models")
+    path = models[(arch, scheme)]
     om = O.OracleModel(path)
     model = dfx.Model(path)
     ctx = dfx.Context(model, 64)
