@@ -169,8 +169,8 @@ def main():
     dfx.sync()
     elapsed_prof = time.perf_counter() - t0
     prof = {t: ctx.profile_read(t) for t in (dfx.TYPE_Q4_K, dfx.TYPE_Q6_K)}
-    q4_big = ctx.profile_read(dfx.TYPE_Q4_K, 1)     # M > 96: k_q4k_w<1, 2>, the dominant kernel
-    q4_small = ctx.profile_read(dfx.TYPE_Q4_K, 2)   # M <= 96: k_q4k<1, 1, 4>, HBM-bound shapes
+    q4_big = ctx.profile_read(dfx.TYPE_Q4_K, 1)     # M > 96: MFMA-bound shapes (mostly k_q4k_w<1, 2>)
+    q4_small = ctx.profile_read(dfx.TYPE_Q4_K, 2)   # M <= 96: weight-bandwidth-bound shapes
     ctx.profile(False)
 
     steps_done = stats.actual_steps
@@ -216,8 +216,9 @@ def main():
         "ms_per_denoise_step_cached_mean": round(float(np.mean(step_ms[1:])), 3) if len(step_ms) > 1 else None,
         "step_forward_ms": step_ms,
         "roofline": {
-            "kernel": "k_q4k_w<1, 2> (exact dequant-fused MFMA GEMM on Q4_K weights, every call over more "
-                      "than 96 rows; split-K reduction included when launched)",
+            "kernel": "Q4_K GEMM calls over more than 96 rows: k_q4k_w<1, 2> (exact dequant-fused MFMA GEMM, "
+                      "LDS-DMA fed), with k_q4k<1, 1, 4> / <1, 1, 2> where the row count favours 32-row tiles; "
+                      "a split-K reduction is included when one is launched",
             "bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": committed_traffic(),
             "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
@@ -228,7 +229,7 @@ def main():
             "gemm_share_of_time": round((q4["ms"] + prof[dfx.TYPE_Q6_K]["ms"]) / (1000 * elapsed_prof), 4),
             "events_pass_tok_s": round(B * args.steps / elapsed_prof, 2),
             "all_q4k_calls_tflops": round(achieved_all, 2),
-            "small_rows": {"kernel": "k_q4k<1, 1, 4> (calls over at most 96 rows)", "bound": "hbm",
+            "small_rows": {"kernel": "Q4_K GEMM calls over at most 96 rows", "bound": "hbm",
                            "achieved": round(small_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(small_gbs / HBM_PEAK_GBS, 4), "launches": q4_small["launches"],
                            "avg_launch_us": round(1000 * q4_small["ms"] / max(q4_small["launches"], 1), 3)},
