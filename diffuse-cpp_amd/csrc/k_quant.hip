@@ -205,12 +205,23 @@ __global__ void __launch_bounds__(1024) k_rmsnorm_convert(int mode, float * x, c
         for (int j = 0; j < BPW; j++) {
             const int b = min(wv * BPW + j, nb - 1);
             float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            for (int s = 0; s < n_part; s++) {
-                const float4 p = *(const float4 *)(pr + s * part_stride + (int64_t)b * 256);
-                v.x = v.x + p.x;
-                v.y = v.y + p.y;
-                v.z = v.z + p.z;
-                v.w = v.w + p.w;
+            // four slices in flight at a time, added in slice order.  Loads past the last
+            // slice read the last slice again and add +0 instead: v starts at +0 and so is
+            // never -0, and v + 0 = v for every other v.
+            for (int s0 = 0; s0 < n_part; s0 += 4) {
+                float4v p[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    p[u] = *(const float4v *)(pr + min(s0 + u, n_part - 1) * part_stride + (int64_t)b * 256);
+                const float4v z = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const float4v q = s0 + u < n_part ? p[u] : z;
+                    v.x = v.x + q.x;
+                    v.y = v.y + q.y;
+                    v.z = v.z + q.z;
+                    v.w = v.w + q.w;
+                }
             }
             t[j] = make_float4(v.x + t[j].x, v.y + t[j].y, v.z + t[j].z, v.w + t[j].w);
             if (wv * BPW + j < nb) *(float4 *)(xr + (int64_t)b * 256 + 4 * lane) = t[j];
