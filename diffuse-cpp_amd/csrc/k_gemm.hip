@@ -1458,9 +1458,10 @@ static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, c
 static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                         float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer) {
     struct cand { int tm, tn, d; };
-    static const cand cands[] = {{2, 2, 2}, {4, 1, 2}, {3, 1, 2}, {2, 1, 2}, {1, 2, 2}, {1, 1, 4},
-                                 {1, 1, 2}, {2, 1, 4}, {2, 2, 4}};
-    constexpr int n_cand = 9;
+    // (a 96-row tile, TM = 3, spills its sums at two workgroups per CU and is not built)
+    static const cand cands[] = {{2, 2, 2}, {4, 1, 2}, {2, 1, 2}, {1, 2, 2}, {1, 1, 4}, {1, 1, 2}, {2, 1, 4}, {2, 2, 4}};
+    constexpr int n_cand = 8;
+    enum { C_2x1x2 = 2, C_1x1x4 = 4, C_1x1x2 = 5 };
     // Kernel and split choice, from a warmed-up sweep of every variant on MI355X over
     // the LLaDA-8B shapes (N 4096 / 12288 / 24576, K 4096 / 12288) and the row counts
     // of a 16-step, 256-mask generation (M 50..288), kept where the whole generation
@@ -1481,23 +1482,23 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
     const int n_col = (N + 127) / 128;
     const bool narrow = n_col <= 32;
     const bool can_split = chunks > 1 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
-    int pick = 3;   // register-ring 64x128 (when the DMA kernel is not used)
+    int pick = C_2x1x2;   // register-ring 64x128 (when the DMA kernel is not used)
     bool dma = true, split = false;
     if (M <= 48) {
         dma = false;
-        pick = 5;
+        pick = C_1x1x4;
         split = can_split && (int64_t)n_col * ((M + 31) / 32) * 4 < 1024;
     } else if (M > 128 && M < 150) {
         dma = false;
-        pick = narrow && chunks > 2 ? 6 : 5;
+        pick = narrow && chunks > 2 ? C_1x1x2 : C_1x1x4;
         split = narrow && chunks > 2 && can_split;
     } else if (narrow && chunks <= 2 && M <= 128) {
         dma = false;
-        pick = 6;
+        pick = C_1x1x2;
         split = can_split;
     } else if (narrow && chunks > 2 && M > 64 && M <= 80) {
         dma = false;
-        pick = 6;
+        pick = C_1x1x2;
         split = can_split;
     } else {
         split = can_split && (chunks > 2 || (int64_t)n_col * ((M + 63) / 64) < 160);
@@ -1532,8 +1533,8 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
 #define Q4K_CASE(c, TM_, TN_, D_) \
     case c: return launch_q4k<TM_, TN_, D_>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer);
     switch (pick) {
-        Q4K_CASE(0, 2, 2, 2) Q4K_CASE(1, 4, 1, 2) Q4K_CASE(2, 3, 1, 2) Q4K_CASE(3, 2, 1, 2) Q4K_CASE(4, 1, 2, 2)
-        Q4K_CASE(5, 1, 1, 4) Q4K_CASE(7, 2, 1, 4) Q4K_CASE(8, 2, 2, 4)
+        Q4K_CASE(0, 2, 2, 2) Q4K_CASE(1, 4, 1, 2) Q4K_CASE(2, 2, 1, 2) Q4K_CASE(3, 1, 2, 2) Q4K_CASE(4, 1, 1, 4)
+        Q4K_CASE(6, 2, 1, 4) Q4K_CASE(7, 2, 2, 4)
         default: return launch_q4k<1, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer);
     }
 #undef Q4K_CASE
@@ -1549,14 +1550,13 @@ static int pick_tm(int M, int max_tm) {
     return best;
 }
 
+// Q8_0: one 32-row tile per workgroup.  The per-32-element block flush keeps three
+// f32 totals per output in registers, and wider row tiles spill them (measured on
+// MI355X: 2-5x slower with 64 or 96 rows per workgroup at M = 96..768).
 template <int WT>
 static int dispatch_mmq(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                         float * y, int64_t ldy, const int32_t * ymap, hipStream_t st) {
-    switch (pick_tm(M, 3)) {
-        case 1: return launch_mmq<WT, 1>(w, N, K, act, M, bias, res, y, ldy, ymap, st);
-        case 2: return launch_mmq<WT, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, st);
-        default: return launch_mmq<WT, 3>(w, N, K, act, M, bias, res, y, ldy, ymap, st);
-    }
+    return launch_mmq<WT, 1>(w, N, K, act, M, bias, res, y, ldy, ymap, st);
 }
 
 // Internal form: output row m goes to row ymap[m] (or m) of Y with leading dimension
