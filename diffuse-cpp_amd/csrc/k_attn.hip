@@ -13,10 +13,10 @@
 #include <algorithm>
 
 // One workgroup per (32-row tile, head of Q|K|V), head size HD.  Q and K heads: wave
-// w rotates rows w, w+4, .., w+28 of the tile, lane i the pairs (i, i + HD/2) (HD/2
-// pairs split over the wave's lanes); all rows' loads are issued before any
-// arithmetic.  V heads: the tile passes through LDS so that the transposed store
-// vt[kvh][dim][p] takes consecutive positions from consecutive lanes.
+// w rotates rows w, w+4, .., w+28 of the tile; HD/8 lanes share a row, each rotating
+// four consecutive pairs (i, i + HD/2) with 16-byte loads and stores; all rows' loads
+// are issued before any arithmetic.  V heads: the tile passes through LDS so that the
+// transposed store vt[kvh][dim][p] takes consecutive positions from consecutive lanes.
 #define ROPE_RT 32
 template <int HD>
 __global__ void __launch_bounds__(256) k_rope_store(const float * __restrict__ qkv, const int32_t * __restrict__ pos,
@@ -24,7 +24,7 @@ __global__ void __launch_bounds__(256) k_rope_store(const float * __restrict__ q
                                                     float * __restrict__ q_out, float * __restrict__ kc,
                                                     float * __restrict__ vt, int64_t v_ld) {
 #pragma clang fp contract(off)
-    constexpr int HALF = HD / 2, PPL = (HALF + 63) / 64;   // pairs per lane
+    constexpr int HALF = HD / 2;
     constexpr int RPW = ROPE_RT / 4;                        // rows per wave
     __shared__ float vtile[ROPE_RT * (HD + 1)];
     const int heads = H + 2 * Hkv;
@@ -33,43 +33,45 @@ __global__ void __launch_bounds__(256) k_rope_store(const float * __restrict__ q
     const int64_t ld = (int64_t)heads * HD;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     if (hh < H + Hkv) {
-        int p[RPW];
-        float x0[RPW][PPL], x1[RPW][PPL];
-        float2 cs[RPW][PPL];
+        constexpr int LPR = HALF / 4;          // lanes per row, four pairs each
+        constexpr int RPI = 64 / LPR;          // rows per pass of the wave
+        constexpr int NIT = RPW / RPI;         // passes
+        static_assert(HALF % 4 == 0 && 64 % LPR == 0 && NIT >= 1 && RPW % RPI == 0, "head size");
+        const int lr = lane / LPR, j4 = 4 * (lane % LPR);
+        int p[NIT];
+        float4 a[NIT], b[NIT], c01[NIT], c23[NIT];
 #pragma unroll
-        for (int r = 0; r < RPW; r++) {
-            const int m = m0 + min(wv + 4 * r, rows - 1);    // clamped: duplicates are not stored
-            p[r] = pos[m];
-#pragma unroll
-            for (int u = 0; u < PPL; u++) {
-                const int i = min(lane + 64 * u, HALF - 1);
-                const float * src = qkv + m * ld + (int64_t)hh * HD;
-                x0[r][u] = src[i];
-                x1[r][u] = src[i + HALF];
-            }
+        for (int it = 0; it < NIT; it++) {
+            const int m = m0 + min(wv + 4 * (it * RPI + lr), rows - 1);   // clamped: duplicates are not stored
+            p[it] = pos[m];
+            const float * src = qkv + m * ld + (int64_t)hh * HD + j4;
+            a[it] = *(const float4 *)src;
+            b[it] = *(const float4 *)(src + HALF);
         }
 #pragma unroll
-        for (int r = 0; r < RPW; r++)
+        for (int it = 0; it < NIT; it++) {
+            const float * cs = tab + ((int64_t)p[it] * HALF + j4) * 2;   // (cos, sin) of pairs j4 .. j4+3
+            c01[it] = *(const float4 *)cs;
+            c23[it] = *(const float4 *)(cs + 4);
+        }
 #pragma unroll
-            for (int u = 0; u < PPL; u++) {
-                const int i = min(lane + 64 * u, HALF - 1);
-                cs[r][u] = *(const float2 *)(tab + ((int64_t)p[r] * HALF + i) * 2);
-            }
+        for (int it = 0; it < NIT; it++) {
+            const int r = wv + 4 * (it * RPI + lr);
+            if (r >= rows) continue;
+            const int m = m0 + r;
+            const float x0[4] = {a[it].x, a[it].y, a[it].z, a[it].w}, x1[4] = {b[it].x, b[it].y, b[it].z, b[it].w};
+            const float c[4] = {c01[it].x, c01[it].z, c23[it].x, c23[it].z};
+            const float sn[4] = {c01[it].y, c01[it].w, c23[it].y, c23[it].w};
+            float y0[4], y1[4];
 #pragma unroll
-        for (int r = 0; r < RPW; r++) {
-            const int m = m0 + wv + 4 * r;
-            if (wv + 4 * r >= rows) continue;
-#pragma unroll
-            for (int u = 0; u < PPL; u++) {
-                const int i = lane + 64 * u;
-                if (i >= HALF) continue;
+            for (int k = 0; k < 4; k++) {
                 // ggml_rope_ext NEOX: rotate (i, i + n_dims/2) by theta_i(p)
-                const float y0 = x0[r][u] * cs[r][u].x - x1[r][u] * cs[r][u].y;
-                const float y1 = x0[r][u] * cs[r][u].y + x1[r][u] * cs[r][u].x;
-                float * dst = hh < H ? q_out + ((int64_t)m * H + hh) * HD : kc + ((int64_t)p[r] * Hkv + (hh - H)) * HD;
-                dst[i] = y0;
-                dst[i + HALF] = y1;
+                y0[k] = x0[k] * c[k] - x1[k] * sn[k];
+                y1[k] = x0[k] * sn[k] + x1[k] * c[k];
             }
+            float * dst = hh < H ? q_out + ((int64_t)m * H + hh) * HD : kc + ((int64_t)p[it] * Hkv + (hh - H)) * HD;
+            *(float4 *)(dst + j4) = make_float4(y0[0], y0[1], y0[2], y0[3]);
+            *(float4 *)(dst + HALF + j4) = make_float4(y1[0], y1[1], y1[2], y1[3]);
         }
     } else {
         const int kvh = hh - H - Hkv;
