@@ -11,6 +11,7 @@
 #include "dfx_device.h"
 
 #include <algorithm>
+#include <atomic>
 
 // One workgroup per (32-row tile, head of Q|K|V), head size HD.  Q and K heads: wave
 // w rotates rows w, w+4, .., w+28 of the tile; HD/8 lanes share a row, each rotating
@@ -384,18 +385,21 @@ extern "C" int dfx_rope_store(const float * qkv, const int32_t * pos, int64_t M,
 
 #define ATTN_LDS_MAX (64 * 1024)
 
-// LDS a workgroup may use on the current device (160 KB on gfx950), read once per device.
+// LDS a workgroup may use on the current device (160 KB on gfx950), read once per device
+// (contexts on several host threads may ask at once).
 static size_t attn_lds_limit() {
-    static size_t cached[64] = {0};
+    static std::atomic<size_t> cached[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 64 * 1024;
-    if (!cached[dev]) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
-            v = 64 * 1024;
-        cached[dev] = (size_t)v;
+    size_t v = cached[dev].load(std::memory_order_relaxed);
+    if (!v) {
+        int a = 0;
+        if (hipDeviceGetAttribute(&a, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || a <= 0)
+            a = 64 * 1024;
+        v = (size_t)a;
+        cached[dev].store(v, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return v;
 }
 
 // Score-row stride of the matrix-core kernel: whole 16-key tiles, plus 4 floats so

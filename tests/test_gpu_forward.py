@@ -173,3 +173,38 @@ def test_generate_cache_off_equals_full_forward_loop(gpu, tiny_models):
     assert rows[0] == 96 and all(r < 96 for r in rows[1:])
     ctx.close()
     model.close()
+
+
+def test_contexts_generate_concurrently(gpu, tiny_models):
+    """Independent sequences (the batched long-context workload's unit): several contexts
+    share one model (read-only after load, as in the reference, main-bench.cpp:153) and
+    generate at the same time from host threads, each on its own stream.  Every sequence
+    must come out exactly as when it runs alone."""
+    import threading
+    path = tiny_models[("llada", "q8_0")]
+    model = dfx.Model(path)
+    V = model.hparams.n_vocab
+    params = dfx.SamplerParams.make(n_steps=8, remasking=dfx.ENTROPY_EXIT, use_cache=True, entropy_threshold=1.5)
+    prompts = [np.random.default_rng(40 + i).integers(0, V - 64, 48).astype(np.int32) for i in range(4)]
+    ctxs = [dfx.Context(model, 48 + 32) for _ in prompts]
+    alone = [c.generate(p, 32, params) for c, p in zip(ctxs, prompts)]
+    together = [None] * len(prompts)
+    errors = []
+
+    def run(i):
+        try:
+            together[i] = ctxs[i].generate(prompts[i], 32, params)
+        except Exception as e:   # noqa: BLE001 - reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(len(prompts))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not errors, errors
+    for a, b in zip(alone, together):
+        assert b is not None and np.array_equal(a, b)
+    for c in ctxs:
+        c.close()
+    model.close()
