@@ -273,6 +273,239 @@ __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q,
     }
 }
 
+// ---- split-bf16 matrix-core attention (the default)
+//
+// Every f32 operand x is split into three bf16 parts, x = hi + mid + lo with
+// hi = bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid) (each rounded to nearest,
+// each difference exact in f32), and a product x*y is taken as the six terms down to
+// 2^-16 of it: hi*hi into one f32 sum and hi*mid + mid*hi + hi*lo + lo*hi + mid*mid
+// into a second, whose values are 2^-8 of the first, so its own rounding is far below
+// f32's.  What is left out (mid*lo, lo*mid, lo*lo and lo's rounding) is below 2^-25 of
+// |x*y|: the products are as accurate as f32 ones, on the bf16 MFMA.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+struct bf16x3 {
+    bf16x8 h, m, l;
+};
+
+__device__ __forceinline__ bf16x3 split_bf16x8(f32x4 a, f32x4 b) {
+    const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    bf16x3 r;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+        const f32x2 v = {x[e], x[e + 1]};
+        const bf16x2 h = __builtin_convertvector(v, bf16x2);
+        const f32x2 r1 = v - __builtin_convertvector(h, f32x2);
+        const bf16x2 m = __builtin_convertvector(r1, bf16x2);
+        const bf16x2 l = __builtin_convertvector(r1 - __builtin_convertvector(m, f32x2), bf16x2);
+        r.h[e] = h[0];
+        r.h[e + 1] = h[1];
+        r.m[e] = m[0];
+        r.m[e + 1] = m[1];
+        r.l[e] = l[0];
+        r.l[e + 1] = l[1];
+    }
+    return r;
+}
+
+// D = big + low at the end.
+struct split_acc {
+    float16v big, low;
+};
+
+__device__ __forceinline__ void mfma_split(const bf16x3 & a, const bf16x3 & b, split_acc & d) {
+    d.big = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.h, b.h, d.big, 0, 0, 0);
+    d.low = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.m, b.m, d.low, 0, 0, 0);
+    d.low = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.h, b.l, d.low, 0, 0, 0);
+    d.low = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.l, b.h, d.low, 0, 0, 0);
+    d.low = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.h, b.m, d.low, 0, 0, 0);
+    d.low = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.m, b.h, d.low, 0, 0, 0);
+}
+
+__device__ __forceinline__ float16v split_sum(const split_acc & d) { return d.big + d.low; }
+
+// max / sum over the 8 lanes of an aligned lane group
+__device__ __forceinline__ float group8_max(float v) {
+    for (int o = 4; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+__device__ __forceinline__ double group8_sum_d(double v) {
+    for (int o = 4; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
+// One head and 32 query rows per workgroup (4 waves, two workgroups per CU), the
+// softmax of the reference (src/diffuse-graph.cpp:107-114 with GGML soft_max:
+// s = dot(k, q) * (1/sqrtf(hd)), e = exp(s - max), sum in double, p = e * (float)(1/sum))
+// with f32 exp.
+// v_mfma_f32_32x32x16_bf16: lane l supplies A[l%32][8*(l/32) + e] and B[8*(l/32) + e][l%32],
+// e < 8, and holds D[8*(r/4) + 4*(l/32) + r%4][l%32], r < 16.
+// Phase 1: S = Q K^T, key tiles of 32 (t = wave + 4j); the query fragments stay in
+// registers; each half tile of keys (64 head dims) is loaded while the other multiplies.
+// Phase 2: softmax with the scores resident in LDS, wave w taking rows 8w..8w+7 at once,
+// eight lanes per row.
+// Phase 3: O = P V: wave w owns output columns 32*(w % CT)..+31 and key steps of 16
+// s = w / CT (mod 4 / CT); with HD = 64 two waves share a column tile and their sums
+// are added through LDS.
+// Workgroups are numbered so that all query tiles of head h run on XCD h % 8.
+#define ATTN_QT 32
+template <int HD>
+__global__ void __launch_bounds__(256, 2) k_attn_split(const float * __restrict__ q, const float * __restrict__ kc,
+                                                       const float * __restrict__ vt, int64_t v_ld, int M, int n_keys,
+                                                       int H, int Hkv, int sstride, int q_tiles,
+                                                       float * __restrict__ out) {
+#pragma clang fp contract(off)
+    extern __shared__ float S[];       // [32][sstride] scores, then probabilities; [2][64][16] partial sums
+    constexpr int QS = HD / 16;        // reduction steps of 16 head dims
+    constexpr int HS = QS / 2;         // steps per half tile
+    constexpr int CT = HD / 32;        // 32-column output tiles
+    constexpr int KW = 4 / CT;         // waves per output tile (key-step interleave)
+    const int L = blockIdx.x, xcd = L & 7, j = L >> 3;
+    const int h = 8 * (j / q_tiles) + xcd, qt = j % q_tiles;
+    if (h >= H) return;
+    const int kvh = h / (H / Hkv);
+    const int q0 = qt * ATTN_QT;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, l32 = lane & 31, hl = lane >> 5;
+    const int64_t kvstride = (int64_t)Hkv * HD;
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int ntiles = (n_keys + 31) >> 5;
+
+    // ---- phase 1
+    bf16x3 qs[QS];
+    {
+        const int row = q0 + l32;
+        const float * qr = q + ((int64_t)min(row, M - 1) * H + h) * HD + 8 * hl;
+#pragma unroll
+        for (int s = 0; s < QS; s++) {
+            const float4 a = ld4_or0(qr + 16 * s, row < M), b = ld4_or0(qr + 16 * s + 4, row < M);
+            qs[s] = split_bf16x8(f32x4{a.x, a.y, a.z, a.w}, f32x4{b.x, b.y, b.z, b.w});
+        }
+    }
+    const float * kbase = kc + (int64_t)kvh * HD + 8 * hl;
+    // steps HS*half .. HS*half + HS-1 of key tile t: lane holds key 32t + l32, dims 16s + 8hl .. +7
+    auto load_kh = [&](f32x4 (&kf)[2 * HS], int t, int half) __attribute__((always_inline)) {
+        const int n = 32 * t + l32;
+        const float * kr = kbase + (int64_t)min(n, n_keys - 1) * kvstride + 16 * HS * half;
+#pragma unroll
+        for (int s = 0; s < HS; s++) {
+            const float4 a = ld4_or0(kr + 16 * s, n < n_keys), b = ld4_or0(kr + 16 * s + 4, n < n_keys);
+            kf[2 * s] = f32x4{a.x, a.y, a.z, a.w};
+            kf[2 * s + 1] = f32x4{b.x, b.y, b.z, b.w};
+        }
+    };
+    auto mul_half = [&](const f32x4 (&kf)[2 * HS], int half, split_acc & d) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < HS; s++) mfma_split(qs[HS * half + s], split_bf16x8(kf[2 * s], kf[2 * s + 1]), d);
+    };
+    f32x4 k0[2 * HS], k1[2 * HS];
+    if (wv < ntiles) {
+        load_kh(k0, wv, 0);
+        load_kh(k1, wv, 1);
+    }
+    for (int t = wv; t < ntiles; t += 4) {
+        split_acc d = {};
+        mul_half(k0, 0, d);
+        if (t + 4 < ntiles) load_kh(k0, t + 4, 0);
+        mul_half(k1, 1, d);
+        if (t + 4 < ntiles) load_kh(k1, t + 4, 1);
+        const float16v acc = split_sum(d);
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+            S[(8 * (r >> 2) + 4 * hl + (r & 3)) * sstride + 32 * t + l32] = acc[r] * scale;
+    }
+    __syncthreads();
+
+    // ---- phase 2: keys >= n_keys (up to the 32-key tile) get probability 0
+    {
+        float * sr = S + (8 * wv + (lane >> 3)) * sstride;
+        const int c0 = 4 * (lane & 7), nk32 = 32 * ntiles;
+        float mx = -INFINITY;
+        for (int n = c0; n < nk32; n += 32) {
+            const f32x4 v = *(const f32x4 *)(sr + n);
+            mx = fmaxf(mx, fmaxf(fmaxf(n < n_keys ? v.x : -INFINITY, n + 1 < n_keys ? v.y : -INFINITY),
+                                 fmaxf(n + 2 < n_keys ? v.z : -INFINITY, n + 3 < n_keys ? v.w : -INFINITY)));
+        }
+        mx = group8_max(mx);
+        double sum = 0.0;
+        for (int n = c0; n < nk32; n += 32) {
+            const f32x4 v = *(const f32x4 *)(sr + n);
+            const f32x4 e = {n < n_keys ? expf(v.x - mx) : 0.0f, n + 1 < n_keys ? expf(v.y - mx) : 0.0f,
+                             n + 2 < n_keys ? expf(v.z - mx) : 0.0f, n + 3 < n_keys ? expf(v.w - mx) : 0.0f};
+            *(f32x4 *)(sr + n) = e;
+            sum += ((double)e.x + (double)e.y) + ((double)e.z + (double)e.w);
+        }
+        sum = group8_sum_d(sum);
+        const float inv = (float)(1.0 / sum);
+        for (int n = c0; n < nk32; n += 32) {
+            const f32x4 e = *(const f32x4 *)(sr + n);
+            *(f32x4 *)(sr + n) = f32x4{e.x * inv, e.y * inv, e.z * inv, e.w * inv};
+        }
+    }
+    __syncthreads();
+
+    // ---- phase 3
+    const int ct = wv % CT, kw = wv / CT;
+    split_acc d = {};
+    // value column 32*ct + l32 of this lane; keys 16s + 8*hl .. +7
+    const float * vb = vt + ((int64_t)kvh * HD + 32 * ct + l32) * v_ld;
+    const int nsteps = 2 * ntiles;
+    auto load_v = [&](f32x4 (&vf)[2], int s) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int n = 16 * s + 8 * hl + 4 * u;
+            // n and v_ld are multiples of 4 and n_keys <= v_ld: a load at n < n_keys stays in
+            // the row; past the sequence, key 0 is read and every key >= n_keys counts as 0
+            const f32x4 v = *(const f32x4 *)(vb + (n < n_keys ? n : 0));
+            vf[u] = f32x4{n < n_keys ? v.x : 0.0f, n + 1 < n_keys ? v.y : 0.0f, n + 2 < n_keys ? v.z : 0.0f,
+                          n + 3 < n_keys ? v.w : 0.0f};
+        }
+    };
+    constexpr int PV = 4;                           // value steps in flight
+    f32x4 vq[PV][2];
+#pragma unroll
+    for (int u = 0; u < PV; u++) load_v(vq[u], kw + KW * u);
+    for (int s0 = kw; s0 < nsteps; s0 += KW * PV) {
+#pragma unroll
+        for (int u = 0; u < PV; u++) {
+            const int s = s0 + KW * u;
+            if (s < nsteps) {
+                const f32x4 v0 = vq[u][0], v1 = vq[u][1];
+                load_v(vq[u], s + KW * PV);
+                const float * pr = S + l32 * sstride + 16 * s + 8 * hl;
+                const f32x4 p0 = *(const f32x4 *)pr, p1 = *(const f32x4 *)(pr + 4);
+                mfma_split(split_bf16x8(p0, p1), split_bf16x8(v0, v1), d);
+            }
+        }
+    }
+    float16v o = split_sum(d);
+    if constexpr (KW > 1) {
+        float * part = S + ATTN_QT * sstride;      // [64 lanes][16] of the second key half
+        __syncthreads();
+        if (kw == 1) {
+#pragma unroll
+            for (int r = 0; r < 16; r += 4)
+                *(f32x4 *)(part + (ct * 64 + lane) * 16 + r) = f32x4{o[r], o[r + 1], o[r + 2], o[r + 3]};
+        }
+        __syncthreads();
+        if (kw == 1) return;
+#pragma unroll
+        for (int r = 0; r < 16; r += 4) {
+            const f32x4 w = *(const f32x4 *)(part + (ct * 64 + lane) * 16 + r);
+            o[r] += w.x;
+            o[r + 1] += w.y;
+            o[r + 2] += w.z;
+            o[r + 3] += w.w;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int row = q0 + 8 * (r >> 2) + 4 * hl + (r & 3);
+        if (row < M) out[(int64_t)row * H * HD + (int64_t)h * HD + 32 * ct + l32] = o[r];
+    }
+}
+
 // VALU form for key counts whose score rows do not fit the matrix-core kernel's LDS:
 // TQ query rows of one head per workgroup (256 threads), full score rows in LDS.
 template <int HD, int TQ>
@@ -406,8 +639,20 @@ static size_t attn_lds_limit() {
 // rows of a 16-row fragment start in different LDS banks.
 static inline int attn_sstride(int64_t n_keys) { return (int)(((n_keys + 15) / 16) * 16 + 4); }
 
+// Score-row stride of the split-bf16 kernel: whole 32-key tiles, plus 4 floats.
+static inline int attn_split_sstride(int64_t n_keys) { return (int)(((n_keys + 31) / 32) * 32 + 4); }
+
 extern "C" int dfx_attention(const float * q, const float * kc, const float * vt, int64_t v_ld, int64_t M,
                              int64_t n_keys, int H, int Hkv, int hd, float * out, void * stream) {
+    return dfx_attention_ex(q, kc, vt, v_ld, M, n_keys, H, Hkv, hd, out, DFX_ATTN_SPLIT_BF16, stream);
+}
+
+extern "C" int dfx_attention_ex(const float * q, const float * kc, const float * vt, int64_t v_ld, int64_t M,
+                                int64_t n_keys, int H, int Hkv, int hd, float * out, int mode, void * stream) {
+    if (mode != DFX_ATTN_SPLIT_BF16 && mode != DFX_ATTN_EXACT) {
+        dfx_set_error("dfx_attention_ex: unknown mode %d", mode);
+        return DFX_ERR_ARG;
+    }
     if (M < 0 || n_keys <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || (hd != 64 && hd != 128) || v_ld < n_keys ||
         (v_ld % 4)) {
         dfx_set_error("dfx_attention: unsupported shape M=%lld keys=%lld H=%d Hkv=%d hd=%d v_ld=%lld "
@@ -417,6 +662,23 @@ extern "C" int dfx_attention(const float * q, const float * kc, const float * vt
     }
     if (M == 0) return DFX_OK;
     hipStream_t st = (hipStream_t)stream;
+    if (mode == DFX_ATTN_SPLIT_BF16) {
+        const int ss = attn_split_sstride(n_keys);
+        const size_t lds = (size_t)ATTN_QT * ss * sizeof(float) + (hd == 64 ? 2 * 64 * 16 * sizeof(float) : 0);
+        if (lds <= attn_lds_limit()) {
+            const int q_tiles = (int)((M + ATTN_QT - 1) / ATTN_QT);
+            const dim3 grid((unsigned)(8 * ((H + 7) / 8) * q_tiles));
+            if (hd == 128)
+                hipLaunchKernelGGL((k_attn_split<128>), grid, dim3(256), lds, st, q, kc, vt, v_ld, (int)M,
+                                   (int)n_keys, H, Hkv, ss, q_tiles, out);
+            else
+                hipLaunchKernelGGL((k_attn_split<64>), grid, dim3(256), lds, st, q, kc, vt, v_ld, (int)M,
+                                   (int)n_keys, H, Hkv, ss, q_tiles, out);
+            DFX_CHECK_LAUNCH("dfx_attention");
+            return DFX_OK;
+        }
+        // longer score rows: the f64 forms below (16-row tiles, then the VALU kernel)
+    }
     const int sstride = attn_sstride(n_keys);
     const size_t lds = (size_t)16 * sstride * sizeof(float);
     if (lds <= attn_lds_limit()) {

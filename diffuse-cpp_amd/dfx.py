@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(HERE, "lib", "libdiffuse.so")
 TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_K = 0, 1, 8, 12, 14, 15
 SCHED_COSINE, SCHED_LINEAR = 0, 1
 LOW_CONFIDENCE, RANDOM, ENTROPY_EXIT, MASKGIT_PLUS, TOPK_MARGIN = 0, 1, 2, 3, 4
+ATTN_SPLIT_BF16, ATTN_EXACT = 0, 1          # dfx_attention_ex modes (include/dfx.h)
 
 
 class DfxError(RuntimeError):
@@ -109,6 +110,7 @@ def _declare(L):
         "dfx_gemm": (I32, [I32, P, I64, I64, P, I64, P, P, P, P, P]),
         "dfx_rope_store": (I32, [P, P, I64, I32, I32, I32, P, P, P, P, I64, P]),
         "dfx_attention": (I32, [P, P, P, I64, I64, I64, I32, I32, I32, P, P]),
+        "dfx_attention_ex": (I32, [P, P, P, I64, I64, I64, I32, I32, I32, P, I32, P]),
         "dfx_row_stats": (I32, [P, I64, P, I64, I64, P, P]),
         "dfx_select": (I32, [P, I32, I32, F, I32, P, P, P]),
         "dfx_quantize_rows": (I32, [I32, P, I64, I64, P]),
@@ -123,6 +125,7 @@ def _declare(L):
         "dfx_generate": (I32, [P, P, I32, I32, C.POINTER(SamplerParams), P, C.POINTER(GenStats)]),
         "dfx_generate_trace": (I32, [P, P, I32, I32, C.POINTER(SamplerParams), P, C.POINTER(GenStats), P]),
         "dfx_context_profile": (I32, [P, I32]),
+        "dfx_context_set_attention": (I32, [P, I32]),
         "dfx_context_profile_read_rows": (I32, [P, I32, I32, C.POINTER(C.c_int64), C.POINTER(C.c_double),
                                                 C.POINTER(C.c_double), C.POINTER(C.c_double)]),
         "dfx_context_profile_read": (I32, [P, I32, C.POINTER(C.c_int64), C.POINTER(C.c_double),
@@ -352,6 +355,10 @@ class Context:
         check(lib().dfx_generate_trace(self.h, _ptr(prompt), len(prompt), n_generate, C.byref(params),
                                        _ptr(out), C.byref(st), _ptr(steps)), "dfx_generate_trace")
         return out, steps
+
+    def set_attention(self, mode):
+        """ATTN_SPLIT_BF16 (the default) or ATTN_EXACT for this context's forward passes."""
+        check(lib().dfx_context_set_attention(self.h, int(mode)), "dfx_context_set_attention")
 
     def profile(self, enable=True):
         check(lib().dfx_context_profile(self.h, 1 if enable else 0), "dfx_context_profile")

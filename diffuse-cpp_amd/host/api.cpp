@@ -78,6 +78,15 @@ extern "C" int dfx_generate_trace(dfx_context * c, const int32_t * prompt, int n
     return engine_generate(c, prompt, n_prompt, n_generate, *p, out, stats, nullptr, unmask_step);
 }
 
+extern "C" int dfx_context_set_attention(dfx_context * c, int mode) {
+    if (!c || (mode != DFX_ATTN_SPLIT_BF16 && mode != DFX_ATTN_EXACT)) {
+        dfx_set_error("dfx_context_set_attention: bad context or mode %d", mode);
+        return DFX_ERR_ARG;
+    }
+    c->attn_mode = mode;
+    return DFX_OK;
+}
+
 extern "C" int dfx_context_profile(dfx_context * c, int enable) {
     if (!c) return DFX_ERR_ARG;
     return engine_profile(c, enable != 0);

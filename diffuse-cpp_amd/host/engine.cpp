@@ -226,7 +226,8 @@ int forward_pass(diffuse_context * c, int M, int n_keys, int n_head) {
         TRY(run_group(c, L.qkv, L.attn_norm, M, D.d, c->qkv, pending));
         TRY(dfx_rope_store(c->qkv, c->d_pos, M, (int)D.H, (int)D.Hkv, (int)D.hd, c->rope_tab, c->qr, kc, vc,
                            c->cap, c->stream));
-        TRY(dfx_attention(c->qr, kc, vc, c->cap, M, n_keys, (int)D.H, (int)D.Hkv, (int)D.hd, c->att, c->stream));
+        TRY(dfx_attention_ex(c->qr, kc, vc, c->cap, M, n_keys, (int)D.H, (int)D.Hkv, (int)D.hd, c->att,
+                             c->attn_mode, c->stream));
         TRY(dfx_act_convert(L.o.type, c->att, M, D.d, c->act, c->stream));
         TRY(gemm(c, L.o, D.d, D.d, M, nullptr, c->x, c->x, D.d, nullptr, true, &pending));
         TRY(run_group(c, L.gu, L.ffn_norm, M, D.d, c->gu, pending));

@@ -106,6 +106,7 @@ struct diffuse_context {
     size_t       out_bytes = 0;
     int32_t *    h_pin = nullptr;    // pinned staging, 8 * cap int32
     hipEvent_t   ev0 = nullptr, ev1 = nullptr, ev2 = nullptr;
+    int          attn_mode = DFX_ATTN_SPLIT_BF16;   // dfx_attention_ex mode of the forward passes
 
     // Optional per-GEMM timing: a pair of events around every GEMM launch on `stream`.
     struct gemm_rec { hipEvent_t a, b; int type; int64_t M; double flops, bytes; };

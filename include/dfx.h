@@ -134,7 +134,21 @@ int dfx_rope_store(const float * qkv, const int32_t * pos, int64_t M, int H, int
  * of the cache (kc[n][Hkv][hd], vt[Hkv][hd][v_ld], n_keys <= v_ld), query head h
  * reads KV head h / (H/Hkv). */
 int dfx_attention(const float * q, const float * kc, const float * vt, int64_t v_ld, int64_t M, int64_t n_keys,
-                  int H, int Hkv, int hd, float * out, void * stream);
+                  int H, int Hkv, int hd, float * out, void * stream);   /* mode DFX_ATTN_SPLIT_BF16 */
+
+/* Attention arithmetic (same contract as dfx_attention; softmax as the reference:
+ * max, exp(s - max), sum in double, p = e * (float)(1/sum)):
+ *   DFX_ATTN_SPLIT_BF16 - scores and P.V on the bf16 MFMA with every f32 operand split
+ *     into three bf16 parts (x = hi + mid + lo) and each product taken as its six terms
+ *     down to 2^-16 of it (error < 2^-25 of the product, as f32), f32 accumulation,
+ *     f32 exp; the default.
+ *   DFX_ATTN_EXACT - products exact in f64, sums in f64 rounded once, correctly rounded
+ *     exp: the float result does not depend on the summation order (the oracle's
+ *     arithmetic, bit for bit). */
+#define DFX_ATTN_SPLIT_BF16 0
+#define DFX_ATTN_EXACT      1
+int dfx_attention_ex(const float * q, const float * kc, const float * vt, int64_t v_ld, int64_t M, int64_t n_keys,
+                     int H, int Hkv, int hd, float * out, int mode, void * stream);
 
 /* Per-row sampler statistics over logits rows (src/diffuse-sampler.cpp:34-57, 241-252):
  * argmax (strict >, lowest index on ties), top-1 and top-2 values and entropy.
@@ -229,6 +243,9 @@ int  dfx_generate(dfx_context * c, const int32_t * prompt, int n_prompt, int n_g
  * HIP events on its stream.  _read returns, for one weight type, the number of
  * launches, their summed duration, and their algorithmic FLOPs (2*M*N*K) and bytes
  * (weights + converted activations + f32 output).  Enabling resets the totals. */
+/* Attention arithmetic of the context's forward passes (DFX_ATTN_SPLIT_BF16, the default,
+ * or DFX_ATTN_EXACT; see dfx_attention_ex).  Build-defined; no counterpart in the reference. */
+int  dfx_context_set_attention(dfx_context * c, int mode);
 int  dfx_context_profile(dfx_context * c, int enable);
 int  dfx_context_profile_read(dfx_context * c, int wtype, int64_t * launches, double * ms, double * flops,
                               double * bytes);

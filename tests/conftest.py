@@ -46,6 +46,12 @@ def tiny_models(model_dir):
     return out
 
 
+def forward_inputs(V):
+    """The token sequences of the forward parity tests: n = 1, 17, 64, seed 3."""
+    rng = np.random.default_rng(3)
+    return [rng.integers(0, V, n).astype(np.int32) for n in (1, 17, 64)]
+
+
 @pytest.fixture(scope="session")
 def longk_models(model_dir):
     """GGUF files of TINY_LLADA_LONGK: {("llada_longk", scheme): path}."""

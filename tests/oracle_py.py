@@ -323,6 +323,22 @@ class OracleModel:
         assert rc == 0
         return (logits, kv) if kv else logits
 
+    def forward_full_perturbed(self, tokens, rel=1e-7, layer=1, seed=9, n_threads=8):
+        """forward_full with the F32 attention-norm weights of one layer multiplied by
+        (1 + rel * N(0, 1)): a probe of how far the oracle's own logits move under a
+        perturbation at the level of f32 rounding (the conditioning of the input)."""
+        lay = self._layers[layer]
+        t0 = OrcTensor(lay.attn_norm.type, lay.attn_norm.ne0, lay.attn_norm.ne1, lay.attn_norm.data)
+        assert t0.type == 0, "F32 norm weights only"
+        base = np.ctypeslib.as_array(C.cast(t0.data, C.POINTER(C.c_float)), shape=(t0.ne0,)).astype(np.float64)
+        pert = np.ascontiguousarray(
+            (base * (1 + rel * np.random.default_rng(seed).standard_normal(base.shape))).astype(np.float32))
+        lay.attn_norm = OrcTensor(t0.type, t0.ne0, t0.ne1, pert.ctypes.data)
+        try:
+            return self.forward_full(tokens, n_threads=n_threads)
+        finally:
+            lay.attn_norm = t0
+
     def new_kv(self, n_tokens):
         d = self.m.n_embd
         k = np.zeros(self.m.n_layer * n_tokens * d, dtype=np.float32)

@@ -245,16 +245,15 @@ def test_rope_store_matches_oracle(gpu, M, H, Hkv, hd, n_ctx):
     assert not kg[untouched].any() and not vg[untouched].any()
 
 
-@pytest.mark.parametrize("M,n_keys,H,Hkv,hd", [(288, 288, 32, 32, 128), (50, 288, 32, 32, 128),
-                                               (128, 128, 28, 4, 128), (7, 768, 8, 2, 64), (3, 2000, 4, 4, 128),
-                                               (2, 3000, 2, 1, 128), (17, 1, 4, 4, 128), (33, 21, 4, 2, 64),
-                                               (768, 768, 32, 32, 128), (256, 768, 32, 32, 128)])
-def test_attention_matches_oracle_and_f64(gpu, M, n_keys, H, Hkv, hd):
-    """Bit-exact with the oracle (f64 accumulation of exact products, correctly rounded
-    exp), and within 1e-6 of an independent f64 evaluation.  Covers the matrix-core
-    kernel (score rows in LDS) and the VALU kernel (3000 keys); the transposed value
-    cache has a padded row (v_ld > n_keys) holding NaN past the sequence, which must
-    not leak into the result."""
+ATTN_SHAPES = [(288, 288, 32, 32, 128), (50, 288, 32, 32, 128), (128, 128, 28, 4, 128), (7, 768, 8, 2, 64),
+               (3, 2000, 4, 4, 128), (2, 3000, 2, 1, 128), (17, 1, 4, 4, 128), (33, 21, 4, 2, 64),
+               (768, 768, 32, 32, 128), (256, 768, 32, 32, 128), (65, 97, 6, 3, 64), (1, 33, 2, 2, 128)]
+
+
+def attention_case(M, n_keys, H, Hkv, hd, mode):
+    """Run one attention on random Q/K/V; returns (got, f64 reference, q, k, v).  The
+    transposed value cache has a padded row (v_ld > n_keys) holding NaN past the
+    sequence, which must not leak into the result."""
     q = rng.standard_normal((M, H, hd)).astype(np.float32)
     k = rng.standard_normal((n_keys, Hkv, hd)).astype(np.float32)
     v = rng.standard_normal((n_keys, Hkv, hd)).astype(np.float32)
@@ -262,7 +261,8 @@ def test_attention_matches_oracle_and_f64(gpu, M, n_keys, H, Hkv, hd):
     vt = np.full((Hkv, hd, v_ld), np.nan, np.float32)
     vt[:, :, :n_keys] = v.transpose(1, 2, 0)
     qb, kb, vb, ob = dfx.Buf.of(q), dfx.Buf.of(k), dfx.Buf.of(vt), dfx.Buf(M * H * hd * 4)
-    dfx.check(L().dfx_attention(qb.ptr, kb.ptr, vb.ptr, v_ld, M, n_keys, H, Hkv, hd, ob.ptr, None), "attention")
+    dfx.check(L().dfx_attention_ex(qb.ptr, kb.ptr, vb.ptr, v_ld, M, n_keys, H, Hkv, hd, ob.ptr, mode, None),
+              "attention")
     got = ob.download(np.float32, shape=(M, H, hd))
     rep = H // Hkv
     kd = np.repeat(k.astype(np.float64), rep, axis=1)        # query head h reads KV head h // rep
@@ -270,10 +270,83 @@ def test_attention_matches_oracle_and_f64(gpu, M, n_keys, H, Hkv, hd):
     s = np.einsum("mhd,nhd->hmn", q.astype(np.float64), kd) / np.sqrt(hd)
     p = np.exp(s - s.max(-1, keepdims=True))
     p /= p.sum(-1, keepdims=True)
-    ref = np.einsum("hmn,nhd->mhd", p, vd)
+    return got, np.einsum("hmn,nhd->mhd", p, vd), q, k, v
+
+
+@pytest.mark.parametrize("M,n_keys,H,Hkv,hd", ATTN_SHAPES)
+def test_attention_exact_matches_oracle_and_f64(gpu, M, n_keys, H, Hkv, hd):
+    """DFX_ATTN_EXACT: bit-exact with the oracle (f64 accumulation of exact products,
+    correctly rounded exp), and within 1e-6 of an independent f64 evaluation.  Covers
+    the 16-row matrix-core kernel (score rows in LDS) and the VALU kernel (3000 keys)."""
+    got, ref, q, k, v = attention_case(M, n_keys, H, Hkv, hd, dfx.ATTN_EXACT)
     assert rel_l2(got, ref) < 1e-6
     exact = O.attention(q, k, v)
     assert np.array_equal(got, exact), int((got != exact).sum())
+
+
+@pytest.mark.parametrize("M,n_keys,H,Hkv,hd", ATTN_SHAPES)
+def test_attention_split_bf16_matches_f64(gpu, M, n_keys, H, Hkv, hd):
+    """The default DFX_ATTN_SPLIT_BF16: f32 operands split into bf16 hi + mid + lo,
+    products from their six leading terms (error per product < 2^-25 of it) on the bf16
+    MFMA with f32 sums and f32 exp.  Bound: rel-L2 <= 1e-6 against an independent f64
+    evaluation and the oracle (f32 arithmetic reaches a few 1e-7), every element within
+    1e-5 absolute (outputs are O(1): averages of N(0, 1) values).  The
+    3000-key and 2000-key cases take the f64 forms (score rows beyond the LDS) and so
+    stay exact; row counts and key counts off the 32-row / 32-key tiles, one key,
+    GQA and both head sizes cover the tile edges."""
+    got, ref, q, k, v = attention_case(M, n_keys, H, Hkv, hd, dfx.ATTN_SPLIT_BF16)
+    assert np.isfinite(got).all()
+    assert rel_l2(got, ref) <= 1e-6, rel_l2(got, ref)
+    assert np.abs(got - ref).max() <= 1e-5
+    assert rel_l2(got, O.attention(q, k, v)) <= 1e-6
+    # the plain entry point is this mode
+    qb, kb = dfx.Buf.of(q), dfx.Buf.of(k)
+    v_ld = (n_keys + 15) // 16 * 16 + 16
+    vt = np.zeros((Hkv, hd, v_ld), np.float32)
+    vt[:, :, :n_keys] = v.transpose(1, 2, 0)
+    vb, ob = dfx.Buf.of(vt), dfx.Buf(M * H * hd * 4)
+    dfx.check(L().dfx_attention(qb.ptr, kb.ptr, vb.ptr, v_ld, M, n_keys, H, Hkv, hd, ob.ptr, None), "attention")
+    assert np.array_equal(ob.download(np.float32, shape=(M, H, hd)), got)
+
+
+def test_attention_split_bf16_is_more_than_one_bf16_pass(gpu):
+    """Large scores (|s| up to ~25) make the softmax sensitive to score error: one bf16
+    pass (8 significant bits) misses the f64 result by more than 1e-3, two parts
+    (16 bits) by more than the split form's bound.  Checks the split form keeps
+    rel-L2 <= 1e-6 there, and that Q and K rounded to one and to two bf16 parts
+    (evaluated here in f64) do not."""
+    M, n_keys, H, Hkv, hd = 64, 256, 2, 2, 128
+    got, ref, q, k, v = attention_case(M, n_keys, H, Hkv, hd, dfx.ATTN_SPLIT_BF16)
+    del got
+    q = (q * 6).astype(np.float32)
+    qb, kb = dfx.Buf.of(q), dfx.Buf.of(k)
+    v_ld = (n_keys + 15) // 16 * 16 + 16
+    vt = np.zeros((Hkv, hd, v_ld), np.float32)
+    vt[:, :, :n_keys] = v.transpose(1, 2, 0)
+    vb, ob = dfx.Buf.of(vt), dfx.Buf(M * H * hd * 4)
+    dfx.check(L().dfx_attention_ex(qb.ptr, kb.ptr, vb.ptr, v_ld, M, n_keys, H, Hkv, hd, ob.ptr,
+                                   dfx.ATTN_SPLIT_BF16, None), "attention")
+    got = ob.download(np.float32, shape=(M, H, hd))
+
+    def f64_attn(qq, kk):
+        s = np.einsum("mhd,nhd->hmn", qq.astype(np.float64), kk.astype(np.float64)) / np.sqrt(hd)
+        p = np.exp(s - s.max(-1, keepdims=True))
+        p /= p.sum(-1, keepdims=True)
+        return np.einsum("hmn,nhd->mhd", p, v.astype(np.float64))
+
+    def to_bf16(x):
+        u = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+        u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+        return u.astype(np.uint32).view(np.float32)
+
+    def two_parts(x):
+        h = to_bf16(x)
+        return (h.astype(np.float64) + to_bf16(x - h).astype(np.float64))
+
+    ref = f64_attn(q, k)
+    assert rel_l2(got, ref) <= 1e-6, rel_l2(got, ref)
+    assert rel_l2(f64_attn(to_bf16(q), to_bf16(k)), ref) > 1e-3
+    assert rel_l2(f64_attn(two_parts(q), two_parts(k)), ref) > 1e-6
 
 
 # ---------------------------------------------------------------- sampler kernels
