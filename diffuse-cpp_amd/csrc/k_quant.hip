@@ -101,24 +101,30 @@ __device__ __forceinline__ void convert_block256(const float v[4], int lane, int
         // GGML quantize_row_q8_K_ref: max = the signed value of the first element
         // with the largest |x|; iscale = -127/max; q = min(127, nearest_int(iscale*x));
         // d = 1/iscale; bsums over 16.  All-zero block -> d = 0, q = 0.
-        float amax = 0.0f, mx = 0.0f;
-        int idx = 0x7fffffff;
+        // one 64-bit key per element: |x| bits (ordered as |x| for non-negative floats),
+        // then the inverted element index (the first of equal |x| wins), then the sign;
+        // the largest key over the wave names max
+        unsigned long long key = 0;
         for (int j = 0; j < 4; j++) {
-            const float ax = fabsf(v[j]);
-            if (ax > amax) { amax = ax; mx = v[j]; idx = 4 * lane + j; }
+            const uint32_t ab = __float_as_uint(v[j]) & 0x7fffffffu;
+            // a NaN never compares greater, as in the reference's |x| > amax scan
+            const uint64_t kj = ab > 0x7f800000u ? 0ull
+                                                 : ((uint64_t)ab << 32) | ((uint64_t)(0xffffu - (4 * lane + j)) << 1) |
+                                                       (__float_as_uint(v[j]) >> 31);
+            key = kj > key ? kj : key;
         }
         for (int off = 32; off > 0; off >>= 1) {
-            const float oa = __shfl_xor(amax, off, WAVE);
-            const float om = __shfl_xor(mx, off, WAVE);
-            const int oi = __shfl_xor(idx, off, WAVE);
-            if (oa > amax || (oa == amax && oi < idx)) { amax = oa; mx = om; idx = oi; }
+            const unsigned long long o = __shfl_xor(key, off, WAVE);
+            key = o > key ? o : key;
         }
+        const float amax = __uint_as_float((uint32_t)(key >> 32));
+        const float mx = (key & 1) ? -amax : amax;
         int qi[4] = {0, 0, 0, 0};
         float d = 0.0f;
         if (amax != 0.0f) {
-            // divisions through double round exactly once, whatever the fp32 divide lowering
-            const float iscale = (float)(-127.0 / (double)mx);
-            d = (float)(1.0 / (double)iscale);
+            // correctly rounded f32 divisions (the compiler's IEEE division)
+            const float iscale = -127.0f / mx;
+            d = 1.0f / iscale;
             for (int j = 0; j < 4; j++) qi[j] = min((int)__builtin_rintf(iscale * v[j]), 127);
         }
         for (int j = 0; j < 4; j++) o[j] = f2h((float)qi[j]);
@@ -243,9 +249,9 @@ __global__ void __launch_bounds__(1024) k_rmsnorm_convert(int mode, float * x, c
     double tot = 0.0;
     for (int i = 0; i < nw; i++) tot += red[i];
     const float mean = (float)(tot / (double)K);
-    // correctly rounded sqrtf and division (double rounding is exact for these ops)
-    const float root = (float)sqrt((double)(mean + eps));
-    const float scale = (float)(1.0 / (double)root);
+    // correctly rounded f32 sqrt and division (the compiler's IEEE forms)
+    const float root = sqrtf(mean + eps);
+    const float scale = 1.0f / root;
     const act_layout Lay = act_layout_of(mode, M, K);
 #pragma unroll
     for (int j = 0; j < BPW; j++) {
