@@ -704,8 +704,9 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
 // All rings (DEPTH slots) are in LDS; registers carry only the sums from one step to
 // the next, which leaves room for every A operand of a step to be in flight at once.
 // Loads complete in issue order, so "this wave's copies for step kt are done" is a
-// wait for all but the 4 + 9*(DEPTH-2) loads issued after them; a barrier then makes
-// every wave's copies visible.  Sums and their order: as k_q4k.
+// wait for all but the (5 + 2*TN)*(DEPTH-2) loads of the later steps issued after
+// them (the step's own nibble copies, issued last, included in the wait); a barrier
+// then makes every wave's copies visible.  Sums and their order: as k_q4k.
 __host__ __device__ constexpr int waitcnt_vm_lgkm(int vm, int lgkm) {
     return (vm & 15) | (7 << 4) | ((lgkm & 15) << 8) | ((vm >> 4) << 14);
 }
@@ -838,7 +839,7 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
     };
     // per step: 4 + 1 + 2*TN loads; after a step's copies of A and its header / scale
     // copy come its 2*TN nibble copies and DEPTH-2 whole steps
-    constexpr int WAIT_TOP = waitcnt_vm_lgkm(2 * TN + (5 + 2 * TN) * (DEPTH - 2), 0);
+    constexpr int WAIT_TOP = waitcnt_vm_lgkm((5 + 2 * TN) * (DEPTH - 2), 0);
 
     float16v P[TM][TN], S[TM][TN], T[TM][TN];
     const float16v zero16 = {};
@@ -931,9 +932,10 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
         }
     };
 
+    // steps 0 .. DEPTH-2 requested up front; step kt requests step kt + DEPTH - 1
     issue(std::integral_constant<int, 0>{}, 0);
-    issue(std::integral_constant<int, 1>{}, 1);
     if constexpr (DEPTH == 4) {
+        issue(std::integral_constant<int, 1>{}, 1);
         issue(std::integral_constant<int, 2>{}, 2);
     }
     for (int c0 = 0; c0 < n_kt; c0 += 2 * SB_CHUNK) {
