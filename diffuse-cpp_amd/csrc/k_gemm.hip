@@ -704,9 +704,8 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
 // All rings (DEPTH slots) are in LDS; registers carry only the sums from one step to
 // the next, which leaves room for every A operand of a step to be in flight at once.
 // Loads complete in issue order, so "this wave's copies for step kt are done" is a
-// wait for all but the (5 + 2*TN)*(DEPTH-2) loads of the later steps issued after
-// them (the step's own nibble copies, issued last, included in the wait); a barrier
-// then makes every wave's copies visible.  Sums and their order: as k_q4k.
+// wait for all but the loads issued after them; a barrier then makes every wave's
+// copies visible.  Sums and their order: as k_q4k.
 __host__ __device__ constexpr int waitcnt_vm_lgkm(int vm, int lgkm) {
     return (vm & 15) | (7 << 4) | ((lgkm & 15) << 8) | ((vm >> 4) << 14);
 }
@@ -839,7 +838,13 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
     };
     // per step: 4 + 1 + 2*TN loads; after a step's copies of A and its header / scale
     // copy come its 2*TN nibble copies and DEPTH-2 whole steps
-    constexpr int WAIT_TOP = waitcnt_vm_lgkm((5 + 2 * TN) * (DEPTH - 2), 0);
+    // at the top of a step: this step's A and header / scale copies (the shared ones, made
+    // visible to every wave by the barrier that follows); its nibble copies (issued last,
+    // read only by the wave that made them) may still be in flight, and so may the DEPTH-2
+    // later steps' copies.  Before the nibble words are read: the step's nibble copies, with
+    // only the DEPTH-1 later steps' copies in flight.
+    constexpr int WAIT_TOP = waitcnt_vm_lgkm(2 * TN + (5 + 2 * TN) * (DEPTH - 2), 0);
+    constexpr int WAIT_NIB = waitcnt_vm_lgkm((5 + 2 * TN) * (DEPTH - 1), 15);   // (no LDS-read wait)
 
     float16v P[TM][TN], S[TM][TN], T[TM][TN];
     const float16v zero16 = {};
@@ -875,6 +880,9 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
 #pragma unroll
             for (int i = 0; i < TM; i++) afr[kk][i] = *(const half8 *)(aslot(stage) + (8 * i + kk) * 512 + 8 * lane);
         u32x4 qw[TN][2];
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(WAIT_NIB);   // this wave's nibble copies for the step
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int t = 0; t < TN; t++)
 #pragma unroll
