@@ -110,8 +110,8 @@ extern "C" int dfx_timer_stop(void * timer, void * stream, float * ms) {
 // ---------------------------------------------------------------------------
 extern "C" int dfx_device_type(int gguf_type) {
     switch (gguf_type) {
-        case DFX_TYPE_Q4_K: case DFX_TYPE_Q6_K: case DFX_TYPE_Q8_0: case DFX_TYPE_F16: return gguf_type;
-        case DFX_TYPE_F32: return DFX_TYPE_F16;
+        case DFX_TYPE_Q4_K: case DFX_TYPE_Q6_K: case DFX_TYPE_Q8_0: case DFX_TYPE_F16: case DFX_TYPE_F32:
+            return gguf_type;
     }
     return -1;
 }
@@ -124,6 +124,7 @@ extern "C" int64_t dfx_device_row_bytes(int type, int64_t n_cols) {
         case DFX_TYPE_Q6_K: return nsb * 224;
         case DFX_TYPE_Q8_0: return nsb * 272;
         case DFX_TYPE_F16:  return n_cols * 2;
+        case DFX_TYPE_F32:  return n_cols * 4;
     }
     return -1;
 }
@@ -140,6 +141,7 @@ extern "C" int dfx_repack_rows(int gguf_type, const void * src, int64_t n_rows, 
     switch (gguf_type) {
         case DFX_TYPE_Q4_K:
         case DFX_TYPE_F16:
+        case DFX_TYPE_F32:
             memcpy(d, s, (size_t)(drb * n_rows));
             return DFX_OK;
         case DFX_TYPE_Q6_K:
@@ -159,12 +161,6 @@ extern "C" int dfx_repack_rows(int gguf_type, const void * src, int64_t n_rows, 
                 }
             }
             return DFX_OK;
-        case DFX_TYPE_F32: {
-            const float * f = (const float *)src;
-            _Float16 * h = (_Float16 *)dst;
-            for (int64_t i = 0; i < n_rows * n_cols; i++) h[i] = (_Float16)f[i];
-            return DFX_OK;
-        }
     }
     dfx_set_error("dfx_repack_rows: unsupported type %d", gguf_type);
     return DFX_ERR_UNSUPPORTED;

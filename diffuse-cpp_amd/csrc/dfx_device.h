@@ -68,7 +68,9 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 // 64*g + 8*(i + 4*p) + s holds element 32*q + 16*g + 4*i + P[s % 4] with quarter
 // q = p + 2*(s >= 4) (g, p in 0..1, i in 0..3): one word of low bits (4 bytes l..l+3)
 // carries quarters p and p+2.
-enum { CONV_Q8_K = 0, CONV_Q8_0 = 1, CONV_F16 = 2, CONV_Q8_K_P4 = 3, CONV_Q8_K_P6 = 4 };
+// For F32 weights (CONV_F32) q holds the f32 activations themselves, [M][K] (GGML's
+// vec_dot_type of F32 is F32: no conversion).
+enum { CONV_Q8_K = 0, CONV_Q8_0 = 1, CONV_F16 = 2, CONV_Q8_K_P4 = 3, CONV_Q8_K_P6 = 4, CONV_F32 = 5 };
 
 // Quantised GEMMs sum the scaled block dot products of each chunk of DFX_DOT_CHUNK
 // K elements from zero, in K order, and add the chunk sums in order (T = T + S).
@@ -79,7 +81,8 @@ __host__ __device__ inline int dot_chunks(int64_t K) { return (int)((K + DFX_DOT
 __host__ __device__ inline int conv_mode(int wtype) {
     return wtype == DFX_TYPE_Q4_K ? CONV_Q8_K_P4
          : wtype == DFX_TYPE_Q6_K ? CONV_Q8_K_P6
-         : (wtype == DFX_TYPE_Q8_0) ? CONV_Q8_0 : CONV_F16;
+         : wtype == DFX_TYPE_Q8_0 ? CONV_Q8_0
+         : wtype == DFX_TYPE_F32 ? CONV_F32 : CONV_F16;
 }
 __host__ __device__ inline bool conv_is_q8k(int mode) {
     return mode == CONV_Q8_K || mode == CONV_Q8_K_P4 || mode == CONV_Q8_K_P6;
@@ -110,7 +113,7 @@ __host__ __device__ inline act_layout act_layout_of(int mode, int64_t M, int64_t
     act_layout L;
     L.q = 0;
     L.mq = act_q_rows(mode, M);
-    L.d = align256((size_t)L.mq * K * 2);
+    L.d = align256((size_t)L.mq * K * (mode == CONV_F32 ? 4 : 2));
     const size_t nd = conv_is_q8k(mode) ? (size_t)L.mq * (K / 256) : mode == CONV_Q8_0 ? (size_t)M * (K / 32) : 0;
     L.bs = align256(L.d + nd * 4);
     const size_t nbs = conv_is_q8k(mode) ? (size_t)M * (K / 16) : 0;

@@ -644,7 +644,7 @@ static inline int attn_split_sstride(int64_t n_keys) { return (int)(((n_keys + 3
 
 extern "C" int dfx_attention(const float * q, const float * kc, const float * vt, int64_t v_ld, int64_t M,
                              int64_t n_keys, int H, int Hkv, int hd, float * out, void * stream) {
-    return dfx_attention_ex(q, kc, vt, v_ld, M, n_keys, H, Hkv, hd, out, DFX_ATTN_SPLIT_BF16, stream);
+    return dfx_attention_ex(q, kc, vt, v_ld, M, n_keys, H, Hkv, hd, out, DFX_ATTN_EXACT, stream);
 }
 
 extern "C" int dfx_attention_ex(const float * q, const float * kc, const float * vt, int64_t v_ld, int64_t M,

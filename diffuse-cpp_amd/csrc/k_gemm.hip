@@ -1265,6 +1265,75 @@ k_gemm_f16(const uint8_t * __restrict__ W, int N, int K, const half_t * __restri
                       lane);
 }
 
+// ---------------------------------------------------------------------------
+// F32 weights (GGML's vec_dot_type of F32 is F32: activations are not converted)
+// ---------------------------------------------------------------------------
+// v_mfma_f32_32x32x2_f32 on f32 operands staged in LDS: workgroup = 4 waves side by side
+// over 128 weight rows, TM row tiles of 32 activation rows per wave, K step 32.  The
+// sums are f32-accurate (GGML sums the f32 products in double in its scalar form, in its
+// own SIMD order otherwise); no activation rounding is involved, so the result stays
+// within f32 rounding of the CPU value.
+#define BKF 32
+#define FSTR (BKF + 1)   // LDS floats per row (odd: the 32 rows a wave reads hit 32 banks)
+template <int TM>
+__global__ void __launch_bounds__(256, 2)
+k_gemm_f32(const float * __restrict__ W, int N, int K, const float * __restrict__ A, int M,
+           const float * __restrict__ bias, const float * res, float * Y, int64_t ldy,
+           const int32_t * __restrict__ ymap) {
+    constexpr int BM = TM * 32, BN = 128;
+    __shared__ float Ws[BN * FSTR];
+    __shared__ float As[BM * FSTR];
+    const int tid = threadIdx.x, lane = tid & 63, wn = tid >> 6, l32 = lane & 31, hl = lane >> 5;
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    float16v acc[TM];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[i][r] = 0.0f;
+    for (int k0 = 0; k0 < K; k0 += BKF) {
+        float4 wv[4], av[TM];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {   // 128 rows x 8 float4
+            const int c = tid + 256 * j, r = c >> 3, q = c & 7;
+            const int n = min(n0 + r, N - 1);
+            wv[j] = *(const float4 *)(W + (int64_t)n * K + k0 + 4 * q);
+        }
+#pragma unroll
+        for (int j = 0; j < TM; j++) {  // BM rows x 8 float4
+            const int c = tid + 256 * j, r = c >> 3, q = c & 7;
+            const int m = min(m0 + r, M - 1);
+            av[j] = *(const float4 *)(A + (int64_t)m * K + k0 + 4 * q);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int c = tid + 256 * j, r = c >> 3, q = c & 7;
+            float * d = Ws + r * FSTR + 4 * q;
+            d[0] = wv[j].x; d[1] = wv[j].y; d[2] = wv[j].z; d[3] = wv[j].w;
+        }
+#pragma unroll
+        for (int j = 0; j < TM; j++) {
+            const int c = tid + 256 * j, r = c >> 3, q = c & 7;
+            float * d = As + r * FSTR + 4 * q;
+            d[0] = av[j].x; d[1] = av[j].y; d[2] = av[j].z; d[3] = av[j].w;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < BKF / 2; kk++) {
+            const float b = Ws[(wn * 32 + l32) * FSTR + 2 * kk + hl];
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const float a = As[(i * 32 + l32) * FSTR + 2 * kk + hl];
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[i], 0, 0, 0);
+            }
+        }
+    }
+    const int n = n0 + wn * 32 + l32;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+        epilogue_tile(acc[i], m0 + i * 32, n, M, N, bias, res, Y, ldy, ymap, nullptr, 0, lane);
+}
+
 // Fixed-order reduction of split-K partials plus epilogue: y = ((0 + p_0) + p_1 ...) + bias + res.
 // Each thread takes REDUCE_R elements spaced one grid apart, so the partial loads of one chunk,
 // the row-map reads and the residual reads are each issued as one batch at clamped (valid)
@@ -1361,6 +1430,16 @@ static int launch_f16(const void * w, int N, int K, const void * act, int M, con
                        (const half_t *)act, M, bias, res, y, ldy, ymap, (float *)ws, per);
     DFX_CHECK_LAUNCH("dfx_gemm f16");
     if (S > 1) return reduce_or_defer(ws, S, M, N, bias, res, y, ldy, ymap, st, defer);
+    return DFX_OK;
+}
+
+template <int TM>
+static int launch_f32(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
+                      float * y, int64_t ldy, const int32_t * ymap, hipStream_t st) {
+    const dim3 grid((N + 127) / 128, (M + 32 * TM - 1) / (32 * TM));
+    hipLaunchKernelGGL((k_gemm_f32<TM>), grid, dim3(256), 0, st, (const float *)w, N, K, (const float *)act, M, bias,
+                       res, y, ldy, ymap);
+    DFX_CHECK_LAUNCH("dfx_gemm f32");
     return DFX_OK;
 }
 
@@ -1599,6 +1678,9 @@ int dfx_gemm_ex(int wtype, const void * w, int64_t N, int64_t K, const void * ac
                 case 3: return launch_f16<3>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer);
                 default: return launch_f16<4>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer);
             }
+        case DFX_TYPE_F32:
+            if (m <= 32) return launch_f32<1>(w, n, k, act, m, bias, residual, y, ldy, ymap, st);
+            return launch_f32<2>(w, n, k, act, m, bias, residual, y, ldy, ymap, st);
     }
     dfx_set_error("dfx_gemm: unsupported weight type %d", wtype);
     return DFX_ERR_UNSUPPORTED;

@@ -95,6 +95,10 @@ __device__ __forceinline__ void store_q4(uint16_t * dst, const uint16_t o[4]) {
 __device__ __forceinline__ void convert_block256(const float v[4], int lane, int mode, uint8_t * act,
                                                  const act_layout & Lay, int64_t m, int64_t K, int64_t b) {
 #pragma clang fp contract(off)
+    if (mode == CONV_F32) {   // F32 weights: the activations go in unchanged
+        *(float4 *)((float *)(act + Lay.q) + m * K + b * 256 + 4 * lane) = make_float4(v[0], v[1], v[2], v[3]);
+        return;
+    }
     uint16_t * q = (uint16_t *)(act + Lay.q) + m * K + b * 256 + 4 * lane;
     uint16_t o[4];
     if (conv_is_q8k(mode)) {
@@ -290,10 +294,9 @@ __global__ void k_swiglu_convert(int mode, const float * gu, int64_t M, int64_t 
 // ---------------------------------------------------------------------------
 // Weight storage types the GEMMs read (activation conversion follows them).
 static bool dev_type_ok(int t) {
-    return t == DFX_TYPE_Q4_K || t == DFX_TYPE_Q6_K || t == DFX_TYPE_Q8_0 || t == DFX_TYPE_F16;
+    return t == DFX_TYPE_Q4_K || t == DFX_TYPE_Q6_K || t == DFX_TYPE_Q8_0 || t == DFX_TYPE_F16 || t == DFX_TYPE_F32;
 }
-// Tables that are only gathered / dequantised may also stay F32.
-static bool table_type_ok(int t) { return dev_type_ok(t) || t == DFX_TYPE_F32; }
+static bool table_type_ok(int t) { return dev_type_ok(t); }
 
 extern "C" int dfx_dequant(int type, const void * w, int64_t n_rows, int64_t n_cols, float * out, void * stream) {
     if (!table_type_ok(type) || n_cols <= 0 || n_rows <= 0 || (n_cols & 255)) {

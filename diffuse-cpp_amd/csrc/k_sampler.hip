@@ -107,6 +107,8 @@ __global__ void __launch_bounds__(RS_THREADS) k_row_stats(const float * __restri
     __syncthreads();
     t = red_t[0];
     for (int w = 1; w < nw; w++) t = top2_merge(t, red_t[w]);
+    // no element above -inf: the reference's argmax stays at its start, index 0
+    if (t.idx == 0x7fffffff) t.idx = 0;
     const float mx = t.best;
     // The reference's running second starts at -1e30 and is replaced by the old best
     // whenever a new best appears, so the sentinel survives only if index 0 is the argmax.
@@ -262,12 +264,68 @@ __global__ void __launch_bounds__(SEL_THREADS) k_select(const dfx_candidate * __
     }
 }
 
+// More candidates than one workgroup sorts: the key order (ties by position) is a strict
+// total order, so candidate i goes to place rank(i) = #{j : j before i}.  Each thread ranks
+// one candidate against all of them, read in 1024-candidate tiles through LDS.
+#define RANK_TILE 1024
+// (key, position) as one unsigned 64-bit value whose order is sel_before's: the key
+// (entropy, or -confidence) mapped to an unsigned int with the float order (-0 as +0,
+// NaN last), then the position.  Unlike float comparisons this is a total order for every
+// input, so the ranks are always a permutation.
+__device__ __forceinline__ uint64_t sel_key(const dfx_candidate & c, bool by_entropy) {
+    const float k = by_entropy ? c.entropy : -c.confidence;
+    uint32_t u = __float_as_uint(k == 0.0f ? 0.0f : k);
+    u = k != k ? 0xFFFFFFFFu : (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint32_t)c.pos;
+}
+__global__ void __launch_bounds__(256) k_select_rank(const dfx_candidate * __restrict__ cand, int n, int by_entropy,
+                                                     int32_t * __restrict__ order) {
+    __shared__ uint64_t t[RANK_TILE];
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const uint64_t me = sel_key(cand[min(i, n - 1)], by_entropy != 0);
+    int rank = 0;
+    for (int j0 = 0; j0 < n; j0 += RANK_TILE) {
+        const int nt = min(RANK_TILE, n - j0);
+        __syncthreads();
+        for (int j = threadIdx.x; j < nt; j += 256) t[j] = sel_key(cand[j0 + j], by_entropy != 0);
+        __syncthreads();
+        // equal keys (only if a caller repeats a position) keep the input order
+        for (int j = 0; j < nt; j++) rank += (t[j] < me || (t[j] == me && j0 + j < i)) ? 1 : 0;
+    }
+    if (i < n) order[rank] = i;
+}
+
+// n_unmask after k_select_rank: entropy_exit unmasks max(n_sched, the number of leading
+// entries of the order with entropy < tau), the others n_sched; capped at n.
+__global__ void __launch_bounds__(1024) k_select_count(const dfx_candidate * __restrict__ cand, int n, int by_entropy,
+                                                       float tau, int n_sched, const int32_t * __restrict__ order,
+                                                       int32_t * __restrict__ n_unmask) {
+    __shared__ int first_hard;
+    if (threadIdx.x == 0) first_hard = n;
+    __syncthreads();
+    if (by_entropy)
+        for (int r = threadIdx.x; r < n; r += 1024)
+            if (!(cand[order[r]].entropy < tau)) atomicMin(&first_hard, r);
+    __syncthreads();
+    if (threadIdx.x == 0) *n_unmask = min(by_entropy ? max(n_sched, first_hard) : n_sched, n);
+}
+
 extern "C" int dfx_select(const dfx_candidate * cand, int n, int remasking, float tau, int n_sched, int32_t * order,
                           int32_t * n_unmask, void * stream) {
     // remasking ids: include/diffuse.h:37-43 (LOW_CONFIDENCE, RANDOM, ENTROPY_EXIT, MASKGIT_PLUS, TOPK_MARGIN)
-    if (n < 0 || n > SEL_MAX || remasking < 0 || remasking > 4 || remasking == 1) {
+    if (n < 0 || remasking < 0 || remasking > 4 || remasking == 1) {
         dfx_set_error("dfx_select: unsupported n=%d or remasking=%d", n, remasking);
         return DFX_ERR_ARG;
+    }
+    if (n > SEL_MAX) {
+        const int by_ent = remasking == 2 ? 1 : 0;
+        hipLaunchKernelGGL(k_select_rank, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, cand, n,
+                           by_ent, order);
+        DFX_CHECK_LAUNCH("dfx_select rank");
+        hipLaunchKernelGGL(k_select_count, dim3(1), dim3(1024), 0, (hipStream_t)stream, cand, n, by_ent, tau, n_sched,
+                           order, n_unmask);
+        DFX_CHECK_LAUNCH("dfx_select count");
+        return DFX_OK;
     }
     int P = 1;
     while (P < n) P <<= 1;

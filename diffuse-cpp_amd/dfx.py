@@ -122,6 +122,7 @@ def _declare(L):
         "dfx_context_new": (I32, [P, I32, C.POINTER(C.c_void_p)]),
         "dfx_context_free": (None, [P]),
         "dfx_forward": (I32, [P, P, I32, P]),
+        "dfx_forward_cached": (I32, [P, P, P, I32, I32, P]),
         "dfx_generate": (I32, [P, P, I32, I32, C.POINTER(SamplerParams), P, C.POINTER(GenStats)]),
         "dfx_generate_trace": (I32, [P, P, I32, I32, C.POINTER(SamplerParams), P, C.POINTER(GenStats), P]),
         "dfx_context_profile": (I32, [P, I32]),
@@ -338,6 +339,17 @@ class Context:
         check(lib().dfx_forward(self.h, _ptr(tokens), len(tokens), _ptr(out)), "dfx_forward")
         return out
 
+    def forward_cached(self, active_tokens, active_pos, n_total):
+        """Logits [n_active][V] of the active rows, attending over all n_total cached
+        positions (the cache must hold a forward of n_total tokens)."""
+        at = np.ascontiguousarray(active_tokens, dtype=np.int32)
+        ap = np.ascontiguousarray(active_pos, dtype=np.int32)
+        V = self.model.hparams.n_vocab
+        out = np.empty((len(at), V), dtype=np.float32)
+        check(lib().dfx_forward_cached(self.h, _ptr(at), _ptr(ap), len(at), int(n_total), _ptr(out)),
+              "dfx_forward_cached")
+        return out
+
     def generate(self, prompt, n_generate, params, stats=None):
         prompt = np.ascontiguousarray(prompt, dtype=np.int32)
         out = np.empty(n_generate, dtype=np.int32)
@@ -357,7 +369,7 @@ class Context:
         return out, steps
 
     def set_attention(self, mode):
-        """ATTN_SPLIT_BF16 (the default) or ATTN_EXACT for this context's forward passes."""
+        """ATTN_EXACT (the default) or ATTN_SPLIT_BF16 for this context's forward passes."""
         check(lib().dfx_context_set_attention(self.h, int(mode)), "dfx_context_set_attention")
 
     def profile(self, enable=True):

@@ -59,6 +59,12 @@ extern "C" int dfx_forward(dfx_context * c, const int32_t * tokens, int n, float
     return engine_forward(c, tokens, n, logits_out);
 }
 
+extern "C" int dfx_forward_cached(dfx_context * c, const int32_t * active_tokens, const int32_t * active_pos,
+                                  int n_active, int n_total, float * logits_out) {
+    if (!c) return DFX_ERR_ARG;
+    return engine_forward_cached(c, active_tokens, active_pos, n_active, n_total, logits_out);
+}
+
 extern "C" int dfx_generate(dfx_context * c, const int32_t * prompt, int n_prompt, int n_generate,
                             const dfx_sampler_params * p, int32_t * out, dfx_gen_stats * stats) {
     if (!c || !p || (!prompt && n_prompt) || (!out && n_generate)) {

@@ -60,6 +60,7 @@ void free_buffers(diffuse_context * c) {
     c->d_cand = nullptr;
     c->h_pin = nullptr;
     c->cap = 0;
+    c->kv_valid = 0;
 }
 
 // NEOX rope angles, as GGML's rope cache: theta_0 = p, theta_{i+1} = theta_i *
@@ -89,7 +90,7 @@ int ensure_capacity(diffuse_context * c, int N) {
     TRY(A((void **)&c->x, n * D.d * 4));
     const int64_t kmax = std::max(D.d, D.F);
     TRY(A((void **)&c->act, std::max({dfx_act_bytes(DFX_TYPE_Q4_K, n, kmax), dfx_act_bytes(DFX_TYPE_Q8_0, n, kmax),
-                                      dfx_act_bytes(DFX_TYPE_F16, n, kmax)})));
+                                      dfx_act_bytes(DFX_TYPE_F16, n, kmax), dfx_act_bytes(DFX_TYPE_F32, n, kmax)})));
     TRY(A((void **)&c->qkv, n * D.nqkv * 4));
     TRY(A((void **)&c->qr, n * D.d * 4));
     TRY(A((void **)&c->att, n * D.d * 4));
@@ -358,8 +359,50 @@ int engine_forward(diffuse_context * c, const int32_t * tokens, int n, float * l
     TRY(upload_i32(c, c->d_pos, idx.data(), n, 1));
     TRY(upload_i32(c, c->d_hrows, idx.data(), n, 2));
     TRY(upload_i32(c, c->d_hmap, idx.data(), n, 3));
+    c->kv_valid = 0;
     TRY(forward_pass(c, n, n, n));
     TRY(hip_ok(hipMemcpyAsync(logits_out, c->logits, (size_t)n * D.V * 4, hipMemcpyDeviceToHost, c->stream), "D2H"));
+    TRY(hip_ok(hipStreamSynchronize(c->stream), "forward"));
+    c->kv_valid = n;   // the K/V of positions 0..n-1 are in the cache
+    prof_collect(c);
+    return DFX_OK;
+}
+
+int engine_forward_cached(diffuse_context * c, const int32_t * active_tokens, const int32_t * active_pos, int n_active,
+                          int n_total, float * logits_out) {
+    if (n_active <= 0 || !active_tokens || !active_pos || !logits_out || n_active > n_total) {
+        dfx_set_error("diffuse_forward_cached: bad arguments");
+        return DFX_ERR_ARG;
+    }
+    if (c->kv_valid != n_total) {
+        dfx_set_error("diffuse_forward_cached: the cache holds %d positions, not %d (run a full forward first)",
+                      c->kv_valid, n_total);
+        return DFX_ERR_ARG;
+    }
+    const dims D(c->model->hparams);
+    std::vector<char> seen(n_total, 0);
+    for (int a = 0; a < n_active; a++) {
+        if (active_tokens[a] < 0 || active_tokens[a] >= c->model->tok_embd.rows) {
+            dfx_set_error("diffuse_forward_cached: token %d out of range", active_tokens[a]);
+            return DFX_ERR_ARG;
+        }
+        if (active_pos[a] < 0 || active_pos[a] >= n_total || seen[active_pos[a]]) {
+            dfx_set_error("diffuse_forward_cached: position %d out of range or repeated", active_pos[a]);
+            return DFX_ERR_ARG;
+        }
+        seen[active_pos[a]] = 1;
+    }
+    std::vector<int32_t> idx(n_active);
+    std::iota(idx.begin(), idx.end(), 0);
+    TRY(upload_i32(c, c->d_tok, active_tokens, n_active, 0));
+    TRY(upload_i32(c, c->d_pos, active_pos, n_active, 1));
+    TRY(upload_i32(c, c->d_hrows, idx.data(), n_active, 2));
+    TRY(upload_i32(c, c->d_hmap, idx.data(), n_active, 3));
+    // the active rows' K/V are written into the cache before attention reads all
+    // n_total positions (update_kv + the [cached | active] concat of the reference)
+    TRY(forward_pass(c, n_active, n_total, n_active));
+    TRY(hip_ok(hipMemcpyAsync(logits_out, c->logits, (size_t)n_active * D.V * 4, hipMemcpyDeviceToHost, c->stream),
+               "D2H"));
     TRY(hip_ok(hipStreamSynchronize(c->stream), "forward"));
     prof_collect(c);
     return DFX_OK;
@@ -387,11 +430,8 @@ int engine_generate(diffuse_context * c, const int32_t * prompt, int n_prompt, i
         dfx_set_error("diffuse_generate: mask token %d outside the embedding table", mask_id);
         return DFX_ERR_FORMAT;
     }
-    if (n_generate > 2048) {
-        dfx_set_error("diffuse_generate: n_generate %d exceeds the selection kernel's 2048", n_generate);
-        return DFX_ERR_UNSUPPORTED;
-    }
     TRY(ensure_capacity(c, N));
+    c->kv_valid = 0;   // the generation leaves the cache partly stale
 
     std::vector<int32_t> seq(prompt, prompt + n_prompt);
     seq.resize(N, mask_id);
@@ -517,6 +557,11 @@ int engine_generate(diffuse_context * c, const int32_t * prompt, int n_prompt, i
                 const auto * ho = (const int32_t *)(hc + c->cap);
                 std::copy(ho, ho + n_cand, order.begin());
                 n_unmask = ho[c->cap];
+                for (int j = 0; j < n_cand; j++)
+                    if (order[j] < 0 || order[j] >= n_cand) {
+                        dfx_set_error("diffuse_generate: selection returned index %d of %d", order[j], n_cand);
+                        return DFX_ERR_HIP;
+                    }
             }
         } else {
             // Stochastic path stays on the host like the reference (src/diffuse-sampler.cpp:256-269).

@@ -106,7 +106,8 @@ struct diffuse_context {
     size_t       out_bytes = 0;
     int32_t *    h_pin = nullptr;    // pinned staging, 8 * cap int32
     hipEvent_t   ev0 = nullptr, ev1 = nullptr, ev2 = nullptr;
-    int          attn_mode = DFX_ATTN_SPLIT_BF16;   // dfx_attention_ex mode of the forward passes
+    int          attn_mode = DFX_ATTN_EXACT;   // dfx_attention_ex mode of the forward passes
+    int          kv_valid = 0;       // positions 0..kv_valid-1 of the cache hold a full forward's K/V
 
     // Optional per-GEMM timing: a pair of events around every GEMM launch on `stream`.
     struct gemm_rec { hipEvent_t a, b; int type; int64_t M; double flops, bytes; };
@@ -126,6 +127,8 @@ void engine_model_free(diffuse_model * m);
 int  engine_context_new(const diffuse_model * m, int n_ctx, int n_threads, diffuse_context ** out);
 void engine_context_free(diffuse_context * c);
 int  engine_forward(diffuse_context * c, const int32_t * tokens, int n, float * logits_out);
+int  engine_forward_cached(diffuse_context * c, const int32_t * active_tokens, const int32_t * active_pos, int n_active,
+                           int n_total, float * logits_out);
 int  engine_profile(diffuse_context * c, bool enable);
 int  engine_profile_read(diffuse_context * c, int wtype, int rows_class, int64_t * launches, double * ms,
                          double * flops, double * bytes);

@@ -226,14 +226,8 @@ struct loader {
 
         // token embedding table
         if (te->ne[0] != d || te->ne[1] < hp.n_vocab) { err = "token_embd.weight shape mismatch"; return false; }
-        const bool embd_f32 = te->type == DFX_TYPE_F32;
-        if (!embd_f32 && !check_matrix(te, d, te->ne[1])) return false;
-        if (embd_f32) {
-            const size_t bytes = (size_t)(d * te->ne[1] * 4);
-            uint8_t * p = (uint8_t *)dalloc(bytes);
-            if (!p || !upload(p, te->data, bytes)) return false;
-            m->tok_embd = dev_matrix{DFX_TYPE_F32, te->ne[1], d, p};
-        } else {
+        if (!check_matrix(te, d, te->ne[1])) return false;
+        {
             uint8_t * p = (uint8_t *)dalloc((size_t)(dfx_device_row_bytes(te->type, d) * te->ne[1]));
             if (!p || !put_matrix(te, p, m->tok_embd)) return false;
         }
@@ -245,13 +239,8 @@ struct loader {
             if (!check_matrix(to, d, hp.n_vocab)) return false;
             uint8_t * p = (uint8_t *)dalloc((size_t)(dfx_device_row_bytes(to->type, d) * hp.n_vocab));
             if (!p || !put_matrix(to, p, m->output)) return false;
-        } else if (!embd_f32) {
-            m->output = m->tok_embd;
-            m->output.rows = hp.n_vocab;
         } else {
-            // F32 table: the gather keeps F32, the GEMM gets an F16 copy
-            uint8_t * p = (uint8_t *)dalloc((size_t)(dfx_device_row_bytes(DFX_TYPE_F32, d) * te->ne[1]));
-            if (!p || !put_matrix(te, p, m->output)) return false;
+            m->output = m->tok_embd;
             m->output.rows = hp.n_vocab;
         }
 

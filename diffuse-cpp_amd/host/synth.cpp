@@ -107,7 +107,12 @@ extern "C" int dfx_quantize_rows(int type, const float * src, int64_t n_rows, in
 
 extern "C" int dfx_synth_model(const char * path, const dfx_synth_spec * s) {
     quant_scheme sch;
-    if (!path || !s || !scheme_for(s->scheme ? s->scheme : "f16", sch)) {
+    const char * scheme = s && s->scheme ? s->scheme : "f16";
+    if (path && s && !strcmp(scheme, "f32")) {
+        // the converters' default output type (tools/convert-llada.py --type f32): every
+        // tensor F32 (the generator's f16-rounded draws are exact in it)
+        sch = {"F32", QT_F32, QT_F32, QT_F32, QT_F32, QT_F32, QT_F32};
+    } else if (!path || !s || !scheme_for(scheme, sch)) {
         dfx_set_error("dfx_synth_model: bad arguments or unknown scheme");
         return DFX_ERR_ARG;
     }

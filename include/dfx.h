@@ -67,8 +67,9 @@ int dfx_timer_stop(void * timer, void * stream, float * ms);
  *   Q6_K  224 B  GGML block_q6_K (210 B) + 14 zero bytes    {ql[128], qh[64], scales[16], d, pad}
  *   Q8_0  272 B  eight GGML block_q8_0 regrouped            {d[8], qs[8][32]}
  *   F16   512 B  256 halves
+ *   F32  1024 B  256 floats
  * dfx_repack_rows converts GGUF bytes (n_rows x n_cols, GGML layout) into this
- * layout on the host; F32 is stored as F16.  n_cols must be a multiple of 256.
+ * layout on the host.  n_cols must be a multiple of 256.
  */
 int64_t dfx_device_row_bytes(int type, int64_t n_cols);   /* -1 if unsupported */
 int     dfx_device_type(int gguf_type);                   /* storage type used for a GGUF type */
@@ -87,9 +88,10 @@ int dfx_embed(int type, const void * table, int64_t n_embd, const int32_t * toke
 
 /* Activation conversion to the weight's vec_dot_type, the way GGML's mul_mat
  * converts src1 before its dot products (Q8_K blocks of 256 for Q4_K/Q6_K, Q8_0
- * blocks of 32 for Q8_0, F16 for F16).  The result goes to an activation buffer
- * of dfx_act_bytes(wtype, M, K) bytes:
- *   q   f16 [M][K]      int8 quants as exact f16 integers (F16: the f16 values)
+ * blocks of 32 for Q8_0, F16 for F16, F32 kept for F32).  The result goes to an
+ * activation buffer of dfx_act_bytes(wtype, M, K) bytes:
+ *   q   f16 [M][K]      int8 quants as exact f16 integers (F16: the f16 values;
+ *                       F32 weights: the f32 values themselves, f32 [M][K])
  *   d   f32 [M][K/blk]  block scales (Q8_K: blk 256; Q8_0: blk 32, the f16 scale)
  *   bs  f16 [M][K/16]   Q8_K only: sums of q over 16 elements
  * each part starting at a 256-byte boundary, in this order.  For Q4_K and Q6_K
@@ -134,17 +136,17 @@ int dfx_rope_store(const float * qkv, const int32_t * pos, int64_t M, int H, int
  * of the cache (kc[n][Hkv][hd], vt[Hkv][hd][v_ld], n_keys <= v_ld), query head h
  * reads KV head h / (H/Hkv). */
 int dfx_attention(const float * q, const float * kc, const float * vt, int64_t v_ld, int64_t M, int64_t n_keys,
-                  int H, int Hkv, int hd, float * out, void * stream);   /* mode DFX_ATTN_SPLIT_BF16 */
+                  int H, int Hkv, int hd, float * out, void * stream);   /* mode DFX_ATTN_EXACT */
 
 /* Attention arithmetic (same contract as dfx_attention; softmax as the reference:
  * max, exp(s - max), sum in double, p = e * (float)(1/sum)):
  *   DFX_ATTN_SPLIT_BF16 - scores and P.V on the bf16 MFMA with every f32 operand split
  *     into three bf16 parts (x = hi + mid + lo) and each product taken as its six terms
  *     down to 2^-16 of it (error < 2^-25 of the product, as f32), f32 accumulation,
- *     f32 exp; the default.
+ *     f32 exp.
  *   DFX_ATTN_EXACT - products exact in f64, sums in f64 rounded once, correctly rounded
  *     exp: the float result does not depend on the summation order (the oracle's
- *     arithmetic, bit for bit). */
+ *     arithmetic, bit for bit); the default of dfx_attention and of every context. */
 #define DFX_ATTN_SPLIT_BF16 0
 #define DFX_ATTN_EXACT      1
 int dfx_attention_ex(const float * q, const float * kc, const float * vt, int64_t v_ld, int64_t M, int64_t n_keys,
@@ -167,7 +169,8 @@ int dfx_row_stats(const float * logits, int64_t ld, const int32_t * rows, int64_
  * top-1 logit descending; TOPK_MARGIN: top1-top2 descending), ties by position
  * ascending.  Writes order[0..n) (candidate indices) and *n_unmask = the count to
  * unmask (schedule count n_sched, or max(n_sched, #entropy < tau) for ENTROPY_EXIT,
- * capped at n).  n <= 2048. */
+ * capped at n).  Any n: up to 2048 candidates are sorted in one workgroup, more are
+ * placed by rank (each candidate counts the ones before it). */
 typedef struct { int32_t pos; int32_t token; float confidence; float entropy; } dfx_candidate;
 int dfx_select(const dfx_candidate * cand, int n, int remasking, float tau, int n_sched,
                int32_t * order, int32_t * n_unmask, void * stream);
@@ -236,6 +239,14 @@ int  dfx_context_new(const dfx_model * m, int n_ctx, dfx_context ** out);  /* di
 void dfx_context_free(dfx_context * c);
 /* tokens[n] (host) -> logits_out[n][n_vocab] (host), src/diffuse-graph.cpp:676-680 */
 int  dfx_forward(dfx_context * c, const int32_t * tokens, int n, float * logits_out);
+/* The cached forward of one denoising step (diffuse_forward_cached, src/diffuse-graph.h:32-41,
+ * src/diffuse-graph.cpp:596-673): the n_active rows at positions active_pos[] (distinct, in
+ * [0, n_total)) run through every layer; their K/V replace those positions in the context's
+ * cache (update_kv, src/diffuse-cache.h:124-140) and attention reads all n_total positions.
+ * The cache must hold a full forward of n_total tokens: the context's last call was dfx_forward
+ * with n = n_total, or dfx_forward_cached after it.  logits_out: [n_active][n_vocab] (host). */
+int  dfx_forward_cached(dfx_context * c, const int32_t * active_tokens, const int32_t * active_pos, int n_active,
+                        int n_total, float * logits_out);
 /* diffuse_generate (src/diffuse-sampler.cpp:373-380); out[n_generate] host. */
 int  dfx_generate(dfx_context * c, const int32_t * prompt, int n_prompt, int n_generate,
                   const dfx_sampler_params * p, int32_t * out, dfx_gen_stats * stats);

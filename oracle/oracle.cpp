@@ -351,16 +351,54 @@ static float dot_q8_0_q8_0(int64_t n, const blk_q8_0 * x, const blk_q8_0 * y) {
     return T;
 }
 
-static float dot_f16_f16(int64_t n, const uint16_t * x, const uint16_t * y) {
+/* F16 / F32 dots: f32 products (rounded to float, as GGML's scalar ggml_vec_dot_f16 /
+ * ggml_vec_dot_f32 form them) summed in double (ggml_float), in 16 interleaved lanes
+ * (lane l takes elements l, l+16, ...; the lanes are added in order at the end).  The
+ * lane order is this restatement's own (GGML's SIMD paths sum in float lanes of their own). */
+/* lanes added in order, then the tail (elements past the last whole 16) */
+static inline float dot_lanes_end(__m256d a0, __m256d a1, __m256d a2, __m256d a3, double tail) {
+    alignas(32) double v[16];
+    _mm256_store_pd(v, a0);
+    _mm256_store_pd(v + 4, a1);
+    _mm256_store_pd(v + 8, a2);
+    _mm256_store_pd(v + 12, a3);
     double s = 0.0;
-    for (int64_t i = 0; i < n; i++) s += (double)(orc_fp16_to_fp32(x[i]) * orc_fp16_to_fp32(y[i]));
-    return (float)s;
+    for (int l = 0; l < 16; l++) s += v[l];
+    return (float)(s + tail);
+}
+
+static float dot_f16_f16(int64_t n, const uint16_t * x, const uint16_t * y) {
+    __m256d a0 = _mm256_setzero_pd(), a1 = a0, a2 = a0, a3 = a0;
+    int64_t i = 0;
+    for (; i + 16 <= n; i += 16) {
+        const __m256 p0 = _mm256_mul_ps(_mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(x + i))),
+                                        _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(y + i))));
+        const __m256 p1 = _mm256_mul_ps(_mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(x + i + 8))),
+                                        _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(y + i + 8))));
+        a0 = _mm256_add_pd(a0, _mm256_cvtps_pd(_mm256_castps256_ps128(p0)));
+        a1 = _mm256_add_pd(a1, _mm256_cvtps_pd(_mm256_extractf128_ps(p0, 1)));
+        a2 = _mm256_add_pd(a2, _mm256_cvtps_pd(_mm256_castps256_ps128(p1)));
+        a3 = _mm256_add_pd(a3, _mm256_cvtps_pd(_mm256_extractf128_ps(p1, 1)));
+    }
+    double t = 0.0;
+    for (; i < n; i++) t += (double)(orc_fp16_to_fp32(x[i]) * orc_fp16_to_fp32(y[i]));
+    return dot_lanes_end(a0, a1, a2, a3, t);
 }
 
 static float dot_f32(int64_t n, const float * x, const float * y) {
-    double s = 0.0;
-    for (int64_t i = 0; i < n; i++) s += (double)(x[i] * y[i]);
-    return (float)s;
+    __m256d a0 = _mm256_setzero_pd(), a1 = a0, a2 = a0, a3 = a0;
+    int64_t i = 0;
+    for (; i + 16 <= n; i += 16) {
+        const __m256 p0 = _mm256_mul_ps(_mm256_loadu_ps(x + i), _mm256_loadu_ps(y + i));
+        const __m256 p1 = _mm256_mul_ps(_mm256_loadu_ps(x + i + 8), _mm256_loadu_ps(y + i + 8));
+        a0 = _mm256_add_pd(a0, _mm256_cvtps_pd(_mm256_castps256_ps128(p0)));
+        a1 = _mm256_add_pd(a1, _mm256_cvtps_pd(_mm256_extractf128_ps(p0, 1)));
+        a2 = _mm256_add_pd(a2, _mm256_cvtps_pd(_mm256_castps256_ps128(p1)));
+        a3 = _mm256_add_pd(a3, _mm256_cvtps_pd(_mm256_extractf128_ps(p1, 1)));
+    }
+    double t = 0.0;
+    for (; i < n; i++) t += (double)(x[i] * y[i]);
+    return dot_lanes_end(a0, a1, a2, a3, t);
 }
 
 /* Attention dot products: f32 x f32 products are exact in f64 and are summed in f64,

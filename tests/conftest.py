@@ -73,6 +73,21 @@ def gpu():
     return n
 
 
+def big_model(tag, arch, scheme, seed, sigma=0.02):
+    """GGUF of a benchmark-size architecture (random-init N(0, sigma), norms 1.0), written
+    once per machine under DFX_BENCH_DIR (default /tmp) with the benchmark's file naming,
+    so the benchmark and these tests share one generated file."""
+    import dfx
+    d = os.environ.get("DFX_BENCH_DIR", "/tmp")
+    p = os.path.join(d, f"dfx-{tag}-{scheme}-s{seed}.gguf")
+    stamp = p + ".ok"
+    if not (os.path.exists(p) and os.path.exists(stamp)):
+        dfx.synth_model(p, arch, scheme=scheme, seed=seed, sigma=sigma, n_threads=16)
+        with open(stamp, "w") as f:
+            f.write("ok\n")
+    return p
+
+
 def rel_l2(a, b):
     a = np.asarray(a, dtype=np.float64)
     b = np.asarray(b, dtype=np.float64)

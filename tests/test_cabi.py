@@ -107,8 +107,8 @@ def test_repack_layouts():
     assert np.array_equal(d8[:, 16:].reshape(-1, 8, 32), b8[:, :, 2:])
     q4 = dfx.quantize_rows(dfx.TYPE_Q4_K, x)
     assert np.array_equal(dfx.repack(dfx.TYPE_Q4_K, q4, rows, cols), q4)
-    f32 = dfx.repack(dfx.TYPE_F32, x.view(np.uint8), rows, cols)
-    assert np.array_equal(f32.view(np.float16).reshape(rows, cols), x.astype(np.float16))
+    f32 = dfx.repack(dfx.TYPE_F32, x.view(np.uint8), rows, cols)   # F32 matrices stay F32
+    assert np.array_equal(f32.view(np.float32).reshape(rows, cols), x)
     with pytest.raises(dfx.DfxError):
         dfx.repack(dfx.TYPE_Q4_K, q4, rows, 100)
 
