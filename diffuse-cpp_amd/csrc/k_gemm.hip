@@ -35,6 +35,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <type_traits>
 
 #define BK 128
@@ -1690,4 +1691,54 @@ extern "C" int dfx_gemm(int wtype, const void * w, int64_t N, int64_t K, const v
                         const float * bias, const float * residual, float * y, void * ws, void * stream) {
     return dfx_gemm_ex(wtype, w, N, K, act, M, bias, residual, y, N, nullptr, ws,
                        ws ? dfx_gemm_ws_bytes(M, N, K) : 0, stream, nullptr);
+}
+
+// ---------------------------------------------------------------------------
+// GEMM with a library-held split-K workspace (no allocation on any call)
+// ---------------------------------------------------------------------------
+// dfx_gemm takes its split-K workspace from the caller.  Callers that cannot allocate
+// device memory at all (code under stream capture, serving loops that forbid hipMalloc)
+// use dfx_gemm_noalloc instead: the workspace is `scratch`, a file-scope device array of
+// DFX_GEMM_SCRATCH_BYTES that every device holds from module load to process end.  Host
+// code never passes the array's name to a kernel (in host code it is only a stand-in
+// symbol): the device address comes from hipGetSymbolAddress, looked up once per device on
+// that device's first call and kept in scratch_ptr[device].
+#define DFX_GEMM_SCRATCH_BYTES (32u << 20)
+static __device__ __align__(256) uint8_t scratch[DFX_GEMM_SCRATCH_BYTES];
+
+#define DFX_MAX_DEVICES 64
+static void * scratch_ptr[DFX_MAX_DEVICES];
+static std::once_flag scratch_once[DFX_MAX_DEVICES];
+static hipError_t scratch_err[DFX_MAX_DEVICES];
+
+extern "C" int dfx_gemm_noalloc(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
+                                const float * bias, const float * residual, float * y, void * stream) {
+    int dev = -1;
+    const hipError_t ge = hipGetDevice(&dev);
+    if (ge != hipSuccess || dev < 0 || dev >= DFX_MAX_DEVICES) {
+        dfx_set_error("dfx_gemm_noalloc: no current device (%s)", hipGetErrorString(ge));
+        return DFX_ERR_HIP;
+    }
+    std::call_once(scratch_once[dev], [dev] {
+        void * p = nullptr;
+        scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        scratch_ptr[dev] = scratch_err[dev] == hipSuccess ? p : nullptr;
+    });
+    if (!scratch_ptr[dev]) {
+        dfx_set_error("dfx_gemm_noalloc: device %d scratch address: %s", dev, hipGetErrorString(scratch_err[dev]));
+        return DFX_ERR_HIP;
+    }
+    // the split-K partial slices (one per K chunk, every element written by its chunk's
+    // workgroups before the reduction reads it) must fit the scratch array
+    const size_t need = (size_t)std::max<int64_t>(M, 0) * (size_t)std::max<int64_t>(N, 0) *
+                        (size_t)dot_chunks(std::max<int64_t>(K, 1)) * sizeof(float);
+    if (need > DFX_GEMM_SCRATCH_BYTES) {
+        dfx_set_error("dfx_gemm_noalloc: M*N*chunks*4 = %zu bytes exceeds the %u-byte scratch (M=%lld N=%lld K=%lld)",
+                      need, DFX_GEMM_SCRATCH_BYTES, (long long)M, (long long)N, (long long)K);
+        return DFX_ERR_ARG;
+    }
+    // the same workspace size as dfx_gemm's (when it fits), so the same split is chosen
+    const size_t ws_bytes = std::min<size_t>(dfx_gemm_ws_bytes(M, N, K), DFX_GEMM_SCRATCH_BYTES);
+    return dfx_gemm_ex(wtype, w, N, K, act, M, bias, residual, y, N, nullptr, scratch_ptr[dev], ws_bytes, stream,
+                       nullptr);
 }

@@ -122,6 +122,16 @@ size_t dfx_gemm_ws_bytes(int64_t M, int64_t N, int64_t K);
 int dfx_gemm(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
              const float * bias, const float * residual, float * y, void * ws, void * stream);
 
+/* dfx_gemm without a workspace argument and without any allocation: the split-K partial
+ * sums go to a library-held device array of 32 MiB per GPU (held from the library's load to
+ * process end), so M * N * ceil(K / 2048) * 4 bytes must not exceed 32 MiB (DFX_ERR_ARG
+ * otherwise).  Same kernels and the same bits as dfx_gemm with a workspace.  Calls on one GPU
+ * share that array: calls that overlap in time on one GPU (several streams or host threads)
+ * race; serialise them.  No counterpart in the reference: for callers that cannot allocate
+ * device memory (code under stream capture, serving loops that forbid hipMalloc). */
+int dfx_gemm_noalloc(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
+                     const float * bias, const float * residual, float * y, void * stream);
+
 /* NEOX RoPE + cache store (src/diffuse-graph.cpp:71-79, 466-469; cache contents of
  * src/diffuse-cache.h:23-26 but at n_head_kv width — the GQA repeat of 84-95 is
  * index math in the attention kernel).  qkv: [M][(H + 2*Hkv)*hd] f32 (Q | K | V);
