@@ -7,6 +7,11 @@ One bench step = one diffuse_generate of 256 tokens (16 denoising steps).  Weigh
 are random-init N(0, 0.02) from seed 0 with norms 1.0, written as GGUF and
 quantised with the Q4_K_M mixture by the library's generator; the prompt is 32
 ids drawn uniformly from [0, 126000) with seed 1.  Prints one JSON line.
+
+Beside the headline: the other single-GPU workloads of the benchmark set (LLaDA-8B
+32 + 64 low_confidence without cache; Dream-7B 64 + 64 entropy_exit with cache; the
+sampler over a [256 x 126464] logits block), and the CPU baseline (the oracle, a
+restatement of the reference's CPU path, timed on this host).
 """
 import argparse
 import ctypes as C
@@ -25,43 +30,74 @@ import dfx  # noqa: E402
 B, PROMPT, STEPS = 256, 32, 16
 MFMA_F16_PEAK_TFLOPS = 2500.0      # MI355X dense f16 MFMA
 HBM_PEAK_GBS = 8000.0
+# The reference's published CPU rate: 1586 ms per Q4_K_M denoising step at 96 rows on a
+# 12-core EPYC 4465P (research/benchmark/RESULTS.md:50-54), 2 * 96 * 7.497e9 FLOP per step.
+GGML_GFLOPS_PER_CORE = 2.0 * 96 * 7.497e9 / 1.586 / 12 / 1e9
 
 
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
-def model_path(scheme, seed):
+def model_path(tag, scheme, seed):
     d = os.environ.get("DFX_BENCH_DIR", "/tmp")
-    return os.path.join(d, f"dfx-llada8b-{scheme}-s{seed}.gguf")
+    return os.path.join(d, f"dfx-{tag}-{scheme}-s{seed}.gguf")
 
 
-def ensure_model(scheme="q4_k_m", seed=0):
-    p = model_path(scheme, seed)
+def ensure_model(tag="llada8b", arch=None, scheme="q4_k_m", seed=0):
+    """Generated once per machine (the parity tests share the file naming)."""
+    p = model_path(tag, scheme, seed)
     stamp = p + ".ok"
     if not (os.path.exists(p) and os.path.exists(stamp)):
         t = time.time()
-        dfx.synth_model(p, dfx.LLADA_8B, scheme=scheme, seed=seed, sigma=0.02)
+        dfx.synth_model(p, arch or dfx.LLADA_8B, scheme=scheme, seed=seed, sigma=0.02, n_threads=16)
         open(stamp, "w").write("ok\n")
         log(f"generated {p} in {time.time() - t:.1f}s")
     return p
 
 
-def cpu_baseline(path, row_plan, head_plan, n_threads):
+def time_generations(ctx, prompt, n_gen, params, reps, warmup):
+    for _ in range(warmup):
+        ctx.generate(prompt, n_gen, params)
+    stats = dfx.GenStats()
+    dfx.sync()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        ctx.generate(prompt, n_gen, params, stats)
+    dfx.sync()
+    return (time.perf_counter() - t0) / reps, stats
+
+
+def cpu_baseline(path, row_plan, n_threads):
     """The CPU oracle (a restatement of the reference's GGML CPU path, run here as the
-    reference cannot be built) timed on this host, on a bounded sample: the full
-    L-layer forward plus vocab head over the 288-row step-0 sequence and the same with
-    one layer (each the better of two runs), and the sampler scan over 288 logits rows.
-    Per-row costs are scaled to the reference's row counts of every step (it runs the
-    head over all active rows)."""
+    reference cannot be built) timed on this host's cores, on a bounded sample:
+      * a whole 16-step generation (entropy_exit + cache, 32 + 256) of a two-layer model of
+        the LLaDA-8B width (vocab head, embedding and sampler at full size), timed end to end;
+      * the 32-layer and the 1-layer forward over the 288-row step-0 sequence, whose
+        difference gives the cost of one layer per row;
+    the full-depth generation = the two-layer one + 30 layers' cost at the rows of every
+    step.  Its GEMM rate per core is reported beside the reference's published rate."""
     sys.path.insert(0, os.path.join(REPO, "tests"))
     import oracle_py as O
+    spent = 0.0
+    # two-layer generate, timed
+    arch2 = dict(dfx.LLADA_8B, n_layer=2)
+    p2 = ensure_model("llada8b-2l", arch2, "q4_k_m", 0)
+    om2 = O.OracleModel(p2)
+    prompt = np.random.default_rng(1).integers(0, 126000, PROMPT).astype(np.int32)
+    t = time.perf_counter()
+    _, st = om2.generate(prompt, B, n_steps=STEPS, remasking=dfx.ENTROPY_EXIT, use_cache=True, seed=42,
+                         n_threads=n_threads)
+    t_gen2 = time.perf_counter() - t
+    spent += t_gen2
+    rows2 = [st.rows_per_step[i] for i in range(st.actual_steps)]
+    # per-layer-row cost from a 1-layer and the full-depth forward (better of two runs)
     om = O.OracleModel(path)
-    L_full = om.m.n_layer
+    L = om.m.n_layer
     M = PROMPT + B
     toks = np.random.default_rng(1).integers(0, 126000, M).astype(np.int32)
-    times, spent = {}, 0.0
-    for nl in (1, L_full):
+    times = {}
+    for nl in (1, L):
         om.m.n_layer = nl
         best = float("inf")
         for _ in range(2):
@@ -71,30 +107,95 @@ def cpu_baseline(path, row_plan, head_plan, n_threads):
             spent += dt
             best = min(best, dt)
         times[nl] = best
-    om.m.n_layer = L_full
-    t_layer_row = max(times[L_full] - times[1], 1e-9) / ((L_full - 1) * M)
-    t_head_row = max(times[1] - t_layer_row * M, 0.0) / M
-    rows = np.random.default_rng(4).standard_normal((M, om.dims["V"])).astype(np.float32) * 2
-    t = time.perf_counter()
-    for r in rows:
-        O.entropy(r)
-        O.top2(r)
-    dt = time.perf_counter() - t
-    spent += dt
-    t_samp_row = dt / M
-    total = sum(L_full * t_layer_row * m + t_head_row * h for m, h in zip(row_plan, head_plan))
-    total += t_samp_row * sum(head_plan)
+    om.m.n_layer = L
+    t_layer_row = max(times[L] - times[1], 1e-9) / ((L - 1) * M)
+    total = t_gen2 + (L - 2) * t_layer_row * sum(rows2)
     gflop_layer = 2.0 * (4 * 4096 * 4096 + 3 * 4096 * 12288) * M / 1e9
+    gflops_core = gflop_layer / max(t_layer_row * M, 1e-9) / n_threads
+    value = B / total
     return {
-        "value": round(B / total, 4), "unit": "tok/s", "cores": n_threads, "kind": "port",
-        "sample": (f"oracle (GGML-semantics C++ restatement, {n_threads} threads): the {L_full}-layer and the "
-                   f"1-layer forward + vocab head over the {M}-row step-0 sequence (better of 2 runs each) and "
-                   f"the sampler scan of {M} rows, {spent:.1f}s of CPU time in all; per-row costs scaled to the "
-                   f"reference's rows per step {row_plan} (head over all active rows)"),
-        "ms_per_denoise_step": round(1000 * total / len(row_plan), 1),
-        "step0_forward_s": round(times[L_full], 3),
-        "layer_gflops_per_core": round(gflop_layer / max(t_layer_row * M, 1e-9) / n_threads, 2),
+        "value": round(value, 4), "unit": "tok/s", "cores": n_threads, "kind": "port",
+        "sample": (f"oracle (GGML-semantics C++ restatement, {n_threads} threads, AVX2 integer block dots): "
+                   f"a whole 16-step generate (entropy_exit + cache, 32 + 256) of a 2-layer LLaDA-8B-width "
+                   f"model timed end to end ({t_gen2:.1f}s, rows {rows2}), plus 30 layers at those rows from "
+                   f"the 32- and 1-layer 288-row forwards (better of 2 each); {spent:.1f}s of CPU time in all"),
+        "two_layer_generate_s": round(t_gen2, 2),
+        "step0_forward_s": round(times[L], 3),
+        "ms_per_denoise_step": round(1000 * total / STEPS, 1),
+        "layer_gflops_per_core": round(gflops_core, 2),
+        "reference_published_gflops_per_core": round(GGML_GFLOPS_PER_CORE, 2),
+        # the same generation at the reference's published per-core GEMM rate on these cores
+        "value_at_reference_rate": round(value * GGML_GFLOPS_PER_CORE / gflops_core, 4),
     }
+
+
+def config_llada_b64(model):
+    """LLaDA-8B Q4_K_M, 32 + 64 masks, low_confidence, no cache, 16 steps (96 rows a step)."""
+    prompt = np.random.default_rng(1).integers(0, 126000, 32).astype(np.int32)
+    ctx = dfx.Context(model, 96)
+    params = dfx.SamplerParams.make(n_steps=16, remasking=dfx.LOW_CONFIDENCE, use_cache=False, seed=42)
+    sec, st = time_generations(ctx, prompt, 64, params, 3, 1)
+    ctx.close()
+    return {"workload": "LLaDA-8B Q4_K_M, prompt 32 + B=64, 16 steps, low_confidence, no cache",
+            "tok_s": round(64 / sec, 2), "ms_per_generation": round(1000 * sec, 3),
+            "ms_per_denoise_step": round(st.forward_ms / max(st.actual_steps, 1), 3),
+            "rows_per_step": [st.rows_per_step[i] for i in range(st.actual_steps)]}
+
+
+def config_dream():
+    """Dream-7B Q4_K_M, 64 + 64 masks, entropy_exit + cache, 16 steps."""
+    path = ensure_model("dream7b", dfx.DREAM_7B, "q4_k_m", 2)
+    model = dfx.Model(path)
+    prompt = np.random.default_rng(3).integers(0, 151643, 64).astype(np.int32)
+    ctx = dfx.Context(model, 128)
+    params = dfx.SamplerParams.make(n_steps=16, remasking=dfx.ENTROPY_EXIT, use_cache=True, seed=42,
+                                    entropy_threshold=1.5)
+    sec, st = time_generations(ctx, prompt, 64, params, 3, 1)
+    ctx.close()
+    model.close()
+    steps = [round(st.step_ms[i], 3) for i in range(st.actual_steps)]
+    return {"workload": "Dream-7B Q4_K_M, prompt 64 + B=64, 16 steps, entropy_exit + inter-step KV cache",
+            "tok_s": round(64 / sec, 2), "ms_per_generation": round(1000 * sec, 3),
+            "ms_per_denoise_step_full": steps[0] if steps else None,
+            "ms_per_denoise_step_cached_mean": round(float(np.mean(steps[1:])), 3) if len(steps) > 1 else None,
+            "rows_per_step": [st.rows_per_step[i] for i in range(st.actual_steps)]}
+
+
+def config_sampler():
+    """The sampler over [256 x 126464] f32 logits N(0, sigma), sigma in {0.5, 2, 8} (seed 4):
+    row statistics (softmax max / sum, entropy, top-2), candidate records and the selection
+    of the 16 to unmask (256 / 16), on device.  HBM rate of the statistics pass: the logits
+    block read once (129.5 MB) over its time."""
+    R, V, L = 256, 126464, dfx.lib
+    rows = dfx.Buf.of(np.arange(R, dtype=np.int32))
+    pos = dfx.Buf.of(np.arange(R, dtype=np.int32) + 32)
+    st, cand, order, nun = dfx.Buf(R * 16), dfx.Buf(R * 16), dfx.Buf(R * 4), dfx.Buf(4)
+    out = {}
+    for sigma in (0.5, 2.0, 8.0):
+        x = dfx.Buf.of(np.random.default_rng(4).standard_normal((R, V), dtype=np.float32) * np.float32(sigma))
+
+        def run():
+            dfx.check(L().dfx_row_stats(x.ptr, V, rows.ptr, R, V, st.ptr, None), "row_stats")
+            dfx.check(L().dfx_make_candidates(st.ptr, pos.ptr, R, 0, cand.ptr, None), "candidates")
+            dfx.check(L().dfx_select(cand.ptr, R, dfx.ENTROPY_EXIT, 1.5, R // 16, order.ptr, nun.ptr, None), "select")
+
+        def timed(fn, reps=20):
+            for _ in range(3):
+                fn()
+            tm, ms = C.c_void_p(), C.c_float()
+            dfx.check(L().dfx_timer_start(C.byref(tm), None), "timer")
+            for _ in range(reps):
+                fn()
+            dfx.check(L().dfx_timer_stop(tm, None, C.byref(ms)), "timer")
+            return 1000.0 * ms.value / reps
+        total_us = timed(run)
+        stats_us = timed(lambda: dfx.check(L().dfx_row_stats(x.ptr, V, rows.ptr, R, V, st.ptr, None), "row_stats"))
+        gbs = R * V * 4 / (stats_us * 1e-6) / 1e9
+        out[f"sigma_{sigma:g}"] = {"us_per_step": round(total_us, 2), "row_stats_us": round(stats_us, 2),
+                                   "row_stats_gbs": round(gbs, 1), "frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        del x
+    return {"workload": "sampler: [256 x 126464] f32 logits N(0, sigma), stats + candidates + select 16",
+            "results": out}
 
 
 def committed_traffic():
@@ -117,6 +218,7 @@ def main():
     ap.add_argument("--steps", type=int, default=3, help="timed diffuse_generate calls")
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-configs", action="store_true", help="skip the other workloads")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 3 device-to-device copies of 512 MiB (reference kernel for the "
@@ -158,6 +260,7 @@ def main():
         ctx.generate(prompt, B, params, stats)
     dfx.sync()
     elapsed = time.perf_counter() - t0
+    log(f"timed {args.steps} generations: {1000 * elapsed / args.steps:.2f} ms each")
     # The same K generations again with a HIP event pair around every GEMM launch on the
     # engine stream: the roofline's average launch time comes from these events.  The
     # event packets slow the stream a little, so this pass does not give `value`.
@@ -172,6 +275,7 @@ def main():
     q4_big = ctx.profile_read(dfx.TYPE_Q4_K, 1)     # M > 96: MFMA-bound shapes (mostly k_q4k_w<1, 2>)
     q4_small = ctx.profile_read(dfx.TYPE_Q4_K, 2)   # M <= 96: weight-bandwidth-bound shapes
     ctx.profile(False)
+    ctx.close()
 
     steps_done = stats.actual_steps
     rows = [stats.rows_per_step[i] for i in range(steps_done)]
@@ -182,16 +286,26 @@ def main():
     achieved_all = q4["flops"] / (q4["ms"] * 1e-3) / 1e12 if q4["ms"] > 0 else 0.0
     small_gbs = q4_small["bytes"] / (q4_small["ms"] * 1e-3) / 1e9 if q4_small["ms"] > 0 else 0.0
 
-    # the reference runs the vocab head over every active row; its row counts per step
-    masked, head_plan = B, []
-    for s in range(steps_done):
-        head_plan.append(rows[s])
-        masked -= stats.unmasked_per_step[s]
+    configs = None
+    if not args.no_configs:
+        configs = {}
+        t = time.time()
+        configs["llada8b_q4km_b64_low_confidence_no_cache"] = config_llada_b64(model)
+        log(f"B=64 workload took {time.time() - t:.1f}s")
+    model.close()
+    if configs is not None:
+        t = time.time()
+        configs["dream7b_q4km_b64_entropy_exit_cache"] = config_dream()
+        log(f"Dream workload took {time.time() - t:.1f}s")
+        t = time.time()
+        configs["sampler_256x126464"] = config_sampler()
+        log(f"sampler workload took {time.time() - t:.1f}s")
+
     cpu = None
     if not args.no_cpu:
         n_thr = args.cpu_threads or min(os.cpu_count() or 1, 16)
         t = time.time()
-        cpu = cpu_baseline(path, rows, head_plan, n_thr)
+        cpu = cpu_baseline(path, rows, n_thr)
         log(f"cpu baseline leg took {time.time() - t:.1f}s")
 
     out = {
@@ -235,12 +349,12 @@ def main():
                            "avg_launch_us": round(1000 * q4_small["ms"] / max(q4_small["launches"], 1), 3)},
         },
         "cpu_baseline": cpu,
+        "other_workloads": configs,
     }
     if cpu:
         out["vs_cpu"] = round(out["value"] / cpu["value"], 1)
+        out["vs_cpu_at_reference_rate"] = round(out["value"] / cpu["value_at_reference_rate"], 1)
     print(json.dumps(out))
-    ctx.close()
-    model.close()
 
 
 if __name__ == "__main__":

@@ -506,87 +506,154 @@ __global__ void __launch_bounds__(256, 2) k_attn_split(const float * __restrict_
     }
 }
 
-// VALU form for key counts whose score rows do not fit the matrix-core kernel's LDS:
-// TQ query rows of one head per workgroup (256 threads), full score rows in LDS.
-template <int HD, int TQ>
-__global__ void __launch_bounds__(256) k_attention(const float * __restrict__ q, const float * __restrict__ kc,
+// Exact form for any key count: the score rows are not kept (they need not fit the LDS);
+// each 16-key score tile is recomputed in three passes over the keys, with the same
+// products, sums and rounding as k_attn_mfma's phase 1, so every pass sees the same scores:
+//   pass 1: row maxima;
+//   pass 2: e = exp(s - max) (correctly rounded), sums in double, inv = (float)(1 / sum);
+//   pass 3: per block of 64 keys, the four waves' probability tiles p = e * inv go through
+//           LDS and each wave adds P V for its value columns on the f64 MFMA.
+// One head and 16 query rows per workgroup (4 waves); wave w takes the score tile 4b + w of
+// key block b.  Keys past n_keys score -inf (no weight) and read as zero values.
+#define LONG_PSTR 68   // LDS floats per probability row of a 64-key block (16-byte aligned rows)
+template <int HD>
+__global__ void __launch_bounds__(256) k_attn_long(const float * __restrict__ q, const float * __restrict__ kc,
                                                    const float * __restrict__ vt, int64_t v_ld, int M, int n_keys,
-                                                   int H, int Hkv, float * __restrict__ out) {
+                                                   int H, int Hkv, int q_tiles, float * __restrict__ out) {
 #pragma clang fp contract(off)
-    extern __shared__ float smem[];
-    float * Qs = smem;                 // [TQ][HD]
-    float * S = smem + TQ * HD;        // [TQ][n_keys]
-    const int h = blockIdx.y, kvh = h / (H / Hkv);
-    const int q0 = blockIdx.x * TQ;
-    const int nq = min(TQ, M - q0);
+    __shared__ __attribute__((aligned(16))) float P[16 * LONG_PSTR];
+    __shared__ float red_f[4][16];
+    __shared__ double red_d[4][16];
+    constexpr int SS = HD / 16, CT = HD / 64;
+    const int L = blockIdx.x, xcd = L & 7, j = L >> 3;
+    const int h = 8 * (j / q_tiles) + xcd, qt = j % q_tiles;
+    if (h >= H) return;
+    const int kvh = h / (H / Hkv);
+    const int q0 = qt * 16;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int64_t kvstride = (int64_t)Hkv * HD;
     const float scale = 1.0f / sqrtf((float)HD);
+    const int ntiles = (n_keys + 15) >> 4, nblocks = (ntiles + 3) >> 2;
 
-    for (int i = tid; i < TQ * HD; i += 256) {
-        const int r = i / HD, j = i - r * HD;
-        Qs[i] = (r < nq) ? q[((int64_t)(q0 + r) * H + h) * HD + j] : 0.0f;
+    float4 qf[SS];
+    {
+        const int row = q0 + li;
+        const float * qr = q + ((int64_t)min(row, M - 1) * H + h) * HD + 4 * lg;
+#pragma unroll
+        for (int s = 0; s < SS; s++) qf[s] = ld4_or0(qr + 16 * s, row < M);
+    }
+    const float * kbase = kc + (int64_t)kvh * HD + 4 * lg;
+    // scores of tile t for rows lg + 4i, key 16t + li (-inf past the keys)
+    auto scores = [&](int t, float (&sc)[4]) __attribute__((always_inline)) {
+        const int n = 16 * t + li;
+        const float * kr = kbase + (int64_t)min(n, n_keys - 1) * kvstride;
+        float4 kf[SS];
+#pragma unroll
+        for (int s = 0; s < SS; s++) kf[s] = ld4_or0(kr + 16 * s, n < n_keys);
+        double4v a[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int s = 0; s < SS; s++) {
+            const float kb[4] = {kf[s].x, kf[s].y, kf[s].z, kf[s].w};
+            const float qa[4] = {qf[s].x, qf[s].y, qf[s].z, qf[s].w};
+#pragma unroll
+            for (int c = 0; c < 4; c++) a[c] = mfma_f64((double)qa[c], (double)kb[c], a[c]);
+        }
+        const double4v acc = (a[0] + a[1]) + (a[2] + a[3]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) sc[i] = n < n_keys ? (float)acc[i] * scale : -INFINITY;
+    };
+
+    // ---- pass 1: row maxima (lane: rows lg + 4i)
+    float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    for (int t = wv; t < ntiles; t += 4) {
+        float sc[4];
+        scores(t, sc);
+#pragma unroll
+        for (int i = 0; i < 4; i++) mx[i] = fmaxf(mx[i], sc[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        for (int o = 8; o > 0; o >>= 1) mx[i] = fmaxf(mx[i], __shfl_xor(mx[i], o, WAVE));   // over li
+        if (li == 0) red_f[wv][lg + 4 * i] = mx[i];
     }
     __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = lg + 4 * i;
+        mx[i] = fmaxf(fmaxf(red_f[0][r], red_f[1][r]), fmaxf(red_f[2][r], red_f[3][r]));
+    }
 
-    for (int n = tid; n < n_keys; n += 256) {
-        const float * kr = kc + ((int64_t)n * Hkv + kvh) * HD;
-        double acc[TQ];
+    // ---- pass 2: sums of e = exp(s - max) in double
+    double sum[4] = {0.0, 0.0, 0.0, 0.0};
+    for (int t = wv; t < ntiles; t += 4) {
+        float sc[4];
+        scores(t, sc);
 #pragma unroll
-        for (int r = 0; r < TQ; r++) acc[r] = 0.0;
-        for (int d0 = 0; d0 < HD; d0 += 16) {
-            float kv[16];
+        for (int i = 0; i < 4; i++) sum[i] += (double)(float)exp((double)(sc[i] - mx[i]));
+    }
 #pragma unroll
-            for (int j = 0; j < 16; j += 4) {
-                const float4 t = *(const float4 *)(kr + d0 + j);
-                kv[j] = t.x; kv[j + 1] = t.y; kv[j + 2] = t.z; kv[j + 3] = t.w;
+    for (int i = 0; i < 4; i++) {
+        for (int o = 8; o > 0; o >>= 1) sum[i] += __shfl_xor(sum[i], o, WAVE);
+        if (li == 0) red_d[wv][lg + 4 * i] = sum[i];
+    }
+    __syncthreads();
+    float inv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = lg + 4 * i;
+        inv[i] = (float)(1.0 / (((red_d[0][r] + red_d[1][r]) + red_d[2][r]) + red_d[3][r]));
+    }
+
+    // ---- pass 3: O = P V, one 64-key block at a time
+    double4v o[CT][2];
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) o[ct][0] = o[ct][1] = 0.0;
+    const float * vb = vt + ((int64_t)kvh * HD + 16 * wv + li) * v_ld;
+    for (int b = 0; b < nblocks; b++) {
+        const int t = 4 * b + wv;
+        float sc[4];
+        scores(min(t, ntiles - 1), sc);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float e = (float)exp((double)(sc[i] - mx[i]));
+            P[(lg + 4 * i) * LONG_PSTR + 16 * wv + li] = t < ntiles ? e * inv[i] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int n = 64 * b + 16 * s + 4 * lg;          // first of this lane's 4 keys
+            const float4 pf = *(const float4 *)(P + li * LONG_PSTR + 16 * s + 4 * lg);
+            const float pa[4] = {pf.x, pf.y, pf.z, pf.w};
+            float4 vv[CT];
+#pragma unroll
+            for (int ct = 0; ct < CT; ct++) {
+                // in-row address (v_ld is a multiple of 16, so a row holds whole 16-key steps
+                // of the cache); keys past the sequence read as zero
+                const f32x4 v = *(const f32x4 *)(vb + (int64_t)64 * ct * v_ld + min(n, (int)v_ld - 4));
+                vv[ct] = make_float4(n < n_keys ? v.x : 0.0f, n + 1 < n_keys ? v.y : 0.0f,
+                                     n + 2 < n_keys ? v.z : 0.0f, n + 3 < n_keys ? v.w : 0.0f);
             }
 #pragma unroll
-            for (int r = 0; r < TQ; r++) {
-                double a = acc[r];
+            for (int c = 0; c < 4; c++) {
+                const double a = (double)pa[c];
 #pragma unroll
-                for (int j = 0; j < 16; j++) a += (double)kv[j] * (double)Qs[r * HD + d0 + j];
-                acc[r] = a;
+                for (int ct = 0; ct < CT; ct++) {
+                    const float vvv[4] = {vv[ct].x, vv[ct].y, vv[ct].z, vv[ct].w};
+                    o[ct][c & 1] = mfma_f64(a, (double)vvv[c], o[ct][c & 1]);
+                }
             }
         }
-#pragma unroll
-        for (int r = 0; r < TQ; r++) S[r * n_keys + n] = (float)acc[r] * scale;
-    }
-    __syncthreads();
-
-    for (int r = wv; r < nq; r += 4) {
-        float * sr = S + r * n_keys;
-        float mx = -INFINITY;
-        for (int n = lane; n < n_keys; n += 64) mx = fmaxf(mx, sr[n]);
-        mx = wave_max(mx);
-        double sum = 0.0;
-        for (int n = lane; n < n_keys; n += 64) {
-            const float e = (float)exp((double)(sr[n] - mx));
-            sr[n] = e;
-            sum += (double)e;
-        }
-        sum = wave_sum_d(sum);
-        const float inv = (float)(1.0 / sum);
-        for (int n = lane; n < n_keys; n += 64) sr[n] = sr[n] * inv;
-    }
-    __syncthreads();
-
-    constexpr int G = 256 / HD;
-    constexpr int RP = (TQ + G - 1) / G;      // query rows per thread
-    const int j = tid % HD, g = tid / HD;
-    const int r0 = g * RP;
-    if (r0 >= TQ) return;
-    double acc[RP];
-#pragma unroll
-    for (int r = 0; r < RP; r++) acc[r] = 0.0;
-    const float * vcol = vt + ((int64_t)kvh * HD + j) * v_ld;
-    for (int n = 0; n < n_keys; n++) {
-        const double v = (double)vcol[n];
-#pragma unroll
-        for (int r = 0; r < RP; r++) acc[r] += v * (double)S[(r0 + r) * n_keys + n];
+        __syncthreads();
     }
 #pragma unroll
-    for (int r = 0; r < RP; r++)
-        if (r0 + r < nq) out[(int64_t)(q0 + r0 + r) * H * HD + (int64_t)h * HD + j] = (float)acc[r];
+    for (int i = 0; i < 4; i++) {
+        const int row = q0 + lg + 4 * i;
+        if (row >= M) continue;
+#pragma unroll
+        for (int ct = 0; ct < CT; ct++)
+            out[(int64_t)row * H * HD + (int64_t)h * HD + 16 * wv + 64 * ct + li] = (float)(o[ct][0][i] + o[ct][1][i]);
+    }
 }
 
 extern "C" int dfx_rope_store(const float * qkv, const int32_t * pos, int64_t M, int H, int Hkv, int hd,
@@ -615,8 +682,6 @@ extern "C" int dfx_rope_store(const float * qkv, const int32_t * pos, int64_t M,
     DFX_CHECK_LAUNCH("dfx_rope_store");
     return DFX_OK;
 }
-
-#define ATTN_LDS_MAX (64 * 1024)
 
 // LDS a workgroup may use on the current device (160 KB on gfx950), read once per device
 // (contexts on several host threads may ask at once).
@@ -654,9 +719,9 @@ extern "C" int dfx_attention_ex(const float * q, const float * kc, const float *
         return DFX_ERR_ARG;
     }
     if (M < 0 || n_keys <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || (hd != 64 && hd != 128) || v_ld < n_keys ||
-        (v_ld % 4)) {
+        (v_ld % 16) || M > INT32_MAX || n_keys > INT32_MAX) {
         dfx_set_error("dfx_attention: unsupported shape M=%lld keys=%lld H=%d Hkv=%d hd=%d v_ld=%lld "
-                      "(v_ld must be a multiple of 4, >= keys)", (long long)M, (long long)n_keys, H, Hkv, hd,
+                      "(v_ld must be a multiple of 16, >= keys)", (long long)M, (long long)n_keys, H, Hkv, hd,
                       (long long)v_ld);
         return DFX_ERR_UNSUPPORTED;
     }
@@ -677,37 +742,26 @@ extern "C" int dfx_attention_ex(const float * q, const float * kc, const float *
             DFX_CHECK_LAUNCH("dfx_attention");
             return DFX_OK;
         }
-        // longer score rows: the f64 forms below (16-row tiles, then the VALU kernel)
+        // longer score rows: the exact forms below
     }
     const int sstride = attn_sstride(n_keys);
     const size_t lds = (size_t)16 * sstride * sizeof(float);
+    const int q_tiles = (int)((M + 15) / 16);
+    const dim3 grid((unsigned)(8 * ((H + 7) / 8) * q_tiles));
     if (lds <= attn_lds_limit()) {
-        const int q_tiles = (int)((M + 15) / 16);
-        const dim3 grid((unsigned)(8 * ((H + 7) / 8) * q_tiles));
         if (hd == 128)
             hipLaunchKernelGGL((k_attn_mfma<128>), grid, dim3(256), lds, st, q, kc, vt, v_ld, (int)M, (int)n_keys, H,
                                Hkv, sstride, q_tiles, out);
         else
             hipLaunchKernelGGL((k_attn_mfma<64>), grid, dim3(256), lds, st, q, kc, vt, v_ld, (int)M, (int)n_keys, H,
                                Hkv, sstride, q_tiles, out);
-        DFX_CHECK_LAUNCH("dfx_attention");
-        return DFX_OK;
+    } else if (hd == 128) {   // score rows longer than the LDS holds: recomputed in three passes
+        hipLaunchKernelGGL((k_attn_long<128>), grid, dim3(256), 0, st, q, kc, vt, v_ld, (int)M, (int)n_keys, H, Hkv,
+                           q_tiles, out);
+    } else {
+        hipLaunchKernelGGL((k_attn_long<64>), grid, dim3(256), 0, st, q, kc, vt, v_ld, (int)M, (int)n_keys, H, Hkv,
+                           q_tiles, out);
     }
-    int TQ = 32;
-    while (TQ > 1 && (size_t)TQ * (hd + n_keys) * sizeof(float) > ATTN_LDS_MAX) TQ >>= 1;
-    const size_t lds2 = (size_t)TQ * (hd + n_keys) * sizeof(float);
-    if (lds2 > ATTN_LDS_MAX) {
-        dfx_set_error("dfx_attention: %lld keys exceed the LDS score row", (long long)n_keys);
-        return DFX_ERR_UNSUPPORTED;
-    }
-    dim3 grid((unsigned)((M + TQ - 1) / TQ), (unsigned)H);
-#define ATTN_CASE(HD_, TQ_)                                                                                \
-    if (hd == HD_ && TQ == TQ_)                                                                            \
-        hipLaunchKernelGGL((k_attention<HD_, TQ_>), grid, dim3(256), lds2, st, q, kc, vt, v_ld, (int)M,   \
-                           (int)n_keys, H, Hkv, out);
-    ATTN_CASE(128, 32) ATTN_CASE(128, 16) ATTN_CASE(128, 8) ATTN_CASE(128, 4) ATTN_CASE(128, 2) ATTN_CASE(128, 1)
-    ATTN_CASE(64, 32) ATTN_CASE(64, 16) ATTN_CASE(64, 8) ATTN_CASE(64, 4) ATTN_CASE(64, 2) ATTN_CASE(64, 1)
-#undef ATTN_CASE
     DFX_CHECK_LAUNCH("dfx_attention");
     return DFX_OK;
 }

@@ -195,9 +195,13 @@ __global__ void k_make_candidates(const dfx_row_stat * __restrict__ st, const in
     out[i] = c;
 }
 
-int dfx_make_candidates(const dfx_row_stat * stats, const int32_t * pos, int n, int margin, dfx_candidate * out,
-                        void * stream) {
-    if (n <= 0) return DFX_OK;
+extern "C" int dfx_make_candidates(const dfx_row_stat * stats, const int32_t * pos, int n, int margin,
+                                   dfx_candidate * out, void * stream) {
+    if (n < 0 || (n > 0 && (!stats || !pos || !out))) {
+        dfx_set_error("dfx_make_candidates: bad arguments (n=%d)", n);
+        return DFX_ERR_ARG;
+    }
+    if (n == 0) return DFX_OK;
     hipLaunchKernelGGL(k_make_candidates, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, stats,
                        pos, n, margin, out);
     DFX_CHECK_LAUNCH("dfx_make_candidates");

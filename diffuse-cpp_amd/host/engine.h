@@ -24,8 +24,6 @@ int dfx_rmsnorm_convert_ex(int wtype, const float * x, const int32_t * xmap, con
 int dfx_rmsnorm_convert_add(int wtype, float * x, const int32_t * xmap, const float * part, int n_part,
                             int64_t part_rows, const float * w, int64_t M, int64_t K, float eps, void * act,
                             void * stream);
-int dfx_make_candidates(const dfx_row_stat * stats, const int32_t * pos, int n, int margin, dfx_candidate * out,
-                        void * stream);
 extern "C" void dfx_set_error(const char * fmt, ...);
 
 // A weight matrix in the device layout of dfx.h: rows x cols, rows of super-blocks.

@@ -143,8 +143,9 @@ int dfx_rope_store(const float * qkv, const int32_t * pos, int64_t M, int H, int
 
 /* Bidirectional attention, no mask (src/diffuse-graph.cpp:97-119 / 528-553):
  * out[m][h*hd + j] = sum_n softmax_n(q_m . k_n / sqrt(hd)) * v_n[j], keys 0..n_keys-1
- * of the cache (kc[n][Hkv][hd], vt[Hkv][hd][v_ld], n_keys <= v_ld), query head h
- * reads KV head h / (H/Hkv). */
+ * of the cache (kc[n][Hkv][hd], vt[Hkv][hd][v_ld], n_keys <= v_ld, v_ld a multiple of
+ * 16), query head h reads KV head h / (H/Hkv).  Any number of keys: score rows that do not
+ * fit the LDS are recomputed instead of stored. */
 int dfx_attention(const float * q, const float * kc, const float * vt, int64_t v_ld, int64_t M, int64_t n_keys,
                   int H, int Hkv, int hd, float * out, void * stream);   /* mode DFX_ATTN_EXACT */
 
@@ -174,6 +175,13 @@ typedef struct {
 int dfx_row_stats(const float * logits, int64_t ld, const int32_t * rows, int64_t n_rows, int64_t V,
                   dfx_row_stat * out, void * stream);
 
+/* Candidate records of masked positions from their row statistics (the push at
+ * src/diffuse-sampler.cpp:253-255): {pos[i], argmax, confidence, entropy} with confidence =
+ * the top-1 logit, or top-1 minus top-2 when margin != 0 (TOPK_MARGIN). */
+typedef struct { int32_t pos; int32_t token; float confidence; float entropy; } dfx_candidate;
+int dfx_make_candidates(const dfx_row_stat * stats, const int32_t * pos, int n, int margin, dfx_candidate * out,
+                        void * stream);
+
 /* Remask selection (src/diffuse-sampler.cpp:277-305): orders n candidates by the
  * policy's key (ENTROPY_EXIT: entropy ascending; LOW_CONFIDENCE / MASKGIT_PLUS:
  * top-1 logit descending; TOPK_MARGIN: top1-top2 descending), ties by position
@@ -181,7 +189,6 @@ int dfx_row_stats(const float * logits, int64_t ld, const int32_t * rows, int64_
  * unmask (schedule count n_sched, or max(n_sched, #entropy < tau) for ENTROPY_EXIT,
  * capped at n).  Any n: up to 2048 candidates are sorted in one workgroup, more are
  * placed by rank (each candidate counts the ones before it). */
-typedef struct { int32_t pos; int32_t token; float confidence; float entropy; } dfx_candidate;
 int dfx_select(const dfx_candidate * cand, int n, int remasking, float tau, int n_sched,
                int32_t * order, int32_t * n_unmask, void * stream);
 

@@ -252,7 +252,9 @@ def test_rope_store_matches_oracle(gpu, M, H, Hkv, hd, n_ctx):
 
 ATTN_SHAPES = [(288, 288, 32, 32, 128), (50, 288, 32, 32, 128), (128, 128, 28, 4, 128), (7, 768, 8, 2, 64),
                (3, 2000, 4, 4, 128), (2, 3000, 2, 1, 128), (17, 1, 4, 4, 128), (33, 21, 4, 2, 64),
-               (768, 768, 32, 32, 128), (256, 768, 32, 32, 128), (65, 97, 6, 3, 64), (1, 33, 2, 2, 128)]
+               (768, 768, 32, 32, 128), (256, 768, 32, 32, 128), (65, 97, 6, 3, 64), (1, 33, 2, 2, 128),
+               # score rows longer than the LDS holds (three-pass form), past 16k keys, both head sizes
+               (19, 40000, 2, 1, 128), (5, 9000, 4, 2, 64)]
 
 
 def attention_case(M, n_keys, H, Hkv, hd, mode):
