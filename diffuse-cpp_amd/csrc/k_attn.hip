@@ -101,8 +101,11 @@ __global__ void __launch_bounds__(256) k_rope_store(const float * __restrict__ q
 //   s = dot(k, q) * (1/sqrtf(hd));  max;  e = exp(s - max);  sum in double;
 //   p = e * (float)(1/sum);  out = sum_n v_n * p_n.
 // f32 x f32 products are exact in f64; the dot products and the P.V sums are
-// accumulated in f64 and rounded to float once, so the float result does not
-// depend on the summation order.  exp is correctly rounded.
+// accumulated in f64 and rounded to float once.  f64 addition is not associative,
+// so the float result depends on the summation order only when two orders' f64
+// sums fall on either side of a float rounding boundary: measured about one
+// element in 10^6-10^7 differing by one float ulp from a sequential f64 sum.
+// exp is correctly rounded.
 
 typedef double double4v __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -115,6 +118,17 @@ __device__ __forceinline__ float4 ld4_or0(const float * p, bool keep) {
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
     const f32x4 r = keep ? v : z;
     return make_float4(r.x, r.y, r.z, r.w);
+}
+
+// Causal mask (src/ar-graph.cpp:70-88): with q_pos0 >= 0, query row r sits at position
+// q_pos0 + r and sees the keys lo..hi, hi = its position, lo = hi - window + 1 with a
+// window (> 0), else 0.  q_pos0 < 0: every key is visible.  Rows past M (tile padding)
+// take the last row's range, so every row keeps a visible key.
+struct key_range { int lo, hi; };
+__device__ __forceinline__ key_range row_keys(int row, int M, int n_keys, int q_pos0, int window) {
+    if (q_pos0 < 0) return {0, n_keys - 1};
+    const int hi = min(q_pos0 + min(row, M - 1), n_keys - 1);
+    return {window > 0 ? max(hi - window + 1, 0) : 0, hi};
 }
 
 // v_mfma_f64_16x16x4f64: D[16][16] += A[16][4] B[4][16].
@@ -136,7 +150,7 @@ __device__ __forceinline__ double4v mfma_f64(double a, double b, double4v c) {
 template <int HD>
 __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q, const float * __restrict__ kc,
                                                    const float * __restrict__ vt, int64_t v_ld, int M, int n_keys,
-                                                   int H, int Hkv, int sstride, int q_tiles,
+                                                   int H, int Hkv, int sstride, int q_tiles, int q_pos0, int window,
                                                    float * __restrict__ out) {
 #pragma clang fp contract(off)
     extern __shared__ float S[];       // [16][sstride] scores, then probabilities
@@ -181,8 +195,13 @@ __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q,
             for (int c = 0; c < 4; c++) a[c] = mfma_f64((double)qa[c], (double)kb[c], a[c]);
         }
         const double4v acc = (a[0] + a[1]) + (a[2] + a[3]);
+        const int n = 16 * t + li;
 #pragma unroll
-        for (int i = 0; i < 4; i++) S[(lg + 4 * i) * sstride + 16 * t + li] = (float)acc[i] * scale;
+        for (int i = 0; i < 4; i++) {
+            // masked keys score -inf: weight exactly 0 in the sums below
+            const key_range kr = row_keys(q0 + lg + 4 * i, M, n_keys, q_pos0, window);
+            S[(lg + 4 * i) * sstride + n] = n >= kr.lo && n <= kr.hi ? (float)acc[i] * scale : -INFINITY;
+        }
     };
 #pragma unroll
     for (int u = 0; u < 3; u++)
@@ -519,7 +538,8 @@ __global__ void __launch_bounds__(256, 2) k_attn_split(const float * __restrict_
 template <int HD>
 __global__ void __launch_bounds__(256) k_attn_long(const float * __restrict__ q, const float * __restrict__ kc,
                                                    const float * __restrict__ vt, int64_t v_ld, int M, int n_keys,
-                                                   int H, int Hkv, int q_tiles, float * __restrict__ out) {
+                                                   int H, int Hkv, int q_tiles, int q_pos0, int window,
+                                                   float * __restrict__ out) {
 #pragma clang fp contract(off)
     __shared__ __attribute__((aligned(16))) float P[16 * LONG_PSTR];
     __shared__ float red_f[4][16];
@@ -561,7 +581,10 @@ __global__ void __launch_bounds__(256) k_attn_long(const float * __restrict__ q,
         }
         const double4v acc = (a[0] + a[1]) + (a[2] + a[3]);
 #pragma unroll
-        for (int i = 0; i < 4; i++) sc[i] = n < n_keys ? (float)acc[i] * scale : -INFINITY;
+        for (int i = 0; i < 4; i++) {
+            const key_range kr = row_keys(q0 + lg + 4 * i, M, n_keys, q_pos0, window);
+            sc[i] = n >= kr.lo && n <= kr.hi ? (float)acc[i] * scale : -INFINITY;
+        }
     };
 
     // ---- pass 1: row maxima (lane: rows lg + 4i)
@@ -707,6 +730,32 @@ static inline int attn_sstride(int64_t n_keys) { return (int)(((n_keys + 15) / 1
 // Score-row stride of the split-bf16 kernel: whole 32-key tiles, plus 4 floats.
 static inline int attn_split_sstride(int64_t n_keys) { return (int)(((n_keys + 31) / 32) * 32 + 4); }
 
+// The exact (f64-summed) kernels: scores kept in LDS when a 16-row tile of them fits,
+// else recomputed in three passes.  q_pos0 / window: the causal mask (q_pos0 < 0: none).
+static int attn_exact(const float * q, const float * kc, const float * vt, int64_t v_ld, int M, int n_keys, int H,
+                      int Hkv, int hd, int q_pos0, int window, float * out, hipStream_t st) {
+    const int sstride = attn_sstride(n_keys);
+    const size_t lds = (size_t)16 * sstride * sizeof(float);
+    const int q_tiles = (M + 15) / 16;
+    const dim3 grid((unsigned)(8 * ((H + 7) / 8) * q_tiles));
+    if (lds <= attn_lds_limit()) {
+        if (hd == 128)
+            hipLaunchKernelGGL((k_attn_mfma<128>), grid, dim3(256), lds, st, q, kc, vt, v_ld, M, n_keys, H, Hkv,
+                               sstride, q_tiles, q_pos0, window, out);
+        else
+            hipLaunchKernelGGL((k_attn_mfma<64>), grid, dim3(256), lds, st, q, kc, vt, v_ld, M, n_keys, H, Hkv,
+                               sstride, q_tiles, q_pos0, window, out);
+    } else if (hd == 128) {   // score rows longer than the LDS holds: recomputed in three passes
+        hipLaunchKernelGGL((k_attn_long<128>), grid, dim3(256), 0, st, q, kc, vt, v_ld, M, n_keys, H, Hkv, q_tiles,
+                           q_pos0, window, out);
+    } else {
+        hipLaunchKernelGGL((k_attn_long<64>), grid, dim3(256), 0, st, q, kc, vt, v_ld, M, n_keys, H, Hkv, q_tiles,
+                           q_pos0, window, out);
+    }
+    DFX_CHECK_LAUNCH("dfx_attention");
+    return DFX_OK;
+}
+
 extern "C" int dfx_attention(const float * q, const float * kc, const float * vt, int64_t v_ld, int64_t M,
                              int64_t n_keys, int H, int Hkv, int hd, float * out, void * stream) {
     return dfx_attention_ex(q, kc, vt, v_ld, M, n_keys, H, Hkv, hd, out, DFX_ATTN_EXACT, stream);
@@ -744,24 +793,20 @@ extern "C" int dfx_attention_ex(const float * q, const float * kc, const float *
         }
         // longer score rows: the exact forms below
     }
-    const int sstride = attn_sstride(n_keys);
-    const size_t lds = (size_t)16 * sstride * sizeof(float);
-    const int q_tiles = (int)((M + 15) / 16);
-    const dim3 grid((unsigned)(8 * ((H + 7) / 8) * q_tiles));
-    if (lds <= attn_lds_limit()) {
-        if (hd == 128)
-            hipLaunchKernelGGL((k_attn_mfma<128>), grid, dim3(256), lds, st, q, kc, vt, v_ld, (int)M, (int)n_keys, H,
-                               Hkv, sstride, q_tiles, out);
-        else
-            hipLaunchKernelGGL((k_attn_mfma<64>), grid, dim3(256), lds, st, q, kc, vt, v_ld, (int)M, (int)n_keys, H,
-                               Hkv, sstride, q_tiles, out);
-    } else if (hd == 128) {   // score rows longer than the LDS holds: recomputed in three passes
-        hipLaunchKernelGGL((k_attn_long<128>), grid, dim3(256), 0, st, q, kc, vt, v_ld, (int)M, (int)n_keys, H, Hkv,
-                           q_tiles, out);
-    } else {
-        hipLaunchKernelGGL((k_attn_long<64>), grid, dim3(256), 0, st, q, kc, vt, v_ld, (int)M, (int)n_keys, H, Hkv,
-                           q_tiles, out);
+    return attn_exact(q, kc, vt, v_ld, (int)M, (int)n_keys, H, Hkv, hd, -1, 0, out, st);
+}
+
+extern "C" int dfx_attention_causal(const float * q, const float * kc, const float * vt, int64_t v_ld, int64_t M,
+                                    int64_t n_keys, int H, int Hkv, int hd, int64_t q_pos0, int window, float * out,
+                                    void * stream) {
+    if (M < 0 || n_keys <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || (hd != 64 && hd != 128) || v_ld < n_keys ||
+        (v_ld % 16) || M > INT32_MAX || n_keys > INT32_MAX || q_pos0 < 0 || q_pos0 + M > n_keys || window < 0) {
+        dfx_set_error("dfx_attention_causal: unsupported shape M=%lld keys=%lld H=%d Hkv=%d hd=%d v_ld=%lld "
+                      "q_pos0=%lld window=%d (queries must lie within the keys)", (long long)M, (long long)n_keys, H,
+                      Hkv, hd, (long long)v_ld, (long long)q_pos0, window);
+        return DFX_ERR_UNSUPPORTED;
     }
-    DFX_CHECK_LAUNCH("dfx_attention");
-    return DFX_OK;
+    if (M == 0) return DFX_OK;
+    return attn_exact(q, kc, vt, v_ld, (int)M, (int)n_keys, H, Hkv, hd, (int)q_pos0, window, out,
+                      (hipStream_t)stream);
 }

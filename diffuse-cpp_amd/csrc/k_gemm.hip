@@ -1387,6 +1387,57 @@ __global__ void k_gemm_reduce(const float * __restrict__ ws, int S, int64_t MN, 
 
 #define MAX_SPLIT 8
 
+// Forced tile of the Q4_K / Q6_K kernels, for tuning and tests:
+// "<TM>x<TN>[x<D>]" picks a register tile, "s" splits K when possible, "n" never
+// splits, "w" / "w1" pick the LDS-DMA Q4_K kernel (64 x 64 / 64 x 32 per wave).
+// Set with dfx_gemm_force_tile; DFX_Q4K_TILE / DFX_Q6K_TILE are read once, at the
+// first GEMM launch or setter call.  Parsed once, not per launch.
+struct tile_force {
+    bool on = false;
+    int got = 0, tm = 0, tn = 0, d = 0;
+    bool split = false, nosplit = false, w = false, w1 = false;
+};
+static std::mutex g_force_mu;
+static tile_force g_force[2];   // [0] Q4_K, [1] Q6_K
+static std::once_flag g_force_env;
+
+static tile_force parse_force(const char * f) {
+    tile_force t;
+    if (!f || !*f) return t;
+    t.on = true;
+    t.got = sscanf(f, "%dx%dx%d", &t.tm, &t.tn, &t.d);
+    t.split = strchr(f, 's') != nullptr;
+    t.nosplit = strchr(f, 'n') != nullptr;
+    t.w = strchr(f, 'w') != nullptr;
+    t.w1 = strstr(f, "w1") != nullptr;
+    return t;
+}
+
+static void force_from_env() {
+    std::call_once(g_force_env, [] {
+        std::lock_guard<std::mutex> lk(g_force_mu);
+        g_force[0] = parse_force(getenv("DFX_Q4K_TILE"));
+        g_force[1] = parse_force(getenv("DFX_Q6K_TILE"));
+    });
+}
+
+static tile_force forced_tile(int which) {
+    force_from_env();
+    std::lock_guard<std::mutex> lk(g_force_mu);
+    return g_force[which];
+}
+
+extern "C" int dfx_gemm_force_tile(int wtype, const char * spec) {
+    if (wtype != DFX_TYPE_Q4_K && wtype != DFX_TYPE_Q6_K) {
+        dfx_set_error("dfx_gemm_force_tile: only Q4_K and Q6_K have tile choices (type %d)", wtype);
+        return DFX_ERR_ARG;
+    }
+    force_from_env();
+    std::lock_guard<std::mutex> lk(g_force_mu);
+    g_force[wtype == DFX_TYPE_Q4_K ? 0 : 1] = parse_force(spec);
+    return DFX_OK;
+}
+
 // Split-K partials: F16 up to MAX_SPLIT slices, quantised types one slice per K chunk.
 extern "C" size_t dfx_gemm_ws_bytes(int64_t M, int64_t N, int64_t K) {
     const int64_t slices = std::max<int64_t>(MAX_SPLIT, dot_chunks(K));
@@ -1515,7 +1566,7 @@ static int launch_q6k(const void * w, int N, int K, const void * act, int M, con
 }
 
 // Q6_K: 64x128 workgroup tiles (2-deep weight ring), split K when the grid is small.
-// DFX_Q6K_TILE = "<TM>x<TN>[s|n]" forces a tile (tuning, tests).
+// A forced tile "<TM>x<TN>[x<D>][s|n]" (dfx_gemm_force_tile) overrides the choice.
 static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                         float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer) {
     int tm = M > 48 ? 2 : 1, tn = 1;
@@ -1523,13 +1574,11 @@ static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, c
     const int64_t tiles = (int64_t)((M + 32 * tm - 1) / (32 * tm)) * ((N + 128 * tn - 1) / (128 * tn));
     bool split = chunks > 1 && tiles * 4 < 1024 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
     int d = 2;
-    if (const char * f = getenv("DFX_Q6K_TILE")) {
-        int a = 0, b = 0, c = 0;
-        const int got = sscanf(f, "%dx%dx%d", &a, &b, &c);
-        if (got >= 2 && ((a == 1 || a == 2) && b == 1)) { tm = a; tn = b; }
-        if (got == 3 && (c == 2 || c == 4)) d = c;
-        if (strchr(f, 's')) split = chunks > 1 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
-        if (strchr(f, 'n')) split = false;
+    if (const tile_force f = forced_tile(1); f.on) {
+        if (f.got >= 2 && ((f.tm == 1 || f.tm == 2) && f.tn == 1)) { tm = f.tm; tn = f.tn; }
+        if (f.got == 3 && (f.d == 2 || f.d == 4)) d = f.d;
+        if (f.split) split = chunks > 1 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
+        if (f.nosplit) split = false;
     }
     // a 4-deep ring needs a multiple of 4 K steps in every workgroup
     const int sb = K / 256, sb_last = sb - (chunks - 1) * (DFX_DOT_CHUNK / 256);
@@ -1593,25 +1642,24 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
     } else {
         split = can_split && (chunks > 2 || (int64_t)n_col * ((M + 63) / 64) < 160);
     }
-    // DFX_Q4K_TILE="<TM>x<TN>[x<D>][s|n]" forces a configuration (tuning, tests):
+    // A forced tile "<TM>x<TN>[x<D>][s|n]" (dfx_gemm_force_tile) overrides the choice:
     // s = split K when possible, n = never split.
-    if (const char * f = getenv("DFX_Q4K_TILE")) {
-        int tm = 0, tn = 0, d = 0;
-        const int got = sscanf(f, "%dx%dx%d", &tm, &tn, &d);
-        if (got >= 2) {
+    const tile_force f = forced_tile(0);
+    if (f.on) {
+        if (f.got >= 2) {
             dma = false;
             for (int c = n_cand - 1; c >= 0; c--)
-                if (cands[c].tm == tm && cands[c].tn == tn && (got < 3 || cands[c].d == d)) pick = c;
+                if (cands[c].tm == f.tm && cands[c].tn == f.tn && (f.got < 3 || cands[c].d == f.d)) pick = c;
         }
-        if (strchr(f, 's')) split = chunks > 1 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
-        if (strchr(f, 'n')) split = false;
+        if (f.split) split = chunks > 1 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
+        if (f.nosplit) split = false;
     }
     // a 4-deep ring needs a multiple of 4 K steps in every workgroup
     const int sb = K / 256, sb_last = sb - (chunks - 1) * (DFX_DOT_CHUNK / 256);
-    if (const char * f = getenv("DFX_Q4K_TILE"); f && strchr(f, 'w')) {
+    if (f.on && f.w) {
         // "w": 64 x 64 per wave; "w1": 64 x 32 per wave, two workgroups per CU
         float * wsw = split ? (float *)ws : nullptr;
-        if (strstr(f, "w1")) return launch_q4k_w<1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
+        if (f.w1) return launch_q4k_w<1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
         if (sb_last % 2) return launch_q4k_w<2, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
         return launch_q4k_w<2, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
     }

@@ -338,3 +338,112 @@ extern "C" int dfx_select(const dfx_candidate * cand, int n, int remasking, floa
     DFX_CHECK_LAUNCH("dfx_select");
     return DFX_OK;
 }
+
+// ---------------------------------------------------------------------------
+// Autoregressive decoding (src/ar-sampler.cpp, src/ar-graph.cpp)
+// ---------------------------------------------------------------------------
+// Greedy sample_token (src/ar-sampler.cpp:99-117) on one logits row, in place:
+// the repetition penalty over the recent tokens (src/ar-sampler.cpp:83-97; a token
+// listed k times is penalised k times, in any order: each application maps x to x/p
+// when x > 0 and to x*p otherwise, so only the count matters), then the first index
+// of the maximum (strict >, from index 0).  A NaN in row[0], or a row with no value
+// above -inf, gives token 0, as the reference's scan does.
+// The decode state st lives on the device: [0] token of the next pass, [1] its
+// position, [2] number of recent tokens n, [3] ring start, [4..4+R) ring of the last
+// R (= repeat_last_n) tokens.  The chosen token becomes st[0], the position advances,
+// the token enters the ring (the oldest leaves once R are held), and it is also
+// written to tok_out.
+__global__ void __launch_bounds__(RS_THREADS) k_ar_greedy(float * __restrict__ row, int V, int32_t * __restrict__ st,
+                                                          int R, float penalty, int32_t * __restrict__ tok_out) {
+#pragma clang fp contract(off)
+    __shared__ float red_v[RS_THREADS / 64];
+    __shared__ int red_i[RS_THREADS / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    if (tid == 0 && penalty > 1.0f && R > 0) {
+        const int n = st[2], start = st[3];
+        for (int j = 0; j < n; j++) {
+            const int t = st[4 + (start + j) % R];
+            if (t >= 0 && t < V) {
+                const float v = row[t];
+                row[t] = v > 0.0f ? v / penalty : v * penalty;
+            }
+        }
+    }
+    __syncthreads();   // the penalised values are visible to the whole workgroup
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = tid; i < V; i += RS_THREADS) {
+        const float v = row[i];
+        if (v > bv) { bv = v; bi = i; }     // increasing i per thread: the first maximum stays
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, WAVE);
+        const int oi = __shfl_xor(bi, o, WAVE);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) { red_v[wv] = bv; red_i[wv] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < RS_THREADS / 64; w++)
+            if (red_v[w] > bv || (red_v[w] == bv && red_i[w] < bi)) { bv = red_v[w]; bi = red_i[w]; }
+        const float r0 = row[0];
+        const int tok = (r0 != r0 || bi == 0x7fffffff) ? 0 : bi;
+        st[0] = tok;
+        st[1] = st[1] + 1;
+        if (R > 0) {
+            const int n = st[2], start = st[3];
+            if (n < R) {
+                st[4 + (start + n) % R] = tok;
+                st[2] = n + 1;
+            } else {
+                st[4 + start] = tok;
+                st[3] = (start + 1) % R;
+            }
+        }
+        tok_out[0] = tok;
+    }
+}
+
+extern "C" int dfx_ar_greedy(float * row, int64_t V, int32_t * state, int repeat_last_n, float repeat_penalty,
+                             int32_t * token_out, void * stream) {
+    if (!row || !state || !token_out || V <= 0 || V > INT32_MAX) {
+        dfx_set_error("dfx_ar_greedy: bad arguments (V=%lld)", (long long)V);
+        return DFX_ERR_ARG;
+    }
+    hipLaunchKernelGGL(k_ar_greedy, dim3(1), dim3(RS_THREADS), 0, (hipStream_t)stream, row, (int)V, state,
+                       repeat_last_n > 0 ? repeat_last_n : 0, repeat_penalty, token_out);
+    DFX_CHECK_LAUNCH("dfx_ar_greedy");
+    return DFX_OK;
+}
+
+// Layer impact of ar_profile_layers (src/ar-graph.cpp:219-228): for each row m,
+// out[m] = sum over i of (double)(d * d), d = x[m][i] - x_in[m][i] in float, added in
+// increasing i (one thread per row, so the double sum has the scalar order).  The caller
+// adds the rows in order in double and rounds to float, as ggml_sum does.
+__global__ void __launch_bounds__(64) k_layer_impact(const float * __restrict__ x, const float * __restrict__ x_in,
+                                                     int M, int64_t d, double * __restrict__ out) {
+#pragma clang fp contract(off)
+    const int m = blockIdx.x * 64 + threadIdx.x;
+    if (m >= M) return;
+    const float * a = x + (int64_t)m * d;
+    const float * b = x_in + (int64_t)m * d;
+    double s = 0.0;
+    for (int64_t i = 0; i < d; i++) {
+        const float df = a[i] - b[i];
+        s += (double)(df * df);
+    }
+    out[m] = s;
+}
+
+extern "C" int dfx_layer_impact(const float * x, const float * x_in, int64_t M, int64_t d, double * out,
+                                void * stream) {
+    if (M < 0 || M > INT32_MAX || d <= 0) {
+        dfx_set_error("dfx_layer_impact: bad shape M=%lld d=%lld", (long long)M, (long long)d);
+        return DFX_ERR_ARG;
+    }
+    if (M == 0) return DFX_OK;
+    hipLaunchKernelGGL(k_layer_impact, dim3((unsigned)((M + 63) / 64)), dim3(64), 0, (hipStream_t)stream, x, x_in,
+                       (int)M, d, out);
+    DFX_CHECK_LAUNCH("dfx_layer_impact");
+    return DFX_OK;
+}

@@ -50,6 +50,27 @@ class GenStats(C.Structure):
                 ("unmasked_per_step", C.c_int * 256), ("step_ms", C.c_float * 256)]
 
 
+class ArParams(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_int),
+                ("repeat_penalty", C.c_float), ("repeat_last_n", C.c_int), ("seed", C.c_uint32),
+                ("layer_skip", C.c_int), ("sliding_window", C.c_int)]
+
+    @classmethod
+    def make(cls, temperature=0.0, top_p=0.9, top_k=40, repeat_penalty=1.1, repeat_last_n=64, seed=42,
+             layer_skip=0, sliding_window=0):
+        # defaults of ar_sampler_params, include/diffuse.h:96-107
+        return cls(temperature, top_p, top_k, repeat_penalty, repeat_last_n, seed, layer_skip, sliding_window)
+
+
+class ArStats(C.Structure):
+    _fields_ = [("prefill_ms", C.c_double), ("decode_ms", C.c_double), ("total_ms", C.c_double),
+                ("n_prompt", C.c_int), ("n_decoded", C.c_int), ("n_generated", C.c_int),
+                ("n_skipped_layers", C.c_int)]
+
+
+AR_TOKEN_FN = C.CFUNCTYPE(C.c_int, C.c_int32, C.c_int, C.c_void_p)
+
+
 class SynthSpec(C.Structure):
     _fields_ = [("n_vocab", C.c_uint32), ("n_embd", C.c_uint32), ("n_head", C.c_uint32),
                 ("n_head_kv", C.c_uint32), ("n_layer", C.c_uint32), ("n_ff", C.c_uint32),
@@ -109,6 +130,7 @@ def _declare(L):
         "dfx_gemm_ws_bytes": (S, [I64, I64, I64]),
         "dfx_gemm": (I32, [I32, P, I64, I64, P, I64, P, P, P, P, P]),
         "dfx_gemm_noalloc": (I32, [I32, P, I64, I64, P, I64, P, P, P, P]),
+        "dfx_gemm_force_tile": (I32, [I32, C.c_char_p]),
         "dfx_rope_store": (I32, [P, P, I64, I32, I32, I32, P, P, P, P, I64, P]),
         "dfx_attention": (I32, [P, P, P, I64, I64, I64, I32, I32, I32, P, P]),
         "dfx_attention_ex": (I32, [P, P, P, I64, I64, I64, I32, I32, I32, P, I32, P]),
@@ -127,6 +149,13 @@ def _declare(L):
         "dfx_forward_cached": (I32, [P, P, P, I32, I32, P]),
         "dfx_generate": (I32, [P, P, I32, I32, C.POINTER(SamplerParams), P, C.POINTER(GenStats)]),
         "dfx_generate_trace": (I32, [P, P, I32, I32, C.POINTER(SamplerParams), P, C.POINTER(GenStats), P]),
+        "dfx_attention_causal": (I32, [P, P, P, I64, I64, I64, I32, I32, I32, I64, I32, P, P]),
+        "dfx_ar_greedy": (I32, [P, I64, P, I32, F, P, P]),
+        "dfx_layer_impact": (I32, [P, P, I64, I64, P, P]),
+        "dfx_ar_forward": (I32, [P, P, I32, I32, I32, P]),
+        "dfx_ar_profile_layers": (I32, [P, P, I32, I32, I32, P, P, P]),
+        "dfx_ar_generate": (I32, [P, P, I32, I32, C.POINTER(ArParams), P, C.POINTER(C.c_int), C.POINTER(ArStats),
+                                  AR_TOKEN_FN, P]),
         "dfx_context_profile": (I32, [P, I32]),
         "dfx_context_set_attention": (I32, [P, I32]),
         "dfx_context_profile_read_rows": (I32, [P, I32, I32, C.POINTER(C.c_int64), C.POINTER(C.c_double),
@@ -283,6 +312,11 @@ def repack(gguf_type, raw, n_rows, n_cols):
     return out
 
 
+def force_tile(wtype, spec):
+    """Force the Q4_K / Q6_K GEMM tile for later calls (None restores the built-in choice)."""
+    check(lib().dfx_gemm_force_tile(wtype, spec.encode() if spec else None), "force_tile")
+
+
 def quantize_rows(gguf_type, x):
     x = np.ascontiguousarray(x, dtype=np.float32)
     n_rows, n_cols = x.shape
@@ -369,6 +403,37 @@ class Context:
         check(lib().dfx_generate_trace(self.h, _ptr(prompt), len(prompt), n_generate, C.byref(params),
                                        _ptr(out), C.byref(st), _ptr(steps)), "dfx_generate_trace")
         return out, steps
+
+    def ar_forward(self, tokens, reset=False, sliding_window=0):
+        """One causal pass of the autoregressive graph: logits [n_new][V] of tokens at
+        positions n_past.. (n_past = 0 with reset)."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty((len(t), self.model.hparams.n_vocab), dtype=np.float32)
+        check(lib().dfx_ar_forward(self.h, _ptr(t), len(t), 1 if reset else 0, sliding_window, _ptr(out)),
+              "dfx_ar_forward")
+        return out
+
+    def ar_profile_layers(self, tokens, n_skip, sliding_window=0):
+        """(logits, impact, skip) of ar_profile_layers' prefill."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        L = self.model.hparams.n_layer
+        out = np.empty((len(t), self.model.hparams.n_vocab), dtype=np.float32)
+        imp = np.empty(L, dtype=np.float32)
+        skip = np.empty(L, dtype=np.uint8)
+        check(lib().dfx_ar_profile_layers(self.h, _ptr(t), len(t), sliding_window, n_skip, _ptr(out), _ptr(imp),
+                                          _ptr(skip)), "dfx_ar_profile_layers")
+        return out, imp, skip
+
+    def ar_generate(self, prompt, max_tokens, params, stats=None, callback=None):
+        """Generated ids of ar_generate; callback(token, pos) -> bool (False stops)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.empty(max(max_tokens, 1), dtype=np.int32)
+        n = C.c_int()
+        st = stats if stats is not None else ArStats()
+        fn = AR_TOKEN_FN(lambda t, p, u: 1 if callback(t, p) else 0) if callback else AR_TOKEN_FN()
+        check(lib().dfx_ar_generate(self.h, _ptr(prompt), len(prompt), max_tokens, C.byref(params), _ptr(out),
+                                    C.byref(n), C.byref(st), fn, None), "dfx_ar_generate")
+        return out[:n.value].copy()
 
     def set_attention(self, mode):
         """ATTN_EXACT (the default) or ATTN_SPLIT_BF16 for this context's forward passes."""

@@ -110,6 +110,35 @@ extern "C" int dfx_context_profile_read_rows(dfx_context * c, int wtype, int row
     return engine_profile_read(c, wtype, rows_class, launches, ms, flops, bytes);
 }
 
+extern "C" int dfx_ar_forward(dfx_context * c, const int32_t * tokens, int n_new, int reset, int sliding_window,
+                              float * logits_out) {
+    if (!c) return DFX_ERR_ARG;
+    return engine_ar_forward(c, tokens, n_new, reset != 0, sliding_window, logits_out);
+}
+
+extern "C" int dfx_ar_profile_layers(dfx_context * c, const int32_t * tokens, int n_tokens, int sliding_window,
+                                     int n_skip, float * logits_out, float * impact_out, uint8_t * skip_out) {
+    if (!c) return DFX_ERR_ARG;
+    return engine_ar_profile(c, tokens, n_tokens, sliding_window, n_skip, logits_out, impact_out, skip_out);
+}
+
+extern "C" int dfx_ar_generate(dfx_context * c, const int32_t * prompt, int n_prompt, int max_tokens,
+                               const dfx_ar_params * p, int32_t * out, int * n_out, dfx_ar_stats * stats,
+                               dfx_ar_token_fn cb, void * user) {
+    if (!c || !p || !out || !n_out) {
+        dfx_set_error("dfx_ar_generate: null argument");
+        return DFX_ERR_ARG;
+    }
+    *n_out = 0;
+    std::vector<int32_t> toks;
+    std::function<bool(int32_t, int)> f;
+    if (cb) f = [cb, user](int32_t t, int pos) { return cb(t, pos, user) != 0; };
+    const int rc = engine_ar_generate(c, prompt, n_prompt, max_tokens, *p, toks, stats, cb ? &f : nullptr);
+    memcpy(out, toks.data(), toks.size() * 4);
+    *n_out = (int)toks.size();
+    return rc;
+}
+
 // ---- C++ API (include/diffuse.h) ----
 diffuse_model * diffuse_model_load(const std::string & path, int /*n_threads*/) {
     diffuse_model * m = nullptr;
@@ -158,14 +187,33 @@ std::vector<int32_t> diffuse_generate(diffuse_context * ctx, const std::vector<i
     return out;
 }
 
-// The autoregressive path (src/ar-*.cpp) is not part of the denoising hot path;
-// the symbols exist so programs written against diffuse.h link.
-std::vector<int32_t> ar_generate(diffuse_context *, const std::vector<int32_t> &, int, const ar_sampler_params &,
-                                 ar_token_callback) {
-    DIFFUSE_LOG("ar_generate: the autoregressive path is not available in this build");
-    return {};
+// ar_generate (src/ar-sampler.cpp:143-314); a failed forward ends the generation with
+// what was generated so far, as the reference's decode loop does (src/ar-sampler.cpp:262-265),
+// and a failed prefill is fatal (src/ar-sampler.cpp:199-209).
+std::vector<int32_t> ar_generate(diffuse_context * ctx, const std::vector<int32_t> & prompt_tokens, int max_tokens,
+                                 const ar_sampler_params & params, ar_token_callback callback) {
+    dfx_ar_params p;
+    p.temperature = params.temperature;
+    p.top_p = params.top_p;
+    p.top_k = params.top_k;
+    p.repeat_penalty = params.repeat_penalty;
+    p.repeat_last_n = params.repeat_last_n;
+    p.seed = params.seed;
+    p.layer_skip = params.layer_skip;
+    p.sliding_window = params.sliding_window;
+    std::vector<int32_t> out;
+    const std::function<bool(int32_t, int)> cb = callback;
+    const int rc = engine_ar_generate(ctx, prompt_tokens.data(), (int)prompt_tokens.size(), max_tokens, p, out,
+                                      nullptr, cb ? &cb : nullptr);
+    if (rc != DFX_OK) {
+        if (out.empty()) DIFFUSE_DIE("ar_generate: prefill failed: %s", dfx_last_error());
+        DIFFUSE_LOG("ar_generate: decode failed: %s", dfx_last_error());
+    }
+    return out;
 }
 
+// Speculative decoding (src/ar-speculative.cpp) is not built; the symbol exists so programs
+// written against diffuse.h link.
 std::vector<int32_t> ar_speculative_generate(diffuse_context *, diffuse_context *, const std::vector<int32_t> &, int,
                                              const ar_spec_params &, ar_token_callback, ar_spec_stats *) {
     DIFFUSE_LOG("ar_speculative_generate: the autoregressive path is not available in this build");

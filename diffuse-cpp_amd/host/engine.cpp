@@ -46,11 +46,18 @@ struct dims {
 
 void free_buffers(diffuse_context * c) {
     void * bufs[] = {c->x, c->act, c->qkv, c->qr, c->att, c->gu, c->logits, c->kc, c->vc, c->rope_tab,
-                     c->d_ints, c->ws, c->d_stats, c->d_out};
+                     c->d_ints, c->ws, c->d_stats, c->d_out, c->x_prev, c->d_imp, c->d_ar};
     for (void * p : bufs)
         if (p) (void)hipFree(p);
     if (c->h_pin) (void)hipHostFree(c->h_pin);
     if (c->h_out) (void)hipHostFree(c->h_out);
+    if (c->h_row) (void)hipHostFree(c->h_row);
+    c->x_prev = nullptr;
+    c->d_imp = nullptr;
+    c->d_ar = nullptr;
+    c->ar_ring = 0;
+    c->h_row = nullptr;
+    c->ar_past = 0;
     c->x = c->qkv = c->qr = c->att = c->gu = c->logits = c->kc = c->vc = c->rope_tab = nullptr;
     c->act = nullptr;
     c->d_ints = c->d_tok = c->d_pos = c->d_hrows = c->d_hmap = c->d_srows = c->d_spos = c->d_order = c->d_nun = nullptr;
@@ -212,38 +219,53 @@ int run_group(diffuse_context * c, const proj_group & g, const float * norm, int
 
 // Enqueue one forward over the M rows in d_tok/d_pos, attending over keys
 // 0..n_keys-1 of the cache; logits for the n_head rows d_hrows go to logits[d_hmap].
-int forward_pass(diffuse_context * c, int M, int n_keys, int n_head) {
+// o: the autoregressive graph's options (causal mask, skipped layers, impact profile).
+int forward_pass(diffuse_context * c, int M, int n_keys, int n_head, const pass_opts & o = pass_opts()) {
     const diffuse_model & m = *c->model;
     const dims D(m.hparams);
     const float eps = m.hparams.rms_norm_eps;
-    TRY(dfx_embed(m.tok_embd.type, m.tok_embd.data, D.d, c->d_tok, M, c->x, c->stream));
+    const int32_t * tok = o.tok ? o.tok : c->d_tok;
+    const int32_t * pos = o.pos ? o.pos : c->d_pos;
+    const int32_t * hrows = o.hrows ? o.hrows : c->d_hrows;
+    const int32_t * hmap = o.hmap ? o.hmap : c->d_hmap;
+    TRY(dfx_embed(m.tok_embd.type, m.tok_embd.data, D.d, tok, M, c->x, c->stream));
     // split-K partial sums of the last O / down projection, still to be added to x (by
-    // the RMSNorm that reads x next)
+    // the RMSNorm that reads x next); profiling needs x whole after every layer
     int pending = 0;
+    int * defer = o.impact_rows ? nullptr : &pending;
     for (int64_t il = 0; il < D.L; il++) {
+        if (o.skip && o.skip[il]) continue;   // src/ar-graph.cpp:98-102
         const dev_layer & L = m.layers[il];
         float * kc = c->kc + il * (int64_t)c->cap * D.dkv;
         float * vc = c->vc + il * (int64_t)c->cap * D.dkv;
+        if (o.impact_rows)
+            TRY(hip_ok(hipMemcpyAsync(c->x_prev, c->x, (size_t)M * D.d * 4, hipMemcpyDeviceToDevice, c->stream),
+                       "layer input copy"));
         TRY(run_group(c, L.qkv, L.attn_norm, M, D.d, c->qkv, pending));
-        TRY(dfx_rope_store(c->qkv, c->d_pos, M, (int)D.H, (int)D.Hkv, (int)D.hd, c->rope_tab, c->qr, kc, vc,
-                           c->cap, c->stream));
-        TRY(dfx_attention_ex(c->qr, kc, vc, c->cap, M, n_keys, (int)D.H, (int)D.Hkv, (int)D.hd, c->att,
-                             c->attn_mode, c->stream));
+        TRY(dfx_rope_store(c->qkv, pos, M, (int)D.H, (int)D.Hkv, (int)D.hd, c->rope_tab, c->qr, kc, vc, c->cap,
+                           c->stream));
+        if (o.q_pos0 >= 0)
+            TRY(dfx_attention_causal(c->qr, kc, vc, c->cap, M, n_keys, (int)D.H, (int)D.Hkv, (int)D.hd, o.q_pos0,
+                                     o.window, c->att, c->stream));
+        else
+            TRY(dfx_attention_ex(c->qr, kc, vc, c->cap, M, n_keys, (int)D.H, (int)D.Hkv, (int)D.hd, c->att,
+                                 c->attn_mode, c->stream));
         TRY(dfx_act_convert(L.o.type, c->att, M, D.d, c->act, c->stream));
-        TRY(gemm(c, L.o, D.d, D.d, M, nullptr, c->x, c->x, D.d, nullptr, true, &pending));
+        TRY(gemm(c, L.o, D.d, D.d, M, nullptr, c->x, c->x, D.d, nullptr, true, defer));
         TRY(run_group(c, L.gu, L.ffn_norm, M, D.d, c->gu, pending));
         TRY(dfx_swiglu_convert(L.down.type, c->gu, M, D.F, c->act, c->stream));
-        TRY(gemm(c, L.down, D.d, D.F, M, nullptr, c->x, c->x, D.d, nullptr, true, &pending));
+        TRY(gemm(c, L.down, D.d, D.F, M, nullptr, c->x, c->x, D.d, nullptr, true, defer));
+        if (o.impact_rows) TRY(dfx_layer_impact(c->x, c->x_prev, M, D.d, o.impact_rows + il * M, c->stream));
     }
     if (n_head > 0) {
         // rows without logits never need the last layer's x
         if (pending)
-            TRY(dfx_rmsnorm_convert_add(m.output.type, c->x, c->d_hrows, (const float *)c->ws, pending, M,
+            TRY(dfx_rmsnorm_convert_add(m.output.type, c->x, hrows, (const float *)c->ws, pending, M,
                                         m.output_norm, n_head, D.d, eps, c->act, c->stream));
         else
-            TRY(dfx_rmsnorm_convert_ex(m.output.type, c->x, c->d_hrows, m.output_norm, n_head, D.d, eps, c->act,
+            TRY(dfx_rmsnorm_convert_ex(m.output.type, c->x, hrows, m.output_norm, n_head, D.d, eps, c->act,
                                        c->stream));
-        TRY(gemm(c, m.output, D.V, D.d, n_head, nullptr, nullptr, c->logits, D.V, c->d_hmap, false));
+        TRY(gemm(c, m.output, D.V, D.d, n_head, nullptr, nullptr, c->logits, D.V, hmap, false));
     }
     return DFX_OK;
 }
@@ -360,6 +382,7 @@ int engine_forward(diffuse_context * c, const int32_t * tokens, int n, float * l
     TRY(upload_i32(c, c->d_hrows, idx.data(), n, 2));
     TRY(upload_i32(c, c->d_hmap, idx.data(), n, 3));
     c->kv_valid = 0;
+    c->ar_past = 0;
     TRY(forward_pass(c, n, n, n));
     TRY(hip_ok(hipMemcpyAsync(logits_out, c->logits, (size_t)n * D.V * 4, hipMemcpyDeviceToHost, c->stream), "D2H"));
     TRY(hip_ok(hipStreamSynchronize(c->stream), "forward"));
@@ -432,6 +455,7 @@ int engine_generate(diffuse_context * c, const int32_t * prompt, int n_prompt, i
     }
     TRY(ensure_capacity(c, N));
     c->kv_valid = 0;   // the generation leaves the cache partly stale
+    c->ar_past = 0;
 
     std::vector<int32_t> seq(prompt, prompt + n_prompt);
     seq.resize(N, mask_id);
@@ -663,3 +687,10 @@ int engine_generate(diffuse_context * c, const int32_t * prompt, int n_prompt, i
     memcpy(out, seq.data() + n_prompt, (size_t)n_generate * 4);
     return DFX_OK;
 }
+
+int engine_hip_ok(hipError_t e, const char * what) { return hip_ok(e, what); }
+int engine_reserve(diffuse_context * c, int N) { return ensure_capacity(c, N); }
+int engine_pass(diffuse_context * c, int M, int n_keys, int n_head, const pass_opts & o) {
+    return forward_pass(c, M, n_keys, n_head, o);
+}
+void engine_prof_collect(diffuse_context * c) { prof_collect(c); }

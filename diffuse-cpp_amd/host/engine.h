@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -107,6 +108,17 @@ struct diffuse_context {
     int          attn_mode = DFX_ATTN_EXACT;   // dfx_attention_ex mode of the forward passes
     int          kv_valid = 0;       // positions 0..kv_valid-1 of the cache hold a full forward's K/V
 
+    // Autoregressive state (src/ar-cache.h): positions 0..ar_past-1 of kc / vc hold the keys
+    // and values of the tokens passed so far (layers in ar_skip keep stale rows).
+    int          ar_past = 0;
+    std::vector<uint8_t> ar_skip;    // [L] layers left out of non-profiling passes
+    float *      x_prev = nullptr;   // [cap][d] layer input, kept while profiling
+    double *     d_imp = nullptr;    // [L][cap] per-row layer impact sums
+    int32_t *    d_ar = nullptr;     // [4] zeros (head row / map of a one-row pass), then the
+                                     // greedy decode state of dfx_ar_greedy [4 + ar_ring]
+    int          ar_ring = 0;        // ring capacity of d_ar
+    float *      h_row = nullptr;    // pinned [V]: one logits row for the host sampler
+
     // Optional per-GEMM timing: a pair of events around every GEMM launch on `stream`.
     struct gemm_rec { hipEvent_t a, b; int type; int64_t M; double flops, bytes; };
     bool                  prof = false;
@@ -116,6 +128,35 @@ struct diffuse_context {
     // by row class (0 every launch, 1 M > 96, 2 M <= 96) and weight type id
     prof_total            prof_tot[3][32];
 };
+
+// Options of one forward pass (the autoregressive graph of src/ar-graph.cpp:27-260):
+// causal attention, skipped layers, layer-impact profiling and index arrays other than
+// the context's d_tok / d_pos / d_hrows / d_hmap.
+struct pass_opts {
+    int64_t         q_pos0 = -1;         // >= 0: causal, query row m at position q_pos0 + m
+    int             window = 0;          // causal: keys within this many positions (0 = all)
+    const uint8_t * skip = nullptr;      // [L] host: nonzero = layer left out
+    double *        impact_rows = nullptr;   // device [L][M]: per-row impact sums (no split-K deferral)
+    const int32_t * tok = nullptr;       // device index arrays replacing the context's
+    const int32_t * pos = nullptr;
+    const int32_t * hrows = nullptr;
+    const int32_t * hmap = nullptr;
+};
+
+// engine.cpp internals shared with ar.cpp
+int  engine_hip_ok(hipError_t e, const char * what);
+int  engine_reserve(diffuse_context * c, int N);
+int  engine_pass(diffuse_context * c, int M, int n_keys, int n_head, const pass_opts & o);
+void engine_prof_collect(diffuse_context * c);
+
+// ar.cpp (src/ar-graph.cpp, src/ar-sampler.cpp)
+int  engine_ar_forward(diffuse_context * c, const int32_t * tokens, int n_new, bool reset, int window,
+                       float * logits_out);
+int  engine_ar_profile(diffuse_context * c, const int32_t * tokens, int n, int window, int n_skip, float * logits_out,
+                       float * impact_out, uint8_t * skip_out);
+int  engine_ar_generate(diffuse_context * c, const int32_t * prompt, int n_prompt, int max_tokens,
+                        const dfx_ar_params & p, std::vector<int32_t> & out, dfx_ar_stats * stats,
+                        const std::function<bool(int32_t, int)> * cb);
 
 // model.cpp
 int  engine_model_load(const std::string & path, diffuse_model ** out);

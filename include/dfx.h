@@ -122,6 +122,14 @@ size_t dfx_gemm_ws_bytes(int64_t M, int64_t N, int64_t K);
 int dfx_gemm(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
              const float * bias, const float * residual, float * y, void * ws, void * stream);
 
+/* Force the tile and split-K choice of the Q4_K or Q6_K GEMM for every later call in the
+ * process (tuning and tests; every choice gives the same bits): "<TM>x<TN>[x<D>]" picks a
+ * register tile, "s" splits K where possible, "n" never splits, "w" / "w1" pick the Q4_K
+ * LDS-DMA kernel; NULL or "" restores the built-in choice.  DFX_Q4K_TILE and DFX_Q6K_TILE
+ * in the environment are read once, before the first call.  No counterpart in the
+ * reference (GGML has no tile choice). */
+int dfx_gemm_force_tile(int wtype, const char * spec);
+
 /* dfx_gemm without a workspace argument and without any allocation: the split-K partial
  * sums go to a library-held device array of 32 MiB per GPU (held from the library's load to
  * process end), so M * N * ceil(K / 2048) * 4 bytes must not exceed 32 MiB (DFX_ERR_ARG
@@ -163,6 +171,15 @@ int dfx_attention(const float * q, const float * kc, const float * vt, int64_t v
 int dfx_attention_ex(const float * q, const float * kc, const float * vt, int64_t v_ld, int64_t M, int64_t n_keys,
                      int H, int Hkv, int hd, float * out, int mode, void * stream);
 
+/* Causal attention of the autoregressive graph (src/ar-graph.cpp:70-88 mask, 176-196
+ * ggml_flash_attn_ext): query row m sits at position q_pos0 + m and attends to the
+ * keys q_pos0 + m - window + 1 .. q_pos0 + m (window > 0) or 0 .. q_pos0 + m
+ * (window 0); every query's own position must be a key (q_pos0 + M <= n_keys).  The
+ * exact (f64-summed) form of dfx_attention_ex with DFX_ATTN_EXACT; caches as there. */
+int dfx_attention_causal(const float * q, const float * kc, const float * vt, int64_t v_ld, int64_t M,
+                         int64_t n_keys, int H, int Hkv, int hd, int64_t q_pos0, int window, float * out,
+                         void * stream);
+
 /* Per-row sampler statistics over logits rows (src/diffuse-sampler.cpp:34-57, 241-252):
  * argmax (strict >, lowest index on ties), top-1 and top-2 values and entropy.
  * rows[i] selects row rows[i] of the [*][ld] logits matrix. */
@@ -191,6 +208,22 @@ int dfx_make_candidates(const dfx_row_stat * stats, const int32_t * pos, int n, 
  * placed by rank (each candidate counts the ones before it). */
 int dfx_select(const dfx_candidate * cand, int n, int remasking, float tau, int n_sched,
                int32_t * order, int32_t * n_unmask, void * stream);
+
+/* Greedy sample_token of the autoregressive sampler (src/ar-sampler.cpp:83-117) on one
+ * device logits row, which it modifies: the repetition penalty over the recent tokens
+ * (x/p for x > 0, else x*p, once per occurrence; none unless repeat_penalty > 1), then
+ * the first index of the maximum (token 0 if row[0] is NaN or nothing exceeds -inf).
+ * state (device int32 [4 + repeat_last_n]): [0] next token, [1] its position, [2] number
+ * of recent tokens, [3] ring start, then the ring of recent tokens.  The chosen token is
+ * written to state[0] and token_out[0], state[1] advances by one and the token enters
+ * the ring (src/ar-sampler.cpp:236-242 keeps the last repeat_last_n tokens). */
+int dfx_ar_greedy(float * row, int64_t V, int32_t * state, int repeat_last_n, float repeat_penalty,
+                  int32_t * token_out, void * stream);
+
+/* Per-row layer impact of ar_profile_layers (src/ar-graph.cpp:219-228): out[m] = sum
+ * over i of (x[m][i] - x_in[m][i])^2 with the difference and square in float and the
+ * sum in double in increasing i.  x, x_in: device [M][d]; out: device double [M]. */
+int dfx_layer_impact(const float * x, const float * x_in, int64_t M, int64_t d, double * out, void * stream);
 
 /* ---- weight encoding, quantizer and synthetic models (host side) ---- */
 
@@ -271,8 +304,8 @@ int  dfx_generate(dfx_context * c, const int32_t * prompt, int n_prompt, int n_g
  * HIP events on its stream.  _read returns, for one weight type, the number of
  * launches, their summed duration, and their algorithmic FLOPs (2*M*N*K) and bytes
  * (weights + converted activations + f32 output).  Enabling resets the totals. */
-/* Attention arithmetic of the context's forward passes (DFX_ATTN_SPLIT_BF16, the default,
- * or DFX_ATTN_EXACT; see dfx_attention_ex).  Build-defined; no counterpart in the reference. */
+/* Attention arithmetic of the context's forward passes (DFX_ATTN_EXACT, the default, or
+ * DFX_ATTN_SPLIT_BF16; see dfx_attention_ex).  Build-defined; no counterpart in the reference. */
 int  dfx_context_set_attention(dfx_context * c, int mode);
 int  dfx_context_profile(dfx_context * c, int enable);
 int  dfx_context_profile_read(dfx_context * c, int wtype, int64_t * launches, double * ms, double * flops,
@@ -282,6 +315,49 @@ int  dfx_context_profile_read(dfx_context * c, int wtype, int64_t * launches, do
  * Build-defined instrumentation; no counterpart in the reference. */
 int  dfx_context_profile_read_rows(dfx_context * c, int wtype, int rows_class, int64_t * launches, double * ms,
                                    double * flops, double * bytes);
+/* ---- autoregressive API (include/diffuse.h:96-120; src/ar-graph.h, src/ar-sampler.cpp) ---- */
+/* ar_sampler_params (include/diffuse.h:96-107) */
+typedef struct {
+    float    temperature;      /* <= 0: greedy */
+    float    top_p;
+    int      top_k;            /* 0 = off */
+    float    repeat_penalty;
+    int      repeat_last_n;
+    uint32_t seed;
+    int      layer_skip;       /* layers skipped after profiling the prompt (0 = off) */
+    int      sliding_window;   /* keys within this many positions (0 = all) */
+} dfx_ar_params;
+
+typedef struct {
+    double prefill_ms, decode_ms, total_ms;
+    int    n_prompt, n_decoded, n_generated, n_skipped_layers;
+} dfx_ar_stats;
+
+/* Called after each generated token with its position; returning 0 stops the generation
+ * (ar_token_callback, include/diffuse.h:110). */
+typedef int (*dfx_ar_token_fn)(int32_t token, int pos, void * user);
+
+/* One pass of the causal graph over the context's append-only cache
+ * (ar_forward_prefill / ar_forward_batch / ar_forward_decode, src/ar-graph.h:16-39):
+ * tokens[n_new] at positions n_past.. (n_past = 0 after reset != 0); logits_out:
+ * [n_new][n_vocab] (host), or NULL.  sliding_window as in dfx_ar_params.  Layers marked by
+ * dfx_ar_profile_layers stay skipped until the next profiling.  n_past + n_new must not
+ * exceed the context's n_ctx.  The diffusion cache of dfx_forward_cached is invalidated. */
+int  dfx_ar_forward(dfx_context * c, const int32_t * tokens, int n_new, int reset, int sliding_window,
+                    float * logits_out);
+/* ar_profile_layers (src/ar-graph.cpp:454-505): a prefill (n_past = 0) with every layer,
+ * recording each layer's impact (sum of squared changes of the residual stream), then the
+ * n_skip lowest-impact layers outside the first two and last two are marked skipped.
+ * impact_out (optional, host float[n_layer]); skip_out (optional, host uint8[n_layer]). */
+int  dfx_ar_profile_layers(dfx_context * c, const int32_t * tokens, int n_tokens, int sliding_window, int n_skip,
+                           float * logits_out, float * impact_out, uint8_t * skip_out);
+/* ar_generate (src/ar-sampler.cpp:143-314): out gets up to max(max_tokens, 1) ids and
+ * *n_out their number (generation ends after an end token 151643 / 151645 / 151644, or
+ * when cb returns 0); cb and stats may be NULL.  Temperature <= 0 samples on the device;
+ * otherwise each row is sampled on the host with the reference's std:: algorithms. */
+int  dfx_ar_generate(dfx_context * c, const int32_t * prompt, int n_prompt, int max_tokens, const dfx_ar_params * p,
+                     int32_t * out, int * n_out, dfx_ar_stats * stats, dfx_ar_token_fn cb, void * user);
+
 /* dfx_generate that also records, for each generated position, the step (0-based)
  * at which it was unmasked (-1 if still masked at the end).  Stands in for the
  * per-step callback of include/diffuse.h:67-68 for C callers. */

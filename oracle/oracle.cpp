@@ -550,31 +550,47 @@ static void embed(const orc_model * md, const int32_t * tok, int M, float * x) {
         orc_dequant_row(md->tok_embd.type, (const uint8_t *)md->tok_embd.data + (int64_t)tok[m] * rs, x + m * d, d);
 }
 
-/* Bidirectional attention of M queries over n_keys keys (src/diffuse-graph.cpp:97-119,
- * 528-553): s = dot(K_n, Q_m) * (1/sqrtf(hd)); softmax over keys (max, expf, double sum,
- * multiply by 1/sum); out = sum_n V_n * p_n.  q: [M][H][hd]; k, v: [n_keys][H][hd]
- * (already GQA-expanded); out: [M][H*hd]. */
+/* Attention of M queries over n_keys keys (src/diffuse-graph.cpp:97-119, 528-553):
+ * s = dot(K_n, Q_m) * (1/sqrtf(hd)); softmax over the visible keys (max, expf, double
+ * sum, multiply by 1/sum); out = sum_n V_n * p_n.  q: [M][H][hd]; k, v: [n_keys][H][hd]
+ * (already GQA-expanded); out: [M][H*hd].  Every key is visible unless vis != NULL:
+ * then key n is visible to query m when vis->kpos[n] <= vis->qpos[m] and, with a
+ * window w > 0, vis->qpos[m] - vis->kpos[n] < w — the causal mask of
+ * src/ar-graph.cpp:70-88, whose -inf entries GGML's flash attention skips.  Visible
+ * keys are summed in increasing n. */
+struct key_vis { const int32_t * qpos; const int32_t * kpos; int window; };
+
 static void attention(const float * q, const float * k, const float * v, int M, int n_keys,
-                      int H, int hd, float * out, int n_threads) {
+                      int H, int hd, float * out, int n_threads, const key_vis * vis = nullptr) {
     const float scale = 1.0f / sqrtf((float)hd);
     #pragma omp parallel for num_threads(n_threads) collapse(2) schedule(static)
     for (int h = 0; h < H; h++) {
         for (int m = 0; m < M; m++) {
             std::vector<float> s(n_keys);
+            std::vector<char> on(n_keys, 1);
+            if (vis)
+                for (int n = 0; n < n_keys; n++)
+                    on[n] = vis->kpos[n] <= vis->qpos[m] && (vis->window <= 0 || vis->qpos[m] - vis->kpos[n] < vis->window);
             const float * qm = q + ((size_t)m * H + h) * hd;
             float mx = -INFINITY;
             for (int n = 0; n < n_keys; n++) {
+                if (!on[n]) continue;
                 s[n] = dot_f32_exact(hd, k + ((size_t)n * H + h) * hd, qm) * scale;
                 mx = fmaxf(mx, s[n]);
             }
             double sum = 0.0;
-            for (int n = 0; n < n_keys; n++) { s[n] = exp_cr(s[n] - mx); sum += (double)s[n]; }
+            for (int n = 0; n < n_keys; n++) {
+                if (!on[n]) continue;
+                s[n] = exp_cr(s[n] - mx);
+                sum += (double)s[n];
+            }
             const float inv = (float)(1.0 / sum);
-            for (int n = 0; n < n_keys; n++) s[n] *= inv;
+            for (int n = 0; n < n_keys; n++) s[n] = on[n] ? s[n] * inv : 0.0f;
             float * o = out + (size_t)m * H * hd + (size_t)h * hd;
             for (int dd = 0; dd < hd; dd++) {
                 double acc = 0.0;
-                for (int n = 0; n < n_keys; n++) acc += (double)v[((size_t)n * H + h) * hd + dd] * (double)s[n];
+                for (int n = 0; n < n_keys; n++)
+                    if (on[n]) acc += (double)v[((size_t)n * H + h) * hd + dd] * (double)s[n];
                 o[dd] = (float)acc;
             }
         }
@@ -586,6 +602,13 @@ extern "C" void orc_attention(const float * q, const float * k, const float * v,
     attention(q, k, v, M, n_keys, H, hd, out, n_threads);
 }
 
+extern "C" void orc_attention_causal(const float * q, const float * k, const float * v, int M, int n_keys, int H,
+                                     int hd, const int32_t * qpos, const int32_t * kpos, int window, float * out,
+                                     int n_threads) {
+    const key_vis vis = {qpos, kpos, window};
+    attention(q, k, v, M, n_keys, H, hd, out, n_threads, &vis);
+}
+
 /* GQA repeat (src/diffuse-graph.cpp:84-95): query head h reads KV head h / n_rep. */
 static void expand_heads(const float * src, int M, int Hkv, int H, int hd, float * dst) {
     const int n_rep = H / Hkv;
@@ -594,13 +617,24 @@ static void expand_heads(const float * src, int M, int Hkv, int H, int hd, float
             memcpy(dst + ((size_t)m * H + h) * hd, src + ((size_t)m * Hkv + h / n_rep) * hd, (size_t)hd * 4);
 }
 
+/* Options of the autoregressive graph (src/ar-graph.cpp:27-196): causal mask with an
+ * optional sliding window, skipped layers, and the layer-impact profile. */
+struct pass_opts {
+    bool            causal = false;
+    int             window = 0;
+    const uint8_t * skip = nullptr;     /* [n_layer] nonzero = layer left out */
+    float *         impact = nullptr;   /* [n_layer] sum of squared layer deltas */
+    int             head_from = 0;      /* logits for rows head_from..M-1 only */
+};
+
 /* One transformer stack over M rows with RoPE positions pos[].  Keys/values for
  * attention: if kv_cached != NULL, K_full = [gathered cached rows ‖ this pass's rows]
  * (src/diffuse-graph.cpp:497-525); else just this pass's rows.  The per-layer
  * K/V of this pass (after RoPE + GQA expansion) are returned in k_out/v_out. */
 static int run_layers(const orc_model * md, const int32_t * tok, const int32_t * pos, int M,
                       const orc_kv * kv_cached, const int32_t * cached_pos, int n_cached,
-                      float * logits, float * k_out, float * v_out, int n_threads) {
+                      float * logits, float * k_out, float * v_out, int n_threads,
+                      const pass_opts & opt = pass_opts()) {
     const int d = md->n_embd, H = md->n_head, Hkv = md->n_head_kv, hd = d / H;
     const int dkv = Hkv * hd, F = md->n_ff, L = md->n_layer;
     const float eps = md->rms_norm_eps;
@@ -614,9 +648,16 @@ static int run_layers(const orc_model * md, const int32_t * tok, const int32_t *
         g((size_t)M * F), u((size_t)M * F);
     const int n_keys = n_cached + M;
     std::vector<float> kf((size_t)n_keys * d), vf((size_t)n_keys * d);
+    std::vector<int32_t> kpos(n_keys);
+    for (int c = 0; c < n_cached; c++) kpos[c] = cached_pos[c];
+    for (int m = 0; m < M; m++) kpos[n_cached + m] = pos[m];
+    const key_vis vis = {pos, kpos.data(), opt.window};
+    std::vector<float> x_in;
     embed(md, tok, M, x.data());
 
     for (int il = 0; il < L; il++) {
+        if (opt.skip && opt.skip[il]) continue;   /* src/ar-graph.cpp:98-102 */
+        if (opt.impact) x_in = x;
         const orc_layer & ly = md->layers[il];
         std::vector<float> w = to_f32(ly.attn_norm);
         orc_rms_norm_mul(x.data(), w.data(), M, d, eps, h.data());
@@ -648,7 +689,7 @@ static int run_layers(const orc_model * md, const int32_t * tok, const int32_t *
             kk = kf.data();
             vv = vf.data();
         }
-        attention(q.data(), kk, vv, M, n_keys, H, hd, att.data(), n_threads);
+        attention(q.data(), kk, vv, M, n_keys, H, hd, att.data(), n_threads, opt.causal ? &vis : nullptr);
         if (orc_mul_mat(ly.wo.type, ly.wo.data, d, d, att.data(), M, o.data(), n_threads)) return -1;
         for (size_t i = 0; i < x.size(); i++) x[i] = o[i] + x[i];
 
@@ -659,10 +700,25 @@ static int run_layers(const orc_model * md, const int32_t * tok, const int32_t *
         for (size_t i = 0; i < g.size(); i++) g[i] = orc_silu(g[i]) * u[i];
         if (orc_mul_mat(ly.ffn_down.type, ly.ffn_down.data, d, F, g.data(), M, o.data(), n_threads)) return -1;
         for (size_t i = 0; i < x.size(); i++) x[i] = o[i] + x[i];
+        if (opt.impact) {
+            /* ggml_sum(ggml_sqr(ggml_sub(out, in))) (src/ar-graph.cpp:219-228): float
+             * differences and squares, each row summed in double, rows added in double */
+            double tot = 0.0;
+            for (int m = 0; m < M; m++) {
+                double rs = 0.0;
+                for (int i = 0; i < d; i++) {
+                    const float df = x[(size_t)m * d + i] - x_in[(size_t)m * d + i];
+                    rs += (double)(df * df);
+                }
+                tot += rs;
+            }
+            opt.impact[il] = (float)tot;
+        }
     }
     std::vector<float> w = to_f32(md->output_norm);
-    orc_rms_norm_mul(x.data(), w.data(), M, d, eps, h.data());
-    return orc_mul_mat(md->output.type, md->output.data, md->n_vocab, d, h.data(), M, logits, n_threads);
+    const int hf = opt.head_from;
+    orc_rms_norm_mul(x.data() + (size_t)hf * d, w.data(), M - hf, d, eps, h.data());
+    return orc_mul_mat(md->output.type, md->output.data, md->n_vocab, d, h.data(), M - hf, logits, n_threads);
 }
 
 extern "C" int orc_forward_full(const orc_model * md, const int32_t * tokens, int n, float * logits,
@@ -875,5 +931,165 @@ extern "C" int orc_generate(const orc_model * md, const int32_t * prompt, int n_
         }
     }
     memcpy(out, seq.data() + n_prompt, (size_t)n_generate * 4);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Autoregressive path (src/ar-graph.cpp, src/ar-cache.h, src/ar-sampler.cpp)  */
+/* ------------------------------------------------------------------------ */
+/* Forward of n_new tokens at positions n_past.. over the append-only cache
+ * (src/ar-graph.cpp:262-399): keys are cache rows 0..n_past-1 then the new rows,
+ * causal mask (+ sliding window), skipped layers leave their cache rows alone.
+ * logits: [n_new][V], or only the last row's [V] when last_only. */
+extern "C" int orc_ar_forward(const orc_model * md, const int32_t * tokens, int n_new, orc_ar_cache * c,
+                              float * logits, int last_only, int profile, int n_threads) {
+    if (n_new <= 0 || c->n_past + n_new > c->n_ctx_max) return -1;
+    const int d = md->n_embd, L = md->n_layer;
+    std::vector<int32_t> pos(n_new), cpos(c->n_past);
+    for (int i = 0; i < n_new; i++) pos[i] = c->n_past + i;
+    std::iota(cpos.begin(), cpos.end(), 0);
+    const orc_kv kv = {c->n_ctx_max, c->k, c->v};
+    const size_t per = (size_t)n_new * d;
+    std::vector<float> ko(per * L), vo(per * L);
+    pass_opts opt;
+    opt.causal = true;
+    opt.window = c->sliding_window;
+    opt.skip = profile ? nullptr : c->skip;
+    opt.impact = profile ? c->impact : nullptr;
+    opt.head_from = last_only ? n_new - 1 : 0;
+    const int rc = run_layers(md, tokens, pos.data(), n_new, c->n_past ? &kv : nullptr, cpos.data(), c->n_past, logits,
+                              ko.data(), vo.data(), n_threads, opt);
+    if (rc) return rc;
+    /* append (src/ar-cache.h:129-155) for the layers that ran */
+    const size_t cap = (size_t)c->n_ctx_max * d;
+    for (int il = 0; il < L; il++) {
+        if (opt.skip && opt.skip[il]) continue;
+        memcpy(c->k + il * cap + (size_t)c->n_past * d, ko.data() + il * per, per * 4);
+        memcpy(c->v + il * cap + (size_t)c->n_past * d, vo.data() + il * per, per * 4);
+    }
+    c->n_past += n_new;
+    return 0;
+}
+
+/* ar_profile_layers' choice (src/ar-graph.cpp:454-505): layers ranked by (impact,
+ * index) ascending; the first n_skip outside the two first and two last layers are
+ * skipped.  Returns how many were marked. */
+extern "C" int orc_ar_choose_skip(const float * impact, int n_layer, int n_skip, uint8_t * skip) {
+    memset(skip, 0, (size_t)n_layer);
+    if (n_skip <= 0) return 0;
+    std::vector<std::pair<float, int>> ranked;
+    for (int il = 0; il < n_layer; il++) ranked.push_back({impact[il], il});
+    std::sort(ranked.begin(), ranked.end());
+    int skipped = 0;
+    for (auto & r : ranked) {
+        if (skipped >= n_skip) break;
+        if (r.second < 2 || r.second >= n_layer - 2) continue;
+        skip[r.second] = 1;
+        skipped++;
+    }
+    return skipped;
+}
+
+/* sample_token and its filters (src/ar-sampler.cpp:11-140), on a copy of the row. */
+static void ar_top_k(float * lg, int V, int top_k) {
+    if (top_k <= 0 || top_k >= V) return;
+    std::vector<float> tmp(lg, lg + V);
+    std::nth_element(tmp.begin(), tmp.begin() + top_k, tmp.end(), std::greater<float>());
+    const float threshold = tmp[top_k - 1];
+    for (int i = 0; i < V; i++)
+        if (lg[i] < threshold) lg[i] = -INFINITY;
+}
+
+static void ar_top_p(float * lg, int V, float top_p) {
+    if (top_p >= 1.0f) return;
+    const float mx = *std::max_element(lg, lg + V);
+    float sum = 0.0f;
+    for (int i = 0; i < V; i++) { lg[i] = expf(lg[i] - mx); sum += lg[i]; }
+    for (int i = 0; i < V; i++) lg[i] /= sum;
+    std::vector<int> idx(V);
+    std::iota(idx.begin(), idx.end(), 0);
+    std::sort(idx.begin(), idx.end(), [&](int a, int b) { return lg[a] > lg[b]; });
+    float cum = 0.0f;
+    int cutoff = V;
+    for (int i = 0; i < V; i++) {
+        cum += lg[idx[i]];
+        if (cum >= top_p) { cutoff = i + 1; break; }
+    }
+    for (int i = cutoff; i < V; i++) lg[idx[i]] = 0.0f;
+    for (int i = 0; i < V; i++) lg[i] = lg[i] > 0.0f ? logf(lg[i]) : -INFINITY;
+}
+
+struct orc_rng { std::mt19937 g; };
+
+extern "C" orc_rng * orc_rng_new(uint32_t seed) { return new orc_rng{std::mt19937(seed)}; }
+extern "C" void orc_rng_free(orc_rng * r) { delete r; }
+
+extern "C" int orc_ar_sample(const float * row, int V, const orc_ar_params * p, const int32_t * recent, int n_recent,
+                             orc_rng * rng) {
+    std::vector<float> lg(row, row + V);
+    if (p->repeat_penalty > 1.0f)
+        for (int j = 0; j < n_recent; j++) {
+            const int32_t t = recent[j];
+            if (t >= 0 && t < V) lg[t] = lg[t] > 0.0f ? lg[t] / p->repeat_penalty : lg[t] * p->repeat_penalty;
+        }
+    if (p->temperature <= 0.0f) {
+        int best = 0;
+        float bv = lg[0];
+        for (int i = 1; i < V; i++)
+            if (lg[i] > bv) { bv = lg[i]; best = i; }
+        return best;
+    }
+    for (int i = 0; i < V; i++) lg[i] /= p->temperature;
+    ar_top_k(lg.data(), V, p->top_k);
+    ar_top_p(lg.data(), V, p->top_p);
+    const float mx = *std::max_element(lg.begin(), lg.end());
+    float sum = 0.0f;
+    std::vector<float> probs(V);
+    for (int i = 0; i < V; i++) { probs[i] = expf(lg[i] - mx); sum += probs[i]; }
+    for (int i = 0; i < V; i++) probs[i] /= sum;
+    std::discrete_distribution<int> dist(probs.begin(), probs.end());
+    return dist(rng->g);
+}
+
+/* ar_generate (src/ar-sampler.cpp:143-314). */
+extern "C" int orc_ar_generate(const orc_model * md, const int32_t * prompt, int n_prompt, int max_tokens,
+                               const orc_ar_params * p, int32_t * out, int * n_out, uint8_t * skip_out,
+                               int n_threads) {
+    const int V = md->n_vocab, L = md->n_layer, d = md->n_embd;
+    *n_out = 0;
+    /* the reference samples one token from the prefill whatever max_tokens is */
+    if (n_prompt <= 0 || max_tokens < 0) return -1;
+    orc_ar_cache c;
+    c.n_ctx_max = n_prompt + std::max(max_tokens, 1);
+    c.n_past = 0;
+    c.sliding_window = p->sliding_window;
+    std::vector<float> kc((size_t)L * c.n_ctx_max * d, 0.0f), vc((size_t)L * c.n_ctx_max * d, 0.0f);
+    std::vector<uint8_t> skip(L, 0);
+    std::vector<float> impact(L, 0.0f);
+    c.k = kc.data();
+    c.v = vc.data();
+    c.skip = skip.data();
+    c.impact = impact.data();
+    std::mt19937 gen(p->seed);
+    orc_rng rng{gen};
+    std::vector<float> lg(V);
+    const bool prof = p->layer_skip > 0;
+    if (orc_ar_forward(md, prompt, n_prompt, &c, lg.data(), 1, prof, n_threads)) return -1;
+    if (prof) orc_ar_choose_skip(impact.data(), L, p->layer_skip, skip.data());
+    if (skip_out) memcpy(skip_out, skip.data(), (size_t)L);
+    std::vector<int32_t> recent;
+    for (int i = std::max(0, n_prompt - p->repeat_last_n); i < n_prompt; i++) recent.push_back(prompt[i]);
+    auto push = [&](int32_t t) {
+        out[(*n_out)++] = t;
+        recent.push_back(t);
+        if ((int)recent.size() > p->repeat_last_n) recent.erase(recent.begin());
+    };
+    push(orc_ar_sample(lg.data(), V, p, recent.data(), (int)recent.size(), &rng));
+    for (int i = 1; i < max_tokens; i++) {
+        const int32_t last = out[*n_out - 1];
+        if (last == 151643 || last == 151645 || last == 151644) break;   /* src/ar-sampler.cpp:253-260 */
+        if (orc_ar_forward(md, &last, 1, &c, lg.data(), 1, 0, n_threads)) return -1;
+        push(orc_ar_sample(lg.data(), V, p, recent.data(), (int)recent.size(), &rng));
+    }
     return 0;
 }

@@ -146,6 +146,50 @@ typedef struct {
 int orc_generate(const orc_model * m, const int32_t * prompt, int n_prompt, int n_generate,
                  const orc_sampler_params * p, int32_t * out, orc_gen_stats * stats, int n_threads);
 
+/* ---- autoregressive path (src/ar-graph.cpp, src/ar-cache.h, src/ar-sampler.cpp) ---- */
+/* Causal attention: key n visible to query m when kpos[n] <= qpos[m] and, with window > 0,
+ * qpos[m] - kpos[n] < window (src/ar-graph.cpp:70-88). */
+void orc_attention_causal(const float * q, const float * k, const float * v, int M, int n_keys, int H, int hd,
+                          const int32_t * qpos, const int32_t * kpos, int window, float * out, int n_threads);
+
+/* Append-only cache, k/v [n_layer][n_ctx_max][n_head*head_dim] after RoPE and GQA
+ * expansion; positions 0..n_past-1 valid. */
+typedef struct {
+    int       n_ctx_max, n_past, sliding_window;
+    float *   k;
+    float *   v;
+    uint8_t * skip;     /* [n_layer] layers left out of non-profiling passes */
+    float *   impact;   /* [n_layer] filled by a profiling pass */
+} orc_ar_cache;
+
+/* ar_sampler_params (include/diffuse.h:96-107). */
+typedef struct {
+    float    temperature, top_p;
+    int      top_k;
+    float    repeat_penalty;
+    int      repeat_last_n;
+    uint32_t seed;
+    int      layer_skip, sliding_window;
+} orc_ar_params;
+
+/* ar_forward_impl (src/ar-graph.cpp:262-399): n_new tokens at positions n_past..; logits
+ * [n_new][V], or the last row's only; profile = the layer-impact pass of
+ * ar_profile_layers (every layer runs, impacts written). */
+int orc_ar_forward(const orc_model * m, const int32_t * tokens, int n_new, orc_ar_cache * c, float * logits,
+                   int last_only, int profile, int n_threads);
+int orc_ar_choose_skip(const float * impact, int n_layer, int n_skip, uint8_t * skip);
+
+typedef struct orc_rng orc_rng;   /* std::mt19937 */
+orc_rng * orc_rng_new(uint32_t seed);
+void      orc_rng_free(orc_rng * r);
+/* sample_token (src/ar-sampler.cpp:99-140) on a copy of row. */
+int orc_ar_sample(const float * row, int V, const orc_ar_params * p, const int32_t * recent, int n_recent,
+                  orc_rng * rng);
+/* ar_generate (src/ar-sampler.cpp:143-314): out gets up to max(max_tokens, 1) ids, *n_out how many;
+ * skip_out (n_layer bytes, optional) the skipped-layer mask chosen by profiling. */
+int orc_ar_generate(const orc_model * m, const int32_t * prompt, int n_prompt, int max_tokens,
+                    const orc_ar_params * p, int32_t * out, int * n_out, uint8_t * skip_out, int n_threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,6 +23,34 @@ TINY_DREAM = dict(n_vocab=1280, n_embd=512, n_head=8, n_head_kv=2, n_layer=3, n_
                   rope_theta=1000000.0, rms_norm_eps=1e-6, mask_token_id=1270, is_dream=1)
 # K spans several 2048-element chunks (O: 2304 = 2048 + 256, down: 4608 = 3 chunks), so the
 # O / down GEMMs split K and hand their chunk sums to the next RMSNorm.
+# six layers, so that layers 2 and 3 can be skipped by the autoregressive layer skip (the
+# first and last two are protected)
+TINY_LLADA6 = dict(TINY_LLADA, n_layer=6)
+# vocabulary reaching the end tokens of the autoregressive sampler (151643 / 151645 / 151644)
+EOS_ARCH = dict(n_vocab=151680, n_embd=256, n_head=2, n_head_kv=2, n_layer=2, n_ff=512,
+                rope_theta=1000000.0, rms_norm_eps=1e-6, mask_token_id=151666, is_dream=0)
+
+
+def eos_model(path):
+    """A model whose head scores only two end tokens: output rows 151643 = +u, 151645 = -u
+    (u random), every other row zero, so greedy decoding ends at the first token."""
+    import dfx
+    import oracle_py as O
+    dfx.synth_model(path, EOS_ARCH, scheme="f32", seed=5, sigma=0.05, n_threads=4)
+    ti = O.GGUF(path).tensor("output.weight")
+    assert ti["type"] == O.F32
+    off = ti["start"]
+    mm = np.memmap(path, dtype=np.uint8, mode="r+")
+    w = mm[off:off + EOS_ARCH["n_vocab"] * EOS_ARCH["n_embd"] * 4].view(np.float32).reshape(EOS_ARCH["n_vocab"], -1)
+    u = np.random.default_rng(6).standard_normal(EOS_ARCH["n_embd"]).astype(np.float32)
+    w[:] = 0.0
+    w[151643] = u
+    w[151645] = -u
+    mm.flush()
+    del mm
+    return str(path)
+
+
 TINY_LLADA_LONGK = dict(n_vocab=1024, n_embd=2304, n_head=18, n_head_kv=18, n_layer=2, n_ff=4608,
                         rope_theta=500000.0, rms_norm_eps=1e-5, mask_token_id=1000, is_dream=0)
 

@@ -46,6 +46,14 @@ def oracle():
         L.orc_forward_full.argtypes = [P, P, I, P, P, I]
         L.orc_forward_cached.argtypes = [P, P, P, I, I, P, P, P, I]
         L.orc_generate.argtypes = [P, P, I, I, P, P, P, I]
+        L.orc_attention_causal.argtypes = [P, P, P, I, I, I, I, P, P, I, P, I]
+        L.orc_ar_forward.argtypes = [P, P, I, P, P, I, I, I]
+        L.orc_ar_choose_skip.argtypes = [P, I, I, P]
+        L.orc_rng_new.restype = P
+        L.orc_rng_new.argtypes = [C.c_uint32]
+        L.orc_rng_free.argtypes = [P]
+        L.orc_ar_sample.argtypes = [P, I, P, P, I, P]
+        L.orc_ar_generate.argtypes = [P, P, I, I, P, P, P, P, I]
         _o = L
     return _o
 
@@ -132,6 +140,22 @@ def attention(q, k, v, n_threads=8):
     return out
 
 
+def attention_causal(q, k, v, qpos, kpos, window=0, n_threads=8):
+    """attention with key n visible to query m when kpos[n] <= qpos[m] (and, with a window
+    w > 0, qpos[m] - kpos[n] < w); shapes as attention()."""
+    M, H, hd = q.shape
+    rep = H // k.shape[1]
+    ke = np.ascontiguousarray(np.repeat(k, rep, axis=1), dtype=np.float32)
+    ve = np.ascontiguousarray(np.repeat(v, rep, axis=1), dtype=np.float32)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    qp = np.ascontiguousarray(qpos, dtype=np.int32)
+    kp = np.ascontiguousarray(kpos, dtype=np.int32)
+    out = np.empty((M, H, hd), np.float32)
+    oracle().orc_attention_causal(ptr(q), ptr(ke), ptr(ve), M, k.shape[0], H, hd, ptr(qp), ptr(kp), window,
+                                  ptr(out), n_threads)
+    return out
+
+
 def entropy(row):
     row = np.ascontiguousarray(row, dtype=np.float32)
     return oracle().orc_entropy(ptr(row), row.size)
@@ -151,6 +175,19 @@ def order_candidates(cand, remasking, tau, n_sched):
     c = np.ascontiguousarray(cand.copy(), dtype=CAND)
     n = oracle().orc_order_candidates(ptr(c), len(c), remasking, tau, n_sched)
     return c, n
+
+
+def ar_sample(row, params, recent, rng):
+    row = np.ascontiguousarray(row, dtype=np.float32)
+    rec = np.ascontiguousarray(recent, dtype=np.int32)
+    return oracle().orc_ar_sample(ptr(row), row.size, C.byref(params), ptr(rec), len(rec), rng)
+
+
+def choose_skip(impact, n_skip):
+    imp = np.ascontiguousarray(impact, dtype=np.float32)
+    skip = np.zeros(len(imp), dtype=np.uint8)
+    n = oracle().orc_ar_choose_skip(ptr(imp), len(imp), n_skip, ptr(skip))
+    return skip, n
 
 
 def tokens_to_unmask(step, total, masked, schedule):
@@ -218,6 +255,7 @@ class GGUF:
             nb = row_bytes(ti["type"], n0) * rows
             start = data0 + ti["offset"]
             ti["data"] = self.buf[start:start + nb]
+            ti["start"] = start
             ti["rows"] = rows
 
     def tensor(self, name):
@@ -250,6 +288,36 @@ class OrcSamplerParams(C.Structure):
     _fields_ = [("n_steps", C.c_int), ("temperature", C.c_float), ("schedule", C.c_int), ("remasking", C.c_int),
                 ("seed", C.c_uint32), ("entropy_threshold", C.c_float), ("use_cache", C.c_int),
                 ("cache_refresh", C.c_int), ("cache_keep_active", C.c_int)]
+
+
+class OrcArCache(C.Structure):
+    _fields_ = [("n_ctx_max", C.c_int), ("n_past", C.c_int), ("sliding_window", C.c_int), ("k", C.c_void_p),
+                ("v", C.c_void_p), ("skip", C.c_void_p), ("impact", C.c_void_p)]
+
+
+class OrcArParams(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_int),
+                ("repeat_penalty", C.c_float), ("repeat_last_n", C.c_int), ("seed", C.c_uint32),
+                ("layer_skip", C.c_int), ("sliding_window", C.c_int)]
+
+    @classmethod
+    def make(cls, temperature=0.0, top_p=0.9, top_k=40, repeat_penalty=1.1, repeat_last_n=64, seed=42,
+             layer_skip=0, sliding_window=0):
+        """Defaults of ar_sampler_params (include/diffuse.h:96-107)."""
+        return cls(temperature, top_p, top_k, repeat_penalty, repeat_last_n, seed, layer_skip, sliding_window)
+
+
+class OracleArCache:
+    """Append-only AR cache of the oracle (k/v expanded to n_head, f32)."""
+
+    def __init__(self, om, n_ctx_max, sliding_window=0):
+        m = om.m
+        self.k = np.zeros(m.n_layer * n_ctx_max * m.n_embd, dtype=np.float32)
+        self.v = np.zeros_like(self.k)
+        self.skip = np.zeros(m.n_layer, dtype=np.uint8)
+        self.impact = np.zeros(m.n_layer, dtype=np.float32)
+        self.c = OrcArCache(n_ctx_max, 0, sliding_window, self.k.ctypes.data, self.v.ctypes.data,
+                            self.skip.ctypes.data, self.impact.ctypes.data)
 
 
 class OrcGenStats(C.Structure):
@@ -354,6 +422,25 @@ class OracleModel:
                                          ptr(cached), ptr(logits), n_threads)
         assert rc == 0
         return logits
+
+    def ar_forward(self, cache, tokens, last_only=False, profile=False, n_threads=8):
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        rows = 1 if last_only else len(t)
+        logits = np.empty((rows, self.m.n_vocab), dtype=np.float32)
+        rc = oracle().orc_ar_forward(C.byref(self.m), ptr(t), len(t), C.byref(cache.c), ptr(logits),
+                                     1 if last_only else 0, 1 if profile else 0, n_threads)
+        assert rc == 0
+        return logits
+
+    def ar_generate(self, prompt, max_tokens, params, n_threads=8):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.empty(max(max_tokens, 1), dtype=np.int32)
+        n = C.c_int()
+        skip = np.zeros(self.m.n_layer, dtype=np.uint8)
+        rc = oracle().orc_ar_generate(C.byref(self.m), ptr(prompt), len(prompt), max_tokens, C.byref(params),
+                                      ptr(out), C.byref(n), ptr(skip), n_threads)
+        assert rc == 0
+        return out[:n.value], skip
 
     def generate(self, prompt, n_generate, n_steps=16, temperature=0.0, schedule=0, remasking=0, seed=42,
                  entropy_threshold=1.5, use_cache=True, cache_refresh=0, cache_keep_active=0, n_threads=8):

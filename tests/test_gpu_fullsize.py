@@ -89,3 +89,27 @@ def test_llada8b_width_f16_long_context_unit(gpu):
     arch = dict(dfx.LLADA_8B, n_layer=2)
     path = big_model("llada8b-2l", arch, "f16", 5)
     _step0_and_cached(path, 512, 256, 5, 126000, 1, exact=False)
+
+
+def test_dream7b_q4km_autoregressive_prefill_and_decode(gpu):
+    """The autoregressive path at Dream-7B size (GQA 28/4, Q/K/V bias, V = 152064): a
+    32-token causal prefill, then greedy ar_generate of 4 tokens against the oracle's
+    ar_generate (the same floats, so the same tokens)."""
+    path = big_model("dream7b", dfx.DREAM_7B, "q4_k_m", 2)
+    om = O.OracleModel(path)
+    prompt = np.random.default_rng(3).integers(0, 151643, 32).astype(np.int32)
+    model = dfx.Model(path)
+    ctx = dfx.Context(model, 64)
+    try:
+        cache = O.OracleArCache(om, 64)
+        ref = om.ar_forward(cache, prompt, last_only=True, n_threads=THREADS)
+        got = ctx.ar_forward(prompt, reset=True)[-1:]
+        same = _report("ar prefill (M=32, last row)", got, ref, np.arange(1))
+        assert same == 1.0
+        ref_toks, _ = om.ar_generate(prompt, 4, O.OrcArParams.make(), n_threads=THREADS)
+        got_toks = ctx.ar_generate(prompt, 4, dfx.ArParams.make())
+        print(f"[fullsize] ar_generate greedy: {list(got_toks)} vs oracle {list(ref_toks)}", flush=True)
+        assert list(got_toks) == list(ref_toks)
+    finally:
+        ctx.close()
+        model.close()

@@ -1,4 +1,5 @@
 """Kernel-level parity of the HIP path (through the C ABI) against the CPU oracle."""
+import contextlib
 import ctypes as C
 
 import numpy as np
@@ -133,6 +134,15 @@ GEMM_CASES = [(dfx.TYPE_Q4_K, 4096, 4096, m) for m in (1, 5, 50, 96, 128, 255, 2
     (dfx.TYPE_Q6_K, 152064, 3584, 64)]
 
 
+@contextlib.contextmanager
+def forced_tile(wtype, spec):
+    dfx.force_tile(wtype, spec)
+    try:
+        yield
+    finally:
+        dfx.force_tile(wtype, None)
+
+
 def gpu_gemm(typ, raw, N, K, X, ws=True):
     M = X.shape[0]
     w = to_device_weights(typ, raw, N, K)
@@ -156,40 +166,40 @@ def test_gemm_quantized_bit_exact(gpu, typ, N, K, M):
 
 @pytest.mark.parametrize("tile", ["2x2x2", "4x1x2", "2x1x2", "1x2x2", "1x1x4", "1x1x2", "2x1x4", "2x2x4", "w", "w1"])
 @pytest.mark.parametrize("N,K,M", [(1000, 2048, 77), (4096, 4096, 288)])
-def test_gemm_q4k_every_tile_bit_exact(gpu, monkeypatch, tile, N, K, M):
-    """Every register tile of the Q4_K kernel (forced with DFX_Q4K_TILE), with ragged
+def test_gemm_q4k_every_tile_bit_exact(gpu, tile, N, K, M):
+    """Every register tile of the Q4_K kernel (forced with dfx_gemm_force_tile), with ragged
     N and M, reproduces the oracle bit for bit."""
-    monkeypatch.setenv("DFX_Q4K_TILE", tile)
     raw = quant(dfx.TYPE_Q4_K, N, K)
     X = rng.standard_normal((M, K)).astype(np.float32)
-    got = gpu_gemm(dfx.TYPE_Q4_K, raw, N, K, X)
+    with forced_tile(dfx.TYPE_Q4_K, tile):
+        got = gpu_gemm(dfx.TYPE_Q4_K, raw, N, K, X)
     ref = O.mul_mat(dfx.TYPE_Q4_K, raw, N, K, X)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
 
 
 @pytest.mark.parametrize("tile", ["1x1x4s", "2x1x2s", "1x2x2s", "2x1x4s", "ws", "w1s"])
 @pytest.mark.parametrize("N,K,M", [(512, 12288, 70), (1000, 3584, 33), (640, 2304, 40), (4096, 4096, 256)])
-def test_gemm_q4k_split_k_bit_exact(gpu, monkeypatch, tile, N, K, M):
+def test_gemm_q4k_split_k_bit_exact(gpu, tile, N, K, M):
     """Split K (one workgroup per 2048-element chunk, chunk sums added in order by the
     reduction) gives the same bits as the oracle's chunked K order; covers a short last
     chunk (3584 = 2048 + 1536) and a last chunk of one super-block (2304)."""
-    monkeypatch.setenv("DFX_Q4K_TILE", tile)
     raw = quant(dfx.TYPE_Q4_K, N, K)
     X = rng.standard_normal((M, K)).astype(np.float32)
-    got = gpu_gemm(dfx.TYPE_Q4_K, raw, N, K, X)
+    with forced_tile(dfx.TYPE_Q4_K, tile):
+        got = gpu_gemm(dfx.TYPE_Q4_K, raw, N, K, X)
     ref = O.mul_mat(dfx.TYPE_Q4_K, raw, N, K, X)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
 
 
 @pytest.mark.parametrize("tile", ["2x1n", "1x1n", "2x1s", "1x1s", "2x1x4n", "2x1x4s", "1x1x4s"])
 @pytest.mark.parametrize("N,K,M", [(1000, 4096, 77), (640, 12288, 40), (300, 2304, 33)])
-def test_gemm_q6k_tiles_and_split_bit_exact(gpu, monkeypatch, tile, N, K, M):
+def test_gemm_q6k_tiles_and_split_bit_exact(gpu, tile, N, K, M):
     """Q6_K kernel tiles, with and without split K (scales up to +-127 exercise the
     exact f16 operand split), against the oracle bit for bit."""
-    monkeypatch.setenv("DFX_Q6K_TILE", tile)
     raw = quant(dfx.TYPE_Q6_K, N, K)
     X = rng.standard_normal((M, K)).astype(np.float32)
-    got = gpu_gemm(dfx.TYPE_Q6_K, raw, N, K, X)
+    with forced_tile(dfx.TYPE_Q6_K, tile):
+        got = gpu_gemm(dfx.TYPE_Q6_K, raw, N, K, X)
     ref = O.mul_mat(dfx.TYPE_Q6_K, raw, N, K, X)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
 
