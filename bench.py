@@ -161,6 +161,38 @@ def config_dream():
             "rows_per_step": [st.rows_per_step[i] for i in range(st.actual_steps)]}
 
 
+DREAM_Q4KM_WEIGHT_BYTES = 4.223e9   # Dream-7B Q4_K_M matrices (embedding excluded), read once per decode pass
+
+
+def config_ar(reps=3):
+    """ar_generate on Dream-7B Q4_K_M (the Qwen2 architecture the reference's AR path targets):
+    prompt 64, 128 greedy tokens (temperature 0, repeat penalty 1.1 over 64), 1 warm-up + reps.
+    Decode is one pass over every weight per token: its HBM rate is the matrices' bytes
+    over the mean time per decoded token."""
+    path = ensure_model("dream7b", dfx.DREAM_7B, "q4_k_m", 2)
+    model = dfx.Model(path)
+    prompt = np.random.default_rng(3).integers(0, 151643, 64).astype(np.int32)
+    ctx = dfx.Context(model, 64 + 128)
+    params = dfx.ArParams.make(temperature=0.0)
+    runs = []
+    for i in range(1 + reps):
+        st = dfx.ArStats()
+        toks = ctx.ar_generate(prompt, 128, params, stats=st)
+        if i:
+            runs.append((st.prefill_ms, st.decode_ms, st.n_decoded, st.total_ms, len(toks)))
+    ctx.close()
+    model.close()
+    pre = float(np.mean([r[0] for r in runs]))
+    dec_ms = float(np.mean([r[1] / max(r[2], 1) for r in runs]))
+    tot = float(np.mean([r[3] for r in runs]))
+    gbs = DREAM_Q4KM_WEIGHT_BYTES / (dec_ms * 1e-3) / 1e9
+    return {"workload": "ar_generate, Dream-7B Q4_K_M, prompt 64, 128 tokens greedy (repeat penalty 1.1 / 64)",
+            "prefill_ms": round(pre, 3), "prefill_tok_s": round(64 / (pre * 1e-3), 1),
+            "decode_ms_per_token": round(dec_ms, 4), "decode_tok_s": round(1000.0 / dec_ms, 1),
+            "gen_tok_s": round(runs[0][4] / (tot * 1e-3), 1), "generated": runs[0][4],
+            "decode_weight_gbs": round(gbs, 1), "decode_frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def config_sampler():
     """The sampler over [256 x 126464] f32 logits N(0, sigma), sigma in {0.5, 2, 8} (seed 4):
     row statistics (softmax max / sum, entropy, top-2), candidate records and the selection
@@ -300,6 +332,9 @@ def main():
         t = time.time()
         configs["sampler_256x126464"] = config_sampler()
         log(f"sampler workload took {time.time() - t:.1f}s")
+        t = time.time()
+        configs["ar_dream7b_q4km_decode"] = config_ar()
+        log(f"AR workload took {time.time() - t:.1f}s")
 
     cpu = None
     if not args.no_cpu:

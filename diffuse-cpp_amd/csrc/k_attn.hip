@@ -147,7 +147,7 @@ __device__ __forceinline__ double4v mfma_f64(double a, double b, double4v c) {
 // keys are the reduction: lane group g supplies keys 16s+4g+c to MFMA c, read as one
 // float4 of the transposed value cache, two key steps ahead.
 // Workgroups are numbered so that all query tiles of head h run on XCD h % 8.
-template <int HD>
+template <int HD, int KR>
 __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q, const float * __restrict__ kc,
                                                    const float * __restrict__ vt, int64_t v_ld, int M, int n_keys,
                                                    int H, int Hkv, int sstride, int q_tiles, int q_pos0, int window,
@@ -182,9 +182,9 @@ __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q,
 #pragma unroll
         for (int s = 0; s < SS; s++) kf[s] = ld4_or0(kr + 16 * s, n < n_keys);
     };
-    // key tiles t = wv + 4j in a three-slot register ring, two tiles in flight ahead
+    // key tiles t = wv + 4j in a KR-slot register ring, KR - 1 tiles in flight ahead
     // of the one being multiplied (slot roles fixed by unrolling, so no copies)
-    float4 kr[3][SS];
+    float4 kr[KR][SS];
     auto tile = [&](float4 (&kf)[SS], int t) __attribute__((always_inline)) {
         double4v a[4] = {0.0, 0.0, 0.0, 0.0};      // four independent chains: MFMA c of each step
 #pragma unroll
@@ -204,15 +204,15 @@ __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q,
         }
     };
 #pragma unroll
-    for (int u = 0; u < 3; u++)
+    for (int u = 0; u < KR; u++)
         if (wv + 4 * u < ntiles) load_k(kr[u], wv + 4 * u);
-    for (int t0 = wv; t0 < ntiles; t0 += 12) {
+    for (int t0 = wv; t0 < ntiles; t0 += 4 * KR) {
 #pragma unroll
-        for (int u = 0; u < 3; u++) {
+        for (int u = 0; u < KR; u++) {
             const int t = t0 + 4 * u;
             if (t < ntiles) {
                 tile(kr[u], t);
-                if (t + 12 < ntiles) load_k(kr[u], t + 12);
+                if (t + 4 * KR < ntiles) load_k(kr[u], t + 4 * KR);
             }
         }
     }
@@ -730,6 +730,10 @@ static inline int attn_sstride(int64_t n_keys) { return (int)(((n_keys + 15) / 1
 // Score-row stride of the split-bf16 kernel: whole 32-key tiles, plus 4 floats.
 static inline int attn_split_sstride(int64_t n_keys) { return (int)(((n_keys + 31) / 32) * 32 + 4); }
 
+#ifndef ATTN_KR
+#define ATTN_KR 2   // key-tile ring of the 128-wide kernel: two slots keep it at two waves per SIMD
+#endif
+
 // The exact (f64-summed) kernels: scores kept in LDS when a 16-row tile of them fits,
 // else recomputed in three passes.  q_pos0 / window: the causal mask (q_pos0 < 0: none).
 static int attn_exact(const float * q, const float * kc, const float * vt, int64_t v_ld, int M, int n_keys, int H,
@@ -740,10 +744,10 @@ static int attn_exact(const float * q, const float * kc, const float * vt, int64
     const dim3 grid((unsigned)(8 * ((H + 7) / 8) * q_tiles));
     if (lds <= attn_lds_limit()) {
         if (hd == 128)
-            hipLaunchKernelGGL((k_attn_mfma<128>), grid, dim3(256), lds, st, q, kc, vt, v_ld, M, n_keys, H, Hkv,
+            hipLaunchKernelGGL((k_attn_mfma<128, ATTN_KR>), grid, dim3(256), lds, st, q, kc, vt, v_ld, M, n_keys, H, Hkv,
                                sstride, q_tiles, q_pos0, window, out);
         else
-            hipLaunchKernelGGL((k_attn_mfma<64>), grid, dim3(256), lds, st, q, kc, vt, v_ld, M, n_keys, H, Hkv,
+            hipLaunchKernelGGL((k_attn_mfma<64, 3>), grid, dim3(256), lds, st, q, kc, vt, v_ld, M, n_keys, H, Hkv,
                                sstride, q_tiles, q_pos0, window, out);
     } else if (hd == 128) {   // score rows longer than the LDS holds: recomputed in three passes
         hipLaunchKernelGGL((k_attn_long<128>), grid, dim3(256), 0, st, q, kc, vt, v_ld, M, n_keys, H, Hkv, q_tiles,

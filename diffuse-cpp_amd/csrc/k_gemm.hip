@@ -720,15 +720,17 @@ __device__ __forceinline__ void barrier_only() {
 }
 typedef __attribute__((address_space(3))) void * lds_ptr;
 
-template <int TN, int DEPTH>
+template <int TM, int TN, int DEPTH>
 __global__ void __launch_bounds__(256, TN == 1 ? 2 : 1)
 k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__ act, int M,
         const float * __restrict__ bias, const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
         int n_tiles, int m_tiles, float * __restrict__ ws) {
 #pragma clang fp contract(off)
-    constexpr int TM = 2, BM = 64, BN = 128 * TN, WSZ = 2048 * TN;   // WSZ: nibble bytes per wave and step
+    constexpr int BM = 32 * TM, BN = 128 * TN, WSZ = 2048 * TN;   // WSZ: nibble bytes per wave and step
+    constexpr int NA = 2 * TM;                                     // A operand copies per wave and step
     static_assert(DEPTH == 2 || DEPTH == 4, "ring depth 2 or 4");
     static_assert(TN == 1 || TN == 2, "one or two column tiles per wave");
+    static_assert(TM == 2 || TM == 3, "64- or 96-row tiles");
     // Separate arrays per ring slot: the compiler then knows that reading one slot
     // does not have to wait for the copies in flight into the others.
     __shared__ __attribute__((aligned(1024))) half_t As0[BM * 128], As1[BM * 128], As2[DEPTH > 2 ? BM * 128 : 8],
@@ -738,8 +740,8 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
         Ws3[DEPTH > 2 ? 4 * WSZ : 16];
     // header slots: [wave][lane][16 B] (TN 2: lane = t*32 + row; TN 1: rows repeat in both halves)
     __shared__ __attribute__((aligned(1024))) uint8_t Hs0[4 * 1024], Hs1[DEPTH > 2 ? 4 * 1024 : 16];
-    // scale slots: [0, 2 KB) block sums [row][16], [2 KB, 3 KB) d of rows m0.. (64 used)
-    __shared__ __attribute__((aligned(1024))) uint8_t Sc0[3 * 1024], Sc1[DEPTH > 2 ? 3 * 1024 : 16];
+    // scale slots: [0, TM KB) block sums [row][16], [TM KB, TM KB + 1 KB) d of rows m0.. (BM used)
+    __shared__ __attribute__((aligned(1024))) uint8_t Sc0[(TM + 1) * 1024], Sc1[DEPTH > 2 ? (TM + 1) * 1024 : 16];
     auto aslot = [&](auto stage) __attribute__((always_inline)) -> half_t * {
         constexpr int s = decltype(stage)::value;
         if constexpr (s == 0) return As0;
@@ -776,10 +778,12 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
     const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc((void *)act, 0, (int)Lay.bytes, 0x00020000);
 
     // per-lane byte offsets (fixed); the step moves only the scalar offsets
-    uint32_t off_a[4];   // this wave copies A operands 4wv..4wv+3 of the step: row tile f/8, operand f%8
+    // (arrays here have fixed sizes: this clang drops the host stub of a kernel template whose
+    // lambdas capture a local array sized by a template parameter)
+    uint32_t off_a[6];   // this wave copies A operands NA*wv.. of the step: row tile f/8, operand f%8
 #pragma unroll
-    for (int f = 0; f < 4; f++) {
-        const int ff = 4 * wv + f, mt = min(m0 / 32 + (ff >> 3), m_pad / 32 - 1);
+    for (int f = 0; f < NA; f++) {
+        const int ff = NA * wv + f, mt = min(m0 / 32 + (ff >> 3), m_pad / 32 - 1);
         off_a[f] = (uint32_t)Lay.q + (uint32_t)mt * (uint32_t)(K / 128) * 8192u + (uint32_t)(ff & 7) * 1024u +
                    (uint32_t)lane * 16u;
     }
@@ -789,12 +793,12 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
 #pragma unroll
     for (int t = 0; t < TN; t++) off_w[t] = (uint32_t)min(n0 + (wv * TN + t) * 32 + l32, N - 1) * row_bytes;
     const uint32_t off_h = (uint32_t)min(n0 + 32 * TN * wv + (TN == 2 ? lane : l32), N - 1) * row_bytes;
-    // scale copies (16 bytes a lane): waves 1, 2 the block sums of rows 32(wv-1) + lane/2,
-    // waves 0, 3 the same 1 KB of d from row m0 on (d is [sb][m_pad]; 64 of those rows
+    // scale copies (16 bytes a lane): waves below TM the block sums of rows 32 wv + lane/2,
+    // the others the same 1 KB of d from row m0 on (d is [sb][m_pad]; BM of those rows
     // are used; lanes past the buffer's end read nothing: the buffer's extent is set)
-    const bool bs_wave = wv == 1 || wv == 2;
+    const bool bs_wave = wv < TM;
     const uint32_t off_s = bs_wave
-        ? (uint32_t)Lay.bs + ((uint32_t)min(m0 + 32 * (wv - 1) + (lane >> 1), M - 1) * (uint32_t)(K / 16) +
+        ? (uint32_t)Lay.bs + ((uint32_t)min(m0 + 32 * wv + (lane >> 1), M - 1) * (uint32_t)(K / 16) +
                               (lane & 1) * 8u) * 2u
         : (uint32_t)Lay.d + (uint32_t)m0 * 4u + (uint32_t)lane * 16u;
     const int s_step = bs_wave ? 32 : m_pad * 4;   // bytes per super-block
@@ -812,15 +816,15 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
         if constexpr (DEPTH == 4 && ((s >> 1) & 1)) return Sc1;
         else return Sc0;
     };
-    const int sc_dst = bs_wave ? 1024 * (wv - 1) : 2048;   // this wave's copy within a scale slot
+    const int sc_dst = bs_wave ? 1024 * wv : 1024 * TM;   // this wave's copy within a scale slot
 
     auto issue = [&](auto stage, int kt_req) __attribute__((always_inline)) {
         constexpr int s = decltype(stage)::value, h = s & 1;
         const int kt = 2 * sb_first + min(kt_req, n_kt - 1);
         const int sb = kt >> 1;
 #pragma unroll
-        for (int f = 0; f < 4; f++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_ptr)(aslot(stage) + (4 * wv + f) * 512), 16, off_a[f],
+        for (int f = 0; f < NA; f++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_ptr)(aslot(stage) + (NA * wv + f) * 512), 16, off_a[f],
                                                      kt * 8192, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (h == 0)
@@ -837,15 +841,15 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, (lds_ptr)(wslot(stage) + WSZ * wv + 1024 * (2 * t + jj)), 16,
                                                          off_w[t] + 16 + 16 * jj + 32 * hl, sb * SB_Q4_K + 64 * h, 0, 0);
     };
-    // per step: 4 + 1 + 2*TN loads; after a step's copies of A and its header / scale
+    // per step: NA + 1 + 2*TN loads; after a step's copies of A and its header / scale
     // copy come its 2*TN nibble copies and DEPTH-2 whole steps
     // at the top of a step: this step's A and header / scale copies (the shared ones, made
     // visible to every wave by the barrier that follows); its nibble copies (issued last,
     // read only by the wave that made them) may still be in flight, and so may the DEPTH-2
     // later steps' copies.  Before the nibble words are read: the step's nibble copies, with
     // only the DEPTH-1 later steps' copies in flight.
-    constexpr int WAIT_TOP = waitcnt_vm_lgkm(2 * TN + (5 + 2 * TN) * (DEPTH - 2), 0);
-    constexpr int WAIT_NIB = waitcnt_vm_lgkm((5 + 2 * TN) * (DEPTH - 1), 15);   // (no LDS-read wait)
+    constexpr int WAIT_TOP = waitcnt_vm_lgkm(2 * TN + (NA + 1 + 2 * TN) * (DEPTH - 2), 0);
+    constexpr int WAIT_NIB = waitcnt_vm_lgkm((NA + 1 + 2 * TN) * (DEPTH - 1), 15);   // (no LDS-read wait)
 
     float16v P[TM][TN], S[TM][TN], T[TM][TN];
     const float16v zero16 = {};
@@ -874,12 +878,18 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
                 dmw[t] = h2f((uint16_t)(hdr.x >> 16));
             }
         }
-        // every A operand and nibble word of the step requested at once (one LDS latency)
-        half8 afr[8][TM];
+        // the step's A operands and nibble words requested together (one LDS latency); with
+        // 96 rows the A operands come in two halves of four K slices, to fit two waves per SIMD
+        constexpr int KH = TM == 3 ? 2 : 1, KPH = 8 / KH;
+        half8 afr[8][3];   // [KPH][TM] used
+        auto read_a = [&](int part) __attribute__((always_inline)) {
 #pragma unroll
-        for (int kk = 0; kk < 8; kk++)
+            for (int kq = 0; kq < KPH; kq++)
 #pragma unroll
-            for (int i = 0; i < TM; i++) afr[kk][i] = *(const half8 *)(aslot(stage) + (8 * i + kk) * 512 + 8 * lane);
+                for (int i = 0; i < TM; i++)
+                    afr[kq][i] = *(const half8 *)(aslot(stage) + (8 * i + KPH * part + kq) * 512 + 8 * lane);
+        };
+        read_a(0);
         u32x4 qw[TN][2];
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(WAIT_NIB);   // this wave's nibble copies for the step
@@ -893,16 +903,21 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
 #pragma unroll
         for (int t = 0; t < TN; t++) kc[t] = q4k_group_consts(h == 0 ? sm[t].sc_lo : sm[t].sc_hi, 16 * hl);
 #pragma unroll
-        for (int kk = 0; kk < 8; kk++) {
-            half8 b[TN];
+        for (int part = 0; part < KH; part++) {
+            if (part) read_a(part);
 #pragma unroll
-            for (int t = 0; t < TN; t++) b[t] = q4k_word(qw[t][kk >> 2][kk & 3], kc[t], MASK_LO, MASK_HI, MAGIC);
+            for (int kq = 0; kq < KPH; kq++) {
+                const int kk = KPH * part + kq;
+                half8 b[TN];
 #pragma unroll
-            for (int i = 0; i < TM; i++)
+                for (int t = 0; t < TN; t++) b[t] = q4k_word(qw[t][kk >> 2][kk & 3], kc[t], MASK_LO, MASK_HI, MAGIC);
 #pragma unroll
-                for (int t = 0; t < TN; t++)
-                    P[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afr[kk][i], b[t],
-                                                                     (h == 0 && kk == 0) ? zero16 : P[i][t], 0, 0, 0);
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int t = 0; t < TN; t++)
+                        P[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afr[kq][i], b[t],
+                                                                         (h == 0 && kk == 0) ? zero16 : P[i][t], 0, 0, 0);
+            }
         }
 #ifdef DFX_W_INTERLEAVE
         // interleave: every MFMA followed by a few VALU instructions (the next
@@ -917,7 +932,7 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
         if (h == 1) {
             // super-block complete: x = d_w*isum; x = fma(-dmin_w, msum, x); S = fma(d_a, x, S)
             const half_t * Abs = (const half_t *)sslot(stage);
-            const float * Ad = (const float *)(sslot(stage) + 2048);
+            const float * Ad = (const float *)(sslot(stage) + 1024 * TM);
 #pragma unroll
             for (int t = 0; t < TN; t++) {
                 const half8 bm = mins_half8(hl ? sm[t].mn_hi : sm[t].mn_lo);
@@ -1389,13 +1404,14 @@ __global__ void k_gemm_reduce(const float * __restrict__ ws, int S, int64_t MN, 
 
 // Forced tile of the Q4_K / Q6_K kernels, for tuning and tests:
 // "<TM>x<TN>[x<D>]" picks a register tile, "s" splits K when possible, "n" never
-// splits, "w" / "w1" pick the LDS-DMA Q4_K kernel (64 x 64 / 64 x 32 per wave).
+// splits, "w" / "w1" / "w3" pick the LDS-DMA Q4_K kernel (64 x 64 / 64 x 32 / 96 x 32
+// per wave).
 // Set with dfx_gemm_force_tile; DFX_Q4K_TILE / DFX_Q6K_TILE are read once, at the
 // first GEMM launch or setter call.  Parsed once, not per launch.
 struct tile_force {
     bool on = false;
     int got = 0, tm = 0, tn = 0, d = 0;
-    bool split = false, nosplit = false, w = false, w1 = false;
+    bool split = false, nosplit = false, w = false, w1 = false, w3 = false;
 };
 static std::mutex g_force_mu;
 static tile_force g_force[2];   // [0] Q4_K, [1] Q6_K
@@ -1410,6 +1426,7 @@ static tile_force parse_force(const char * f) {
     t.nosplit = strchr(f, 'n') != nullptr;
     t.w = strchr(f, 'w') != nullptr;
     t.w1 = strstr(f, "w1") != nullptr;
+    t.w3 = strstr(f, "w3") != nullptr;
     return t;
 }
 
@@ -1528,10 +1545,10 @@ static int launch_q4k(const void * w, int N, int K, const void * act, int M, con
     return DFX_OK;
 }
 
-template <int TN, int DEPTH>
+template <int TM, int TN, int DEPTH>
 static int launch_q4k_w(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                         float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st, int * defer) {
-    const int n_tiles = (N + 128 * TN - 1) / (128 * TN), m_tiles = (M + 63) / 64;
+    const int n_tiles = (N + 128 * TN - 1) / (128 * TN), m_tiles = (M + 32 * TM - 1) / (32 * TM);
     const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
     const int chunks = dot_chunks(K), passes = ws ? chunks : 1;
     const int sb = K / 256, sb_last = sb - (chunks - 1) * (DFX_DOT_CHUNK / 256);
@@ -1539,7 +1556,7 @@ static int launch_q4k_w(const void * w, int N, int K, const void * act, int M, c
         dfx_set_error("dfx_gemm q4_k: K=%d does not fit the pipeline depth %d", K, DEPTH);
         return DFX_ERR_ARG;
     }
-    hipLaunchKernelGGL((k_q4k_w<TN, DEPTH>), dim3((unsigned)(per_pass * passes)), dim3(256), 0, st, (const uint8_t *)w, N,
+    hipLaunchKernelGGL((k_q4k_w<TM, TN, DEPTH>), dim3((unsigned)(per_pass * passes)), dim3(256), 0, st, (const uint8_t *)w, N,
                        K, (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles, ws);
     DFX_CHECK_LAUNCH("dfx_gemm q4_k");
     if (ws) return reduce_or_defer(ws, chunks, M, N, bias, res, y, ldy, ymap, st, defer);
@@ -1659,11 +1676,26 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
     if (f.on && f.w) {
         // "w": 64 x 64 per wave; "w1": 64 x 32 per wave, two workgroups per CU
         float * wsw = split ? (float *)ws : nullptr;
-        if (f.w1) return launch_q4k_w<1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
-        if (sb_last % 2) return launch_q4k_w<2, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
-        return launch_q4k_w<2, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
+        if (f.w1) return launch_q4k_w<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
+        if (f.w3) return launch_q4k_w<3, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
+        if (sb_last % 2) return launch_q4k_w<2, 2, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
+        return launch_q4k_w<2, 2, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
     }
-    if (dma) return launch_q4k_w<1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, split ? (float *)ws : nullptr, st, defer);
+    // 96-row tiles (k_q4k_w<3, 1, 2>): each dequantised weight feeds three MFMAs instead of
+    // two, but a workgroup takes 1.5x longer, so they only pay when the chosen kernel's grid
+    // needs more rounds of two workgroups per CU than theirs (measured: gate|up and down at
+    // M = 142-181 of the LLaDA-8B shapes, 3-12% faster; slower wherever the default fits
+    // in one round)
+    if (!f.on && M > 128 && M <= 192) {
+        auto rounds = [](int64_t wgs) { return (wgs + 511) / 512; };
+        const int64_t t3 = (int64_t)n_col * ((M + 95) / 96);
+        const bool split3 = can_split && (chunks > 2 || t3 < 160);
+        const int64_t t_def = (int64_t)n_col * (dma ? (M + 63) / 64 : (M + 31) / 32);
+        if (rounds(t3 * (split3 ? chunks : 1)) < rounds(t_def * (split ? chunks : 1)))
+            return launch_q4k_w<3, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, split3 ? (float *)ws : nullptr, st,
+                                         defer);
+    }
+    if (dma) return launch_q4k_w<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, split ? (float *)ws : nullptr, st, defer);
     if (cands[pick].d == 4 && (sb_last % 2))
         for (int c = 0; c < n_cand; c++)
             if (cands[c].tm == cands[pick].tm && cands[c].tn == cands[pick].tn && cands[c].d == 2) { pick = c; break; }

@@ -63,7 +63,10 @@ int main() {
     assert r.returncode == 0 and r.stdout.strip() == "1"
 
 
-REF_CALLERS = ("tools/main-cli.cpp", "tools/main-bench.cpp", "tools/dump-logits.cpp", "tests/test-forward.cpp")
+# tools/ar-cli.cpp is the reference's caller of the autoregressive API (ar_generate,
+# ar_speculative_generate); it includes <omp.h>, hence -fopenmp
+REF_CALLERS = ("tools/main-cli.cpp", "tools/main-bench.cpp", "tools/dump-logits.cpp", "tests/test-forward.cpp",
+               "tools/ar-cli.cpp")
 
 
 @pytest.mark.skipif(not os.path.isdir("/root/reference/tools"), reason="reference sources not present on this host")
@@ -73,7 +76,7 @@ def test_reference_callers_link_unchanged(tmp_path, rel):
     include/diffuse.h and link against libdiffuse (drop-in check; nothing is run)."""
     exe = tmp_path / os.path.basename(rel).replace(".cpp", "")
     lib = os.path.dirname(dfx.LIB_PATH)
-    subprocess.check_call(["g++", "-std=c++17", "-O0", "-I", os.path.join(REPO, "include"),
+    subprocess.check_call(["g++", "-std=c++17", "-O0", "-fopenmp", "-I", os.path.join(REPO, "include"),
                            os.path.join("/root/reference", rel), "-o", str(exe), "-L", lib, "-ldiffuse",
                            f"-Wl,-rpath,{lib}", "-Wl,--allow-shlib-undefined"])
     assert exe.exists()

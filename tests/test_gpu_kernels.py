@@ -164,7 +164,7 @@ def test_gemm_quantized_bit_exact(gpu, typ, N, K, M):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
 
 
-@pytest.mark.parametrize("tile", ["2x2x2", "4x1x2", "2x1x2", "1x2x2", "1x1x4", "1x1x2", "2x1x4", "2x2x4", "w", "w1"])
+@pytest.mark.parametrize("tile", ["2x2x2", "4x1x2", "2x1x2", "1x2x2", "1x1x4", "1x1x2", "2x1x4", "2x2x4", "w", "w1", "w3"])
 @pytest.mark.parametrize("N,K,M", [(1000, 2048, 77), (4096, 4096, 288)])
 def test_gemm_q4k_every_tile_bit_exact(gpu, tile, N, K, M):
     """Every register tile of the Q4_K kernel (forced with dfx_gemm_force_tile), with ragged
@@ -177,7 +177,7 @@ def test_gemm_q4k_every_tile_bit_exact(gpu, tile, N, K, M):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
 
 
-@pytest.mark.parametrize("tile", ["1x1x4s", "2x1x2s", "1x2x2s", "2x1x4s", "ws", "w1s"])
+@pytest.mark.parametrize("tile", ["1x1x4s", "2x1x2s", "1x2x2s", "2x1x4s", "ws", "w1s", "w3s"])
 @pytest.mark.parametrize("N,K,M", [(512, 12288, 70), (1000, 3584, 33), (640, 2304, 40), (4096, 4096, 256)])
 def test_gemm_q4k_split_k_bit_exact(gpu, tile, N, K, M):
     """Split K (one workgroup per 2048-element chunk, chunk sums added in order by the
