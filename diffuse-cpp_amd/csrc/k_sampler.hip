@@ -447,3 +447,175 @@ extern "C" int dfx_layer_impact(const float * x, const float * x_in, int64_t M, 
     DFX_CHECK_LAUNCH("dfx_layer_impact");
     return DFX_OK;
 }
+
+// ---------------------------------------------------------------------------
+// Device-resident denoising step bookkeeping
+// ---------------------------------------------------------------------------
+// The sequence state lives on the device: seq[N] (token ids), prev[N] (seq as it was
+// right after the last forward, src/diffuse-sampler.cpp:154, 171, 194), masked[N] (0 / 1)
+// and lastc[N] (step at which a change was last seen, -1 never).
+
+// Exclusive prefix of a per-thread flag over a workgroup of SCAN_T threads, and the total.
+#define SCAN_T 1024
+__device__ __forceinline__ int block_scan(bool flag, int * red, int & total) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const unsigned long long b = __ballot(flag);
+    const int in_wave = __popcll(b & ((1ull << lane) - 1ull));
+    if (lane == 0) red[wv] = __popcll(b);
+    __syncthreads();
+    int before = 0;
+    total = 0;
+    for (int w = 0; w < SCAN_T / 64; w++) {
+        const int c = red[w];
+        if (w < wv) before += c;
+        total += c;
+    }
+    __syncthreads();
+    return before + in_wave;
+}
+
+// compute_active_set (src/diffuse-cache.h:79-116) and the row lists of one step.
+//   active: full step, or changed (seq != prev, which also records lastc = step), still
+//   masked, or changed within `keep` steps; a cached step whose active set is empty or
+//   everything becomes full.
+//   pass rows a = 0..M-1 in position order: tok[a] = seq[act[a]], act[a] = position;
+//   head rows: pass rows whose logits the sampler reads (masked positions, or their left
+//   neighbours when shift; every pass row when head_all), hrows[k] = pass row,
+//   hmap[k] = position;
+//   sampler rows: every masked position i in order, srows[k] = i (or max(i-1, 0) when
+//   shift), spos[k] = i.
+// counts = {M, n_head, n_cand, full}.  One workgroup.
+__global__ void __launch_bounds__(SCAN_T) k_step_prepare(int N, int step, int full, int keep, int shift, int head_all,
+                                                         const int32_t * __restrict__ seq,
+                                                         const int32_t * __restrict__ prev,
+                                                         const int32_t * __restrict__ masked, int32_t * lastc,
+                                                         int32_t * tok, int32_t * act, int32_t * hrows, int32_t * hmap,
+                                                         int32_t * srows, int32_t * spos, int32_t * counts) {
+    __shared__ int red[SCAN_T / 64];
+    const int tid = threadIdx.x;
+    int M = 0;
+    if (!full) {
+        for (int t0 = 0; t0 < N; t0 += SCAN_T) {
+            const int i = t0 + tid;
+            bool on = false;
+            if (i < N) {
+                const bool changed = seq[i] != prev[i];
+                int lc = lastc[i];
+                if (changed) {
+                    lc = step;
+                    lastc[i] = step;
+                }
+                const bool recent = keep > 0 && lc >= 0 && step - lc <= keep;
+                on = changed || masked[i] != 0 || recent;
+            }
+            int tot;
+            const int idx = block_scan(on, red, tot);
+            if (on) act[M + idx] = i;
+            M += tot;
+        }
+        if (M >= N || M == 0) full = 1;
+    }
+    if (full) {
+        for (int i = tid; i < N; i += SCAN_T) act[i] = i;
+        M = N;
+    }
+    __syncthreads();
+    // pass tokens and head rows (act is in position order)
+    int nh = 0;
+    for (int a0 = 0; a0 < M; a0 += SCAN_T) {
+        const int a = a0 + tid;
+        bool need = false;
+        int p = 0;
+        if (a < M) {
+            p = act[a];
+            tok[a] = seq[p];
+            need = head_all || (shift ? ((p + 1 < N && masked[p + 1] != 0) || (p == 0 && masked[0] != 0))
+                                      : masked[p] != 0);
+        }
+        int tot;
+        const int idx = block_scan(need, red, tot);
+        if (need) {
+            hrows[nh + idx] = a;
+            hmap[nh + idx] = p;
+        }
+        nh += tot;
+    }
+    // sampler rows
+    int nc = 0;
+    for (int t0 = 0; t0 < N; t0 += SCAN_T) {
+        const int i = t0 + tid;
+        const bool m = i < N && masked[i] != 0;
+        int tot;
+        const int idx = block_scan(m, red, tot);
+        if (m) {
+            srows[nc + idx] = shift ? max(i - 1, 0) : i;
+            spos[nc + idx] = i;
+        }
+        nc += tot;
+    }
+    if (tid == 0) {
+        counts[0] = M;
+        counts[1] = nh;
+        counts[2] = nc;
+        counts[3] = full;
+    }
+}
+
+// update_seq then unmask (src/diffuse-sampler.cpp:154, 316-323): prev = seq (when the cache
+// is on), then the first n_unmask selected candidates write their token and clear their
+// mask; ustep[pos] = step when given; hist[step] = n_unmask, or -1 if the selection named
+// a candidate or position out of range (nothing is written for it).  One workgroup.
+__global__ void __launch_bounds__(SCAN_T) k_step_unmask(int N, int use_cache, int step, int32_t * seq,
+                                                        int32_t * prev, int32_t * masked,
+                                                        const dfx_candidate * __restrict__ cand,
+                                                        const int32_t * __restrict__ order,
+                                                        const int32_t * __restrict__ n_unmask, int n_cand,
+                                                        int32_t * ustep, int32_t * hist) {
+    __shared__ int bad;
+    const int tid = threadIdx.x;
+    if (tid == 0) bad = 0;
+    if (use_cache)
+        for (int i = tid; i < N; i += SCAN_T) prev[i] = seq[i];
+    __syncthreads();
+    const int n = min(*n_unmask, n_cand);
+    for (int j = tid; j < n; j += SCAN_T) {
+        const int o = order[j];
+        const dfx_candidate c = cand[o >= 0 && o < n_cand ? o : 0];
+        if (o < 0 || o >= n_cand || c.pos < 0 || c.pos >= N) {   // never written out of range
+            bad = 1;
+            continue;
+        }
+        seq[c.pos] = c.token;
+        masked[c.pos] = 0;
+        if (ustep) ustep[c.pos] = step;
+    }
+    __syncthreads();
+    if (tid == 0) hist[step] = bad ? -1 : n;   // -1: the selection named a bad candidate
+}
+
+extern "C" int dfx_step_prepare(int N, int step, int full, int keep, int shift, int head_all, const int32_t * seq,
+                                const int32_t * prev, const int32_t * masked, int32_t * lastc, int32_t * tok,
+                                int32_t * act, int32_t * hrows, int32_t * hmap, int32_t * srows, int32_t * spos,
+                                int32_t * counts, void * stream) {
+    if (N <= 0 || !seq || !prev || !masked || !lastc || !tok || !act || !hrows || !hmap || !srows || !spos || !counts) {
+        dfx_set_error("dfx_step_prepare: bad arguments (N=%d)", N);
+        return DFX_ERR_ARG;
+    }
+    hipLaunchKernelGGL(k_step_prepare, dim3(1), dim3(SCAN_T), 0, (hipStream_t)stream, N, step, full, keep, shift,
+                       head_all, seq, prev, masked, lastc, tok, act, hrows, hmap, srows, spos, counts);
+    DFX_CHECK_LAUNCH("dfx_step_prepare");
+    return DFX_OK;
+}
+
+extern "C" int dfx_step_unmask(int N, int use_cache, int step, int32_t * seq, int32_t * prev, int32_t * masked,
+                               const dfx_candidate * cand, const int32_t * order, const int32_t * n_unmask, int n_cand,
+                               int32_t * ustep, int32_t * hist, void * stream) {
+    if (N <= 0 || n_cand < 0 || !seq || !prev || !masked || !n_unmask || !hist || (n_cand && (!cand || !order))) {
+        dfx_set_error("dfx_step_unmask: bad arguments (N=%d, n_cand=%d)", N, n_cand);
+        return DFX_ERR_ARG;
+    }
+    hipLaunchKernelGGL(k_step_unmask, dim3(1), dim3(SCAN_T), 0, (hipStream_t)stream, N, use_cache, step, seq, prev,
+                       masked, cand, order, n_unmask, n_cand, ustep, hist);
+    DFX_CHECK_LAUNCH("dfx_step_unmask");
+    return DFX_OK;
+}

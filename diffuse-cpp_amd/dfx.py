@@ -150,6 +150,9 @@ def _declare(L):
         "dfx_generate": (I32, [P, P, I32, I32, C.POINTER(SamplerParams), P, C.POINTER(GenStats)]),
         "dfx_generate_trace": (I32, [P, P, I32, I32, C.POINTER(SamplerParams), P, C.POINTER(GenStats), P]),
         "dfx_attention_causal": (I32, [P, P, P, I64, I64, I64, I32, I32, I32, I64, I32, P, P]),
+        "dfx_context_set_device_loop": (I32, [P, I32]),
+        "dfx_step_prepare": (I32, [I32, I32, I32, I32, I32, I32, P, P, P, P, P, P, P, P, P, P, P, P]),
+        "dfx_step_unmask": (I32, [I32, I32, I32, P, P, P, P, P, P, I32, P, P, P]),
         "dfx_ar_greedy": (I32, [P, I64, P, I32, F, P, P]),
         "dfx_layer_impact": (I32, [P, P, I64, I64, P, P]),
         "dfx_ar_forward": (I32, [P, P, I32, I32, I32, P]),
@@ -434,6 +437,10 @@ class Context:
         check(lib().dfx_ar_generate(self.h, _ptr(prompt), len(prompt), max_tokens, C.byref(params), _ptr(out),
                                     C.byref(n), C.byref(st), fn, None), "dfx_ar_generate")
         return out[:n.value].copy()
+
+    def set_device_loop(self, enable=True):
+        """Step bookkeeping of greedy dfx_generate on the device (default) or on the host."""
+        check(lib().dfx_context_set_device_loop(self.h, 1 if enable else 0), "dfx_context_set_device_loop")
 
     def set_attention(self, mode):
         """ATTN_EXACT (the default) or ATTN_SPLIT_BF16 for this context's forward passes."""

@@ -93,6 +93,12 @@ extern "C" int dfx_context_set_attention(dfx_context * c, int mode) {
     return DFX_OK;
 }
 
+extern "C" int dfx_context_set_device_loop(dfx_context * c, int enable) {
+    if (!c) return DFX_ERR_ARG;
+    c->device_loop = enable != 0;
+    return DFX_OK;
+}
+
 extern "C" int dfx_context_profile(dfx_context * c, int enable) {
     if (!c) return DFX_ERR_ARG;
     return engine_profile(c, enable != 0);

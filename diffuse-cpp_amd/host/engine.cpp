@@ -46,12 +46,16 @@ struct dims {
 
 void free_buffers(diffuse_context * c) {
     void * bufs[] = {c->x, c->act, c->qkv, c->qr, c->att, c->gu, c->logits, c->kc, c->vc, c->rope_tab,
-                     c->d_ints, c->ws, c->d_stats, c->d_out, c->x_prev, c->d_imp, c->d_ar};
+                     c->d_ints, c->ws, c->d_stats, c->d_out, c->x_prev, c->d_imp, c->d_ar, c->d_state,
+                     c->d_counts, c->d_hist};
     for (void * p : bufs)
         if (p) (void)hipFree(p);
     if (c->h_pin) (void)hipHostFree(c->h_pin);
     if (c->h_out) (void)hipHostFree(c->h_out);
     if (c->h_row) (void)hipHostFree(c->h_row);
+    if (c->h_hist) (void)hipHostFree(c->h_hist);
+    c->d_state = c->d_counts = c->d_hist = c->h_hist = nullptr;
+    c->steps_cap = 0;
     c->x_prev = nullptr;
     c->d_imp = nullptr;
     c->d_ar = nullptr;
@@ -119,6 +123,7 @@ int ensure_capacity(diffuse_context * c, int N) {
                            dfx_gemm_ws_bytes(n, D.d, D.F));
     TRY(A(&c->ws, c->ws_bytes));
     TRY(A((void **)&c->d_stats, n * sizeof(dfx_row_stat)));
+    TRY(A((void **)&c->d_state, 5 * n * 4));
     c->out_bytes = n * sizeof(dfx_candidate) + n * 4 + 16;
     TRY(A(&c->d_out, c->out_bytes));
     c->d_cand = (dfx_candidate *)c->d_out;
@@ -217,21 +222,19 @@ int run_group(diffuse_context * c, const proj_group & g, const float * norm, int
     return DFX_OK;
 }
 
-// Enqueue one forward over the M rows in d_tok/d_pos, attending over keys
-// 0..n_keys-1 of the cache; logits for the n_head rows d_hrows go to logits[d_hmap].
-// o: the autoregressive graph's options (causal mask, skipped layers, impact profile).
-int forward_pass(diffuse_context * c, int M, int n_keys, int n_head, const pass_opts & o = pass_opts()) {
+// Enqueue the layers of one forward over the M rows in d_tok/d_pos, attending over keys
+// 0..n_keys-1 of the cache.  o: the autoregressive graph's options (causal mask, skipped
+// layers, impact profile).  pending: split-K partial sums of the last down projection still
+// to be added to x (by the head's RMSNorm).
+int forward_layers(diffuse_context * c, int M, int n_keys, const pass_opts & o, int & pending) {
     const diffuse_model & m = *c->model;
     const dims D(m.hparams);
-    const float eps = m.hparams.rms_norm_eps;
     const int32_t * tok = o.tok ? o.tok : c->d_tok;
     const int32_t * pos = o.pos ? o.pos : c->d_pos;
-    const int32_t * hrows = o.hrows ? o.hrows : c->d_hrows;
-    const int32_t * hmap = o.hmap ? o.hmap : c->d_hmap;
     TRY(dfx_embed(m.tok_embd.type, m.tok_embd.data, D.d, tok, M, c->x, c->stream));
     // split-K partial sums of the last O / down projection, still to be added to x (by
     // the RMSNorm that reads x next); profiling needs x whole after every layer
-    int pending = 0;
+    pending = 0;
     int * defer = o.impact_rows ? nullptr : &pending;
     for (int64_t il = 0; il < D.L; il++) {
         if (o.skip && o.skip[il]) continue;   // src/ar-graph.cpp:98-102
@@ -257,17 +260,29 @@ int forward_pass(diffuse_context * c, int M, int n_keys, int n_head, const pass_
         TRY(gemm(c, L.down, D.d, D.F, M, nullptr, c->x, c->x, D.d, nullptr, true, defer));
         if (o.impact_rows) TRY(dfx_layer_impact(c->x, c->x_prev, M, D.d, o.impact_rows + il * M, c->stream));
     }
-    if (n_head > 0) {
-        // rows without logits never need the last layer's x
-        if (pending)
-            TRY(dfx_rmsnorm_convert_add(m.output.type, c->x, hrows, (const float *)c->ws, pending, M,
-                                        m.output_norm, n_head, D.d, eps, c->act, c->stream));
-        else
-            TRY(dfx_rmsnorm_convert_ex(m.output.type, c->x, hrows, m.output_norm, n_head, D.d, eps, c->act,
-                                       c->stream));
-        TRY(gemm(c, m.output, D.V, D.d, n_head, nullptr, nullptr, c->logits, D.V, hmap, false));
-    }
     return DFX_OK;
+}
+
+// Final norm + vocab head for the n_head pass rows hrows[] (of M), logits to rows hmap[].
+int forward_head(diffuse_context * c, int M, int n_head, const int32_t * hrows, const int32_t * hmap, int pending) {
+    if (n_head <= 0) return DFX_OK;
+    const diffuse_model & m = *c->model;
+    const dims D(m.hparams);
+    const float eps = m.hparams.rms_norm_eps;
+    // rows without logits never need the last layer's x
+    if (pending)
+        TRY(dfx_rmsnorm_convert_add(m.output.type, c->x, hrows, (const float *)c->ws, pending, M, m.output_norm,
+                                    n_head, D.d, eps, c->act, c->stream));
+    else
+        TRY(dfx_rmsnorm_convert_ex(m.output.type, c->x, hrows, m.output_norm, n_head, D.d, eps, c->act, c->stream));
+    return gemm(c, m.output, D.V, D.d, n_head, nullptr, nullptr, c->logits, D.V, hmap, false);
+}
+
+// One whole forward: layers, then logits for the n_head rows d_hrows go to logits[d_hmap].
+int forward_pass(diffuse_context * c, int M, int n_keys, int n_head, const pass_opts & o = pass_opts()) {
+    int pending = 0;
+    TRY(forward_layers(c, M, n_keys, o, pending));
+    return forward_head(c, M, n_head, o.hrows ? o.hrows : c->d_hrows, o.hmap ? o.hmap : c->d_hmap, pending);
 }
 
 int upload_i32(diffuse_context * c, int32_t * dst, const int32_t * src, int n, int slot) {
@@ -308,6 +323,184 @@ const char * remask_name(int r) {
                                                                                                : "random";
 }
 
+
+// Per-step device records and events of the device-resident loop, for up to n steps.
+int ensure_steps(diffuse_context * c, int n) {
+    if (n > c->steps_cap) {
+        if (c->d_counts) (void)hipFree(c->d_counts);
+        if (c->d_hist) (void)hipFree(c->d_hist);
+        if (c->h_hist) (void)hipHostFree(c->h_hist);
+        c->d_counts = c->d_hist = c->h_hist = nullptr;
+        c->steps_cap = 0;
+        TRY(hip_ok(hipMalloc((void **)&c->d_counts, (size_t)n * 4 * 4), "hipMalloc"));
+        TRY(hip_ok(hipMalloc((void **)&c->d_hist, (size_t)n * 4), "hipMalloc"));
+        TRY(hip_ok(hipHostMalloc((void **)&c->h_hist, (size_t)n * 4, hipHostMallocDefault), "hipHostMalloc"));
+        c->steps_cap = n;
+    }
+    for (auto * v : {&c->ev_unmask, &c->ev_fwd0, &c->ev_fwd1})
+        while ((int)v->size() < n) {
+            hipEvent_t e = nullptr;
+            TRY(hip_ok(hipEventCreate(&e), "hipEventCreate"));
+            v->push_back(e);
+        }
+    return DFX_OK;
+}
+
+// The denoising loop with its bookkeeping on the device (temperature 0, every remasking
+// policy but RANDOM): seq / prev / masked / lastc stay in HBM; each step is
+//   k_step_prepare (active set, pass / head / sampler rows) -> layers -> head -> row
+//   statistics -> candidates -> selection -> k_step_unmask (update_seq + unmask)
+// and no step waits for its own selection.  The host needs a step's row count before
+// enqueueing its layers and its masked count before the head and sampler; both follow from
+// unmask counts of earlier steps (for a cached step: the positions masked when the previous
+// step began, plus, with keep_active, those unmasked in the steps before that whose change
+// was seen within the window), so the host enqueues step s's layers once step s-2 has
+// ended and its head once step s-1 has: the GPU always has the next step's layers queued.
+// A step enqueued speculatively after a step that unmasked everything left is dropped
+// after its layers.  The prepare kernel's own counts are checked against the host's at
+// the end.
+int generate_device(diffuse_context * c, const int32_t * prompt, int n_prompt, int n_generate,
+                    const dfx_sampler_params & p, int32_t * out, dfx_gen_stats * stats,
+                    const diffuse_step_callback * callback, int32_t * unmask_step) {
+    using clk = std::chrono::steady_clock;
+    const diffuse_model & md = *c->model;
+    const int V = (int)md.hparams.n_vocab;
+    const int mask_id = (int)md.hparams.mask_token_id;
+    const bool shift = md.is_dream;
+    const int N = n_prompt + n_generate;
+    const int S = std::max(p.n_steps, 1);
+    const bool use_cache = p.use_cache != 0;
+    const int keep = std::max(p.cache_keep_active, 0);
+    TRY(ensure_steps(c, S));
+    int32_t * d_seq = c->d_state, * d_prev = d_seq + c->cap, * d_msk = d_prev + c->cap;
+    int32_t * d_lastc = d_msk + c->cap, * d_ustep = d_lastc + c->cap;
+    {
+        int32_t * h = c->h_pin;   // 8 * cap int32
+        for (int i = 0; i < N; i++) {
+            h[i] = i < n_prompt ? prompt[i] : mask_id;
+            h[c->cap + i] = -1;
+            h[2 * c->cap + i] = i < n_prompt ? 0 : 1;
+            h[3 * c->cap + i] = -1;
+            h[4 * c->cap + i] = -1;
+        }
+        TRY(hip_ok(hipMemcpyAsync(d_seq, h, (size_t)5 * c->cap * 4, hipMemcpyHostToDevice, c->stream), "H2D"));
+    }
+    std::vector<int> rows(S, 0), nun(S, 0), full_v(S, 0), det(S, 0), masked_start(S + 1, 0);
+    masked_start[0] = n_generate;
+    bool cache_init = false;
+    int actual_steps = 0;
+    const auto gen_start = clk::now();
+    auto step_unmasked = [&](int t) -> int {   // unmask count of an enqueued step (waits for it)
+        TRY(hip_ok(hipEventSynchronize(c->ev_unmask[t]), "step"));
+        const int n = c->h_hist[t];
+        if (n < 0) {
+            dfx_set_error("diffuse_generate: the selection of step %d named a candidate out of range", t);
+            return DFX_ERR_HIP;
+        }
+        nun[t] = n;
+        masked_start[t + 1] = masked_start[t] - n;
+        return DFX_OK;
+    };
+    for (int s = 0; s < p.n_steps; s++) {
+        if (s >= 2) TRY(step_unmasked(s - 2));
+        // ---- row count of the step (compute_active_set, src/diffuse-cache.h:79-116, by counts)
+        const bool force_full = !use_cache || !cache_init || (p.cache_refresh > 0 && s > 0 && s % p.cache_refresh == 0);
+        int M = N;
+        bool full = force_full;
+        if (!force_full) {
+            // positions masked when step s-1 began (still masked, or unmasked by step s-1)
+            M = masked_start[s - 1];
+            // plus those unmasked by step t <= s-2 whose change step t+1 saw, within the window
+            if (keep > 0)
+                for (int t = std::max(0, s - keep - 1); t <= s - 2; t++)
+                    if (det[t + 1]) M += nun[t];
+            if (M >= N || M == 0) full = true;
+        }
+        if (full) M = N;
+        det[s] = !force_full;
+        rows[s] = M;
+        full_v[s] = full;
+        TRY(dfx_step_prepare(N, s, force_full ? 1 : 0, keep, shift ? 1 : 0, shift ? 1 : 0, d_seq, d_prev, d_msk,
+                             d_lastc, c->d_tok, c->d_pos, c->d_hrows, c->d_hmap, c->d_srows, c->d_spos,
+                             c->d_counts + 4 * s, c->stream));
+        TRY(hip_ok(hipEventRecord(c->ev_fwd0[s], c->stream), "event"));
+        int pending = 0;
+        TRY(forward_layers(c, M, N, pass_opts(), pending));
+        TRY(hip_ok(hipEventRecord(c->ev_fwd1[s], c->stream), "event"));
+        if (use_cache) cache_init = true;
+        // ---- the head and the sampler need the masked count when step s begins
+        if (s >= 1) TRY(step_unmasked(s - 1));
+        const int n_masked = masked_start[s];
+        if (n_masked <= 0) break;   // the previous step unmasked everything: this one's layers are dropped
+        actual_steps = s + 1;
+        const int n_head = shift ? M : n_masked;
+        TRY(forward_head(c, M, n_head, c->d_hrows, c->d_hmap, pending));
+        const int n_sched = tokens_to_unmask(s, p.n_steps, n_masked, p.schedule);
+        TRY(dfx_row_stats(c->logits, V, c->d_srows, n_masked, V, c->d_stats, c->stream));
+        TRY(dfx_make_candidates(c->d_stats, c->d_spos, n_masked, p.remasking == 4 ? 1 : 0, c->d_cand, c->stream));
+        TRY(dfx_select(c->d_cand, n_masked, p.remasking, p.entropy_threshold, n_sched, c->d_order, c->d_nun,
+                       c->stream));
+        TRY(dfx_step_unmask(N, use_cache ? 1 : 0, s, d_seq, d_prev, d_msk, c->d_cand, c->d_order, c->d_nun, n_masked,
+                            unmask_step ? d_ustep : nullptr, c->d_hist, c->stream));
+        TRY(hip_ok(hipMemcpyAsync(c->h_hist + s, c->d_hist + s, 4, hipMemcpyDeviceToHost, c->stream), "D2H"));
+        TRY(hip_ok(hipEventRecord(c->ev_unmask[s], c->stream), "event"));
+        if (callback && *callback) {
+            TRY(step_unmasked(s));
+            std::vector<int32_t> seq(N);
+            TRY(hip_ok(hipMemcpy(seq.data(), d_seq, (size_t)N * 4, hipMemcpyDeviceToHost), "D2H"));
+            (*callback)(s + 1, p.n_steps, seq);
+        }
+    }
+    TRY(hip_ok(hipStreamSynchronize(c->stream), "generate"));
+    for (int t = 0; t < actual_steps; t++) TRY(step_unmasked(t));
+    const double gen_ms = std::chrono::duration<double, std::milli>(clk::now() - gen_start).count();
+    // the device's own row counts must be the ones the host launched with
+    std::vector<int32_t> counts((size_t)4 * S);
+    TRY(hip_ok(hipMemcpy(counts.data(), c->d_counts, (size_t)4 * S * 4, hipMemcpyDeviceToHost), "D2H"));
+    for (int t = 0; t < actual_steps; t++)
+        if (counts[4 * t] != rows[t] || counts[4 * t + 3] != full_v[t] ||
+            counts[4 * t + 2] != masked_start[t] || (!shift && counts[4 * t + 1] != masked_start[t])) {
+            dfx_set_error("diffuse_generate: step %d ran %d rows (full %d) but the active set has %d (full %d)", t,
+                          rows[t], full_v[t], counts[4 * t], counts[4 * t + 3]);
+            return DFX_ERR_HIP;
+        }
+    std::vector<int32_t> seq(N);
+    TRY(hip_ok(hipMemcpy(seq.data(), d_seq, (size_t)N * 4, hipMemcpyDeviceToHost), "D2H"));
+    memcpy(out, seq.data() + n_prompt, (size_t)n_generate * 4);
+    if (unmask_step) {
+        std::vector<int32_t> us(N);
+        TRY(hip_ok(hipMemcpy(us.data(), d_ustep, (size_t)N * 4, hipMemcpyDeviceToHost), "D2H"));
+        memcpy(unmask_step, us.data() + n_prompt, (size_t)n_generate * 4);
+    }
+    double total_fwd = 0;
+    for (int t = 0; t < actual_steps; t++) {
+        float ms = 0.0f;
+        TRY(hip_ok(hipEventElapsedTime(&ms, c->ev_fwd0[t], c->ev_fwd1[t]), "event"));
+        total_fwd += ms;
+        DIFFUSE_LOG("  step %d/%d: unmasked %d tokens, %d remaining (fwd=%.1fms, active=%d/%d%s)", t + 1, p.n_steps,
+                    nun[t], masked_start[t + 1], ms, rows[t], N,
+                    !full_v[t] ? " CACHED" : (det[t] == 0 && t > 0 && use_cache) ? " REFRESH" : "");
+        if (stats && t < 256) {
+            stats->rows_per_step[t] = rows[t];
+            stats->unmasked_per_step[t] = nun[t];
+            stats->step_ms[t] = ms;
+        }
+    }
+    const int as = std::max(actual_steps, 1);
+    DIFFUSE_LOG("=== TIMING BREAKDOWN (%d steps, cache=%s, device loop) ===", actual_steps, use_cache ? "ON" : "OFF");
+    DIFFUSE_LOG("  forward:   %8.1f ms  (%5.1f%%)  avg=%.1f ms/step", total_fwd, 100.0 * total_fwd / gen_ms,
+                total_fwd / as);
+    DIFFUSE_LOG("  TOTAL:     %8.1f ms  (%.2f tok/s)", gen_ms, 1000.0 * n_generate / gen_ms);
+    if (stats) {
+        stats->actual_steps = actual_steps;
+        stats->total_ms = gen_ms;
+        stats->forward_ms = total_fwd;
+        stats->sample_ms = gen_ms - total_fwd;
+    }
+    prof_collect(c);
+    return DFX_OK;
+}
+
 }  // namespace
 
 int engine_context_new(const diffuse_model * m, int n_ctx, int n_threads, diffuse_context ** out) {
@@ -337,6 +530,8 @@ void engine_context_free(diffuse_context * c) {
     if (c->ev1) (void)hipEventDestroy(c->ev1);
     if (c->ev2) (void)hipEventDestroy(c->ev2);
     for (hipEvent_t e : c->prof_pool) (void)hipEventDestroy(e);
+    for (auto * v : {&c->ev_unmask, &c->ev_fwd0, &c->ev_fwd1})
+        for (hipEvent_t e : *v) (void)hipEventDestroy(e);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -475,6 +670,9 @@ int engine_generate(diffuse_context * c, const int32_t * prompt, int n_prompt, i
     DIFFUSE_LOG("diffusion: %d steps, %d tokens to generate, scheduler=%s, cache=%s, refresh=%d, keep_active=%d",
                 p.n_steps, n_generate, remask_name(p.remasking), use_cache ? "ON" : "OFF", p.cache_refresh,
                 p.cache_keep_active);
+
+    if (c->device_loop && p.temperature <= 0.0f && p.remasking != 1 && n_generate > 0)
+        return generate_device(c, prompt, n_prompt, n_generate, p, out, stats, callback, unmask_step);
 
     double total_fwd = 0, total_sample = 0, total_sort = 0, total_unmask = 0;
     int actual_steps = 0;

@@ -108,6 +108,18 @@ struct diffuse_context {
     int          attn_mode = DFX_ATTN_EXACT;   // dfx_attention_ex mode of the forward passes
     int          kv_valid = 0;       // positions 0..kv_valid-1 of the cache hold a full forward's K/V
 
+    // Device-resident denoising loop (temperature 0, every policy but RANDOM): the sequence
+    // state lives in d_state [5][cap] = seq | prev | masked | lastc | ustep; per step, the
+    // prepare kernel's counts d_counts [steps][4] and the unmask count d_hist [steps],
+    // copied to the pinned h_hist as each step ends (event ev_unmask[step]).
+    bool         device_loop = true;
+    int32_t *    d_state = nullptr;
+    int32_t *    d_counts = nullptr;
+    int32_t *    d_hist = nullptr;
+    int32_t *    h_hist = nullptr;
+    int          steps_cap = 0;
+    std::vector<hipEvent_t> ev_unmask, ev_fwd0, ev_fwd1;
+
     // Autoregressive state (src/ar-cache.h): positions 0..ar_past-1 of kc / vc hold the keys
     // and values of the tokens passed so far (layers in ar_skip keep stale rows).
     int          ar_past = 0;

@@ -209,6 +209,28 @@ int dfx_make_candidates(const dfx_row_stat * stats, const int32_t * pos, int n, 
 int dfx_select(const dfx_candidate * cand, int n, int remasking, float tau, int n_sched,
                int32_t * order, int32_t * n_unmask, void * stream);
 
+/* Device-resident step bookkeeping of the denoising loop.  The sequence state is device
+ * int32 arrays of N: seq (ids), prev (seq right after the last forward), masked (0/1),
+ * lastc (step of the last change seen, -1 never).
+ * dfx_step_prepare is compute_active_set (src/diffuse-cache.h:79-116) plus the row lists of
+ * the step (src/diffuse-sampler.cpp:222-240): with full = 0 a position is active when it
+ * changed (seq != prev; lastc = step), is masked, or changed within `keep` steps, and an
+ * empty or complete active set makes the step full.  Writes, in position order, the pass
+ * rows tok[a] = seq[act[a]], act[a] = position; the head rows (pass rows that are masked
+ * positions, or their left neighbours when shift, or every pass row when head_all) as
+ * hrows[k] = pass row, hmap[k] = position; the sampler rows srows[k] = masked position i
+ * (max(i - 1, 0) when shift), spos[k] = i; counts = {M, n_head, n_cand, full}.
+ * dfx_step_unmask is update_seq + unmask (src/diffuse-sampler.cpp:154, 316-323): prev = seq
+ * when use_cache, then the first min(*n_unmask, n_cand) candidates cand[order[j]] write
+ * their token into seq and clear masked (ustep[pos] = step when ustep != NULL);
+ * hist[step] = the count, or -1 if the order named a candidate out of range. */
+int dfx_step_prepare(int N, int step, int full, int keep, int shift, int head_all, const int32_t * seq,
+                     const int32_t * prev, const int32_t * masked, int32_t * lastc, int32_t * tok, int32_t * act,
+                     int32_t * hrows, int32_t * hmap, int32_t * srows, int32_t * spos, int32_t * counts, void * stream);
+int dfx_step_unmask(int N, int use_cache, int step, int32_t * seq, int32_t * prev, int32_t * masked,
+                    const dfx_candidate * cand, const int32_t * order, const int32_t * n_unmask, int n_cand,
+                    int32_t * ustep, int32_t * hist, void * stream);
+
 /* Greedy sample_token of the autoregressive sampler (src/ar-sampler.cpp:83-117) on one
  * device logits row, which it modifies: the repetition penalty over the recent tokens
  * (x/p for x > 0, else x*p, once per occurrence; none unless repeat_penalty > 1), then
@@ -307,6 +329,12 @@ int  dfx_generate(dfx_context * c, const int32_t * prompt, int n_prompt, int n_g
 /* Attention arithmetic of the context's forward passes (DFX_ATTN_EXACT, the default, or
  * DFX_ATTN_SPLIT_BF16; see dfx_attention_ex).  Build-defined; no counterpart in the reference. */
 int  dfx_context_set_attention(dfx_context * c, int mode);
+/* Loop of the context's dfx_generate calls at temperature 0 with a policy other than RANDOM:
+ * 1 (the default) keeps the sequence state and the step bookkeeping on the device
+ * (dfx_step_prepare / dfx_step_unmask; no step waits for its own selection), 0 runs that
+ * bookkeeping on the host with one wait per step.  Both give the same tokens.
+ * Build-defined; no counterpart in the reference. */
+int  dfx_context_set_device_loop(dfx_context * c, int enable);
 int  dfx_context_profile(dfx_context * c, int enable);
 int  dfx_context_profile_read(dfx_context * c, int wtype, int64_t * launches, double * ms, double * flops,
                               double * bytes);

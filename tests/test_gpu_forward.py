@@ -181,6 +181,39 @@ def test_generate_matches_oracle_loop(gpu, request, arch, scheme, remasking, use
     model.close()
 
 
+@pytest.mark.parametrize("arch,scheme,remasking,use_cache,B,sched,T,refresh,keep",
+                         [c for c in GEN_CASES if c[6] <= 0.0 and c[2] != dfx.RANDOM] +
+                         [("llada", "q4_k_m", dfx.ENTROPY_EXIT, True, 64, dfx.SCHED_COSINE, 0.0, 0, 0),
+                          ("dream", "q4_k_m", dfx.ENTROPY_EXIT, True, 48, dfx.SCHED_COSINE, 0.0, 4, 3),
+                          ("llada", "q8_0", dfx.LOW_CONFIDENCE, True, 64, dfx.SCHED_LINEAR, 0.0, 0, 5)])
+def test_device_loop_equals_host_loop(gpu, request, arch, scheme, remasking, use_cache, B, sched, T, refresh, keep):
+    """The device-resident loop (state and step bookkeeping in HBM, steps enqueued ahead of
+    their predecessors' selections) against the host-bookkeeping loop: the same tokens, the
+    same step at which each position is unmasked, the same rows and unmask counts per step;
+    entropy_exit with a threshold that exits early exercises a step enqueued after the last
+    one and dropped."""
+    path = _model_path(request, arch, scheme)
+    model = dfx.Model(path)
+    V = model.hparams.n_vocab
+    prompt = np.random.default_rng(8).integers(0, V - 16, 20).astype(np.int32)
+    outs = []
+    for tau in ((1.5, 60.0) if remasking == dfx.ENTROPY_EXIT else (1.5,)):
+        kw = dict(n_steps=16, temperature=T, schedule=sched, remasking=remasking, seed=99, use_cache=use_cache,
+                  cache_refresh=refresh, cache_keep_active=keep, entropy_threshold=tau)
+        for device_loop in (True, False):
+            ctx = dfx.Context(model, len(prompt) + B)
+            ctx.set_device_loop(device_loop)
+            st = dfx.GenStats()
+            toks, steps = ctx.generate_trace(prompt, B, dfx.SamplerParams.make(**kw), st)
+            n = st.actual_steps
+            outs.append((tau, device_loop, list(toks), list(steps), n, list(st.rows_per_step[:n]),
+                         list(st.unmasked_per_step[:n])))
+            ctx.close()
+        a, b = outs[-2], outs[-1]
+        assert a[2:] == b[2:], (tau, a, b)
+    model.close()
+
+
 def test_generate_more_than_2048_tokens(gpu, tiny_models):
     """n_generate above one workgroup's sort (2048 candidates): the selection ranks the
     candidates across workgroups; the reference has no such limit
