@@ -438,9 +438,11 @@ class Context:
                                     C.byref(n), C.byref(st), fn, None), "dfx_ar_generate")
         return out[:n.value].copy()
 
-    def set_device_loop(self, enable=True):
-        """Step bookkeeping of greedy dfx_generate on the device (default) or on the host."""
-        check(lib().dfx_context_set_device_loop(self.h, 1 if enable else 0), "dfx_context_set_device_loop")
+    def set_device_loop(self, enable=True, graphs=True):
+        """Step bookkeeping of greedy dfx_generate on the device (default; its layer stacks
+        replayed from captured graphs unless graphs=False) or on the host."""
+        mode = (1 if graphs else 2) if enable else 0
+        check(lib().dfx_context_set_device_loop(self.h, mode), "dfx_context_set_device_loop")
 
     def set_attention(self, mode):
         """ATTN_EXACT (the default) or ATTN_SPLIT_BF16 for this context's forward passes."""

@@ -94,8 +94,9 @@ extern "C" int dfx_context_set_attention(dfx_context * c, int mode) {
 }
 
 extern "C" int dfx_context_set_device_loop(dfx_context * c, int enable) {
-    if (!c) return DFX_ERR_ARG;
+    if (!c || enable < 0 || enable > 2) return DFX_ERR_ARG;
     c->device_loop = enable != 0;
+    c->use_graphs = enable == 1;
     return DFX_OK;
 }
 

@@ -44,7 +44,13 @@ struct dims {
     }
 };
 
+void drop_graphs(diffuse_context * c) {
+    for (auto & g : c->graphs) (void)hipGraphExecDestroy(g.exec);
+    c->graphs.clear();
+}
+
 void free_buffers(diffuse_context * c) {
+    drop_graphs(c);
     void * bufs[] = {c->x, c->act, c->qkv, c->qr, c->att, c->gu, c->logits, c->kc, c->vc, c->rope_tab,
                      c->d_ints, c->ws, c->d_stats, c->d_out, c->x_prev, c->d_imp, c->d_ar, c->d_state,
                      c->d_counts, c->d_hist};
@@ -324,6 +330,30 @@ const char * remask_name(int r) {
 }
 
 
+// forward_layers over M rows and n_keys keys from a captured graph (captured on first use).
+int layers_graphed(diffuse_context * c, int M, int n_keys, int & pending) {
+    for (auto & g : c->graphs)
+        if (g.M == M && g.n_keys == n_keys && g.mode == c->attn_mode) {
+            pending = g.pending;
+            return hip_ok(hipGraphLaunch(g.exec, c->stream), "hipGraphLaunch");
+        }
+    if (c->graphs.size() >= 64) drop_graphs(c);
+    hipGraph_t graph = nullptr;
+    TRY(hip_ok(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture"));
+    const int rc = forward_layers(c, M, n_keys, pass_opts(), pending);
+    const hipError_t e = hipStreamEndCapture(c->stream, &graph);
+    if (rc != DFX_OK || e != hipSuccess) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return rc != DFX_OK ? rc : hip_ok(e, "hipStreamEndCapture");
+    }
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ei = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    TRY(hip_ok(ei, "hipGraphInstantiate"));
+    c->graphs.push_back({M, n_keys, c->attn_mode, pending, exec});
+    return hip_ok(hipGraphLaunch(exec, c->stream), "hipGraphLaunch");
+}
+
 // Per-step device records and events of the device-resident loop, for up to n steps.
 int ensure_steps(diffuse_context * c, int n) {
     if (n > c->steps_cap) {
@@ -425,7 +455,10 @@ int generate_device(diffuse_context * c, const int32_t * prompt, int n_prompt, i
                              c->d_counts + 4 * s, c->stream));
         TRY(hip_ok(hipEventRecord(c->ev_fwd0[s], c->stream), "event"));
         int pending = 0;
-        TRY(forward_layers(c, M, N, pass_opts(), pending));
+        if (c->use_graphs && !c->prof)
+            TRY(layers_graphed(c, M, N, pending));
+        else
+            TRY(forward_layers(c, M, N, pass_opts(), pending));
         TRY(hip_ok(hipEventRecord(c->ev_fwd1[s], c->stream), "event"));
         if (use_cache) cache_init = true;
         // ---- the head and the sampler need the masked count when step s begins

@@ -113,6 +113,11 @@ struct diffuse_context {
     // prepare kernel's counts d_counts [steps][4] and the unmask count d_hist [steps],
     // copied to the pinned h_hist as each step ends (event ev_unmask[step]).
     bool         device_loop = true;
+    // The layer stack of a step captured once per (rows, keys, attention mode) as a HIP graph
+    // and replayed (kernels only: no memset or copy nodes); dropped with the buffers.
+    struct layers_graph { int M, n_keys, mode, pending; hipGraphExec_t exec; };
+    bool         use_graphs = true;
+    std::vector<layers_graph> graphs;
     int32_t *    d_state = nullptr;
     int32_t *    d_counts = nullptr;
     int32_t *    d_hist = nullptr;

@@ -331,9 +331,11 @@ int  dfx_generate(dfx_context * c, const int32_t * prompt, int n_prompt, int n_g
 int  dfx_context_set_attention(dfx_context * c, int mode);
 /* Loop of the context's dfx_generate calls at temperature 0 with a policy other than RANDOM:
  * 1 (the default) keeps the sequence state and the step bookkeeping on the device
- * (dfx_step_prepare / dfx_step_unmask; no step waits for its own selection), 0 runs that
- * bookkeeping on the host with one wait per step.  Both give the same tokens.
- * Build-defined; no counterpart in the reference. */
+ * (dfx_step_prepare / dfx_step_unmask; no step waits for its own selection) and replays each
+ * step's layer stack from a HIP graph captured once per (rows, keys, attention mode); 2 is
+ * the same loop with every kernel launched one by one; 0 runs the bookkeeping on the host
+ * with one wait per step.  All give the same tokens.  Build-defined; no counterpart in the
+ * reference. */
 int  dfx_context_set_device_loop(dfx_context * c, int enable);
 int  dfx_context_profile(dfx_context * c, int enable);
 int  dfx_context_profile_read(dfx_context * c, int wtype, int64_t * launches, double * ms, double * flops,

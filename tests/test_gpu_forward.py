@@ -188,29 +188,37 @@ def test_generate_matches_oracle_loop(gpu, request, arch, scheme, remasking, use
                           ("llada", "q8_0", dfx.LOW_CONFIDENCE, True, 64, dfx.SCHED_LINEAR, 0.0, 0, 5)])
 def test_device_loop_equals_host_loop(gpu, request, arch, scheme, remasking, use_cache, B, sched, T, refresh, keep):
     """The device-resident loop (state and step bookkeeping in HBM, steps enqueued ahead of
-    their predecessors' selections) against the host-bookkeeping loop: the same tokens, the
-    same step at which each position is unmasked, the same rows and unmask counts per step;
-    entropy_exit with a threshold that exits early exercises a step enqueued after the last
-    one and dropped."""
+    their predecessors' selections, layer stacks replayed from captured HIP graphs) against
+    the same loop launching every kernel and against the host-bookkeeping loop: the same
+    tokens, the same step at which each position is unmasked, the same rows and unmask counts
+    per step.  The graph context generates three times (every step's graph replayed, with the
+    other loops' work and synchronisations in between); entropy_exit with a threshold that
+    exits early exercises a step enqueued after the last one and dropped."""
     path = _model_path(request, arch, scheme)
     model = dfx.Model(path)
     V = model.hparams.n_vocab
     prompt = np.random.default_rng(8).integers(0, V - 16, 20).astype(np.int32)
-    outs = []
+    graphed = dfx.Context(model, len(prompt) + B)
     for tau in ((1.5, 60.0) if remasking == dfx.ENTROPY_EXIT else (1.5,)):
         kw = dict(n_steps=16, temperature=T, schedule=sched, remasking=remasking, seed=99, use_cache=use_cache,
                   cache_refresh=refresh, cache_keep_active=keep, entropy_threshold=tau)
-        for device_loop in (True, False):
-            ctx = dfx.Context(model, len(prompt) + B)
-            ctx.set_device_loop(device_loop)
+
+        def run(ctx):
             st = dfx.GenStats()
             toks, steps = ctx.generate_trace(prompt, B, dfx.SamplerParams.make(**kw), st)
             n = st.actual_steps
-            outs.append((tau, device_loop, list(toks), list(steps), n, list(st.rows_per_step[:n]),
-                         list(st.unmasked_per_step[:n])))
+            return (list(toks), list(steps), n, list(st.rows_per_step[:n]), list(st.unmasked_per_step[:n]))
+        ref = None
+        for mode in ("host", "eager", "graphs"):
+            ctx = dfx.Context(model, len(prompt) + B)
+            ctx.set_device_loop(mode != "host", graphs=(mode == "graphs"))
+            got = run(ctx)
             ctx.close()
-        a, b = outs[-2], outs[-1]
-        assert a[2:] == b[2:], (tau, a, b)
+            if ref is None:
+                ref = got
+            assert got == ref, (tau, mode, got, ref)
+            assert run(graphed) == ref, (tau, "graph replay")
+    graphed.close()
     model.close()
 
 
