@@ -353,28 +353,50 @@ extern "C" int dfx_select(const dfx_candidate * cand, int n, int remasking, floa
 // R (= repeat_last_n) tokens.  The chosen token becomes st[0], the position advances,
 // the token enters the ring (the oldest leaves once R are held), and it is also
 // written to tok_out.
+#define GREEDY_RING_MAX 4096   // recent tokens the device sampler holds (longer windows: host sampler)
 __global__ void __launch_bounds__(RS_THREADS) k_ar_greedy(float * __restrict__ row, int V, int32_t * __restrict__ st,
                                                           int R, float penalty, int32_t * __restrict__ tok_out) {
 #pragma clang fp contract(off)
     __shared__ float red_v[RS_THREADS / 64];
     __shared__ int red_i[RS_THREADS / 64];
+    __shared__ int ring[GREEDY_RING_MAX];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    if (tid == 0 && penalty > 1.0f && R > 0) {
+    if (penalty > 1.0f && R > 0) {
+        // the ring's tokens in LDS; the first occurrence of each token applies the penalty
+        // as many times as the token occurs, in one read-modify-write of the row
         const int n = st[2], start = st[3];
-        for (int j = 0; j < n; j++) {
-            const int t = st[4 + (start + j) % R];
-            if (t >= 0 && t < V) {
-                const float v = row[t];
-                row[t] = v > 0.0f ? v / penalty : v * penalty;
+        for (int j = tid; j < n; j += RS_THREADS) ring[j] = st[4 + (start + j) % R];
+        __syncthreads();
+        for (int j = tid; j < n; j += RS_THREADS) {
+            const int t = ring[j];
+            bool first = true;
+            int count = 0;
+            for (int k = 0; k < n; k++) {
+                first = first && !(k < j && ring[k] == t);
+                count += ring[k] == t;
+            }
+            if (first && t >= 0 && t < V) {
+                float v = row[t];
+                for (int c = 0; c < count; c++) v = v > 0.0f ? v / penalty : v * penalty;
+                row[t] = v;
             }
         }
     }
     __syncthreads();   // the penalised values are visible to the whole workgroup
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = tid; i < V; i += RS_THREADS) {
-        const float v = row[i];
-        if (v > bv) { bv = v; bi = i; }     // increasing i per thread: the first maximum stays
+    // eight loads in flight per thread; increasing i per thread, so the first maximum stays
+    constexpr int U = 8;
+    for (int i0 = tid; i0 < V; i0 += U * RS_THREADS) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = i0 + u * RS_THREADS;
+            v[u] = i < V ? row[i] : -INFINITY;
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (v[u] > bv) { bv = v[u]; bi = i0 + u * RS_THREADS; }
     }
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(bv, o, WAVE);
@@ -406,8 +428,9 @@ __global__ void __launch_bounds__(RS_THREADS) k_ar_greedy(float * __restrict__ r
 
 extern "C" int dfx_ar_greedy(float * row, int64_t V, int32_t * state, int repeat_last_n, float repeat_penalty,
                              int32_t * token_out, void * stream) {
-    if (!row || !state || !token_out || V <= 0 || V > INT32_MAX) {
-        dfx_set_error("dfx_ar_greedy: bad arguments (V=%lld)", (long long)V);
+    if (!row || !state || !token_out || V <= 0 || V > INT32_MAX || repeat_last_n > GREEDY_RING_MAX) {
+        dfx_set_error("dfx_ar_greedy: bad arguments (V=%lld, repeat_last_n=%d, at most %d)", (long long)V,
+                      repeat_last_n, GREEDY_RING_MAX);
         return DFX_ERR_ARG;
     }
     hipLaunchKernelGGL(k_ar_greedy, dim3(1), dim3(RS_THREADS), 0, (hipStream_t)stream, row, (int)V, state,

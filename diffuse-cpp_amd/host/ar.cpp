@@ -263,7 +263,9 @@ int engine_ar_generate(diffuse_context * c, const int32_t * prompt, int n_prompt
     const int V = (int)hp.n_vocab, L = (int)hp.n_layer;
     const int total_ctx = n_prompt + std::max(max_tokens, 1);
     DIFFUSE_LOG("ar_generate: prompt=%d tokens, max_generate=%d, ctx=%d", n_prompt, max_tokens, total_ctx);
-    const bool greedy = p.temperature <= 0.0f;
+    // greedy sampling runs on the device for rings up to 4096 recent tokens (the same
+    // result as the host sampler, which takes longer windows)
+    const bool greedy = p.temperature <= 0.0f && std::min(std::max(p.repeat_last_n, 0), total_ctx) <= 4096;
     // the recent list never holds more than total_ctx tokens, so a ring of that size
     // never evicts where the reference's list would not
     const int ring = std::min(std::max(p.repeat_last_n, 0), total_ctx);
