@@ -121,6 +121,23 @@ __host__ __device__ inline act_layout act_layout_of(int mode, int64_t M, int64_t
     return L;
 }
 
+// GEMM epilogues: plain (y = (v + bias) + residual), or SwiGLU over gate|up columns
+// interleaved in blocks of 32 (columns 32j + i, i < 16: gate of F-index 16j + i; i >= 16:
+// up of 16j + i - 16), written as h[m][f] = silu(gate) * up with row stride ldy.
+#define DFX_EPI_PLAIN 0
+#define DFX_EPI_SWIGLU 1
+
+// exp inside GGML ops (silu, soft_max) is taken correctly rounded: (float)exp((double)x).
+__device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
+// GGML ggml_silu_f32 (x / (1 + exp(-x))) times the up value, as the reference graph's
+// ggml_silu + ggml_mul (src/diffuse-graph.cpp:138-139).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    const float e = exp_cr(-g);
+    const float d = 1.0f + e;
+    const float sg = g / d;   // the compiler's correctly rounded f32 division
+    return sg * u;
+}
+
 // Error plumbing shared by the host-side launch wrappers.
 extern "C" void dfx_set_error(const char * fmt, ...);
 #define DFX_CHECK_LAUNCH(name)                                                     \

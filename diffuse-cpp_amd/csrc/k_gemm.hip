@@ -144,7 +144,27 @@ __device__ __forceinline__ int tile_row(int r, int lane) { return 8 * (r >> 2) +
 template <typename V16>
 __device__ __forceinline__ void epilogue_tile(const V16 & acc, int m0, int n, int M, int N, const float * bias,
                                               const float * res, float * Y, int64_t ldy, const int32_t * ymap,
-                                              float * ws, int z, int lane) {
+                                              float * ws, int z, int lane, int epi) {
+#pragma clang fp contract(off)
+    if (!ws && epi == DFX_EPI_SWIGLU) {
+        // lane ^ 16 holds the same rows of column n ^ 16 (n is 32j + lane % 32): a gate lane
+        // and its up lane share F-index f.  The pair splits the 16 rows: the gate lane forms
+        // h for registers 0..7, the up lane for registers 8..15 (rows 16 further down), each
+        // receiving the partner's value of its rows (no bias, residual or row map here).
+        const bool gate = (n & 16) == 0;
+        const int64_t f = (int64_t)(n >> 5) * 16 + (n & 15);
+        const int dm = gate ? 0 : 16;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float mine_lo = (float)acc[i], mine_hi = (float)acc[i + 8];
+            const float other = __shfl_xor(gate ? mine_hi : mine_lo, 16, WAVE);
+            const float g = gate ? mine_lo : other;
+            const float u = gate ? other : mine_hi;
+            const int m = m0 + tile_row(i, lane) + dm;
+            if (n < N && m < M) Y[(int64_t)m * ldy + f] = silu_mul(g, u);
+        }
+        return;
+    }
     if (ws) {
         if (n < N)
 #pragma unroll
@@ -187,7 +207,8 @@ __device__ __forceinline__ void epilogue_tile(const V16 & acc, int m0, int n, in
 template <int WT, int TM>
 __global__ void __launch_bounds__(256, 2)
 k_mmq(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__ act, int M,
-      const float * __restrict__ bias, const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap) {
+      const float * __restrict__ bias, const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
+      int epi) {
 #pragma clang fp contract(off)
     constexpr int BM = TM * 32, BN = 128, WSTR = wstride<WT>();
     constexpr bool KQ = WT != DFX_TYPE_Q8_0;     // Q8_K activations: d per 256, bsums per 16
@@ -378,7 +399,7 @@ k_mmq(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
 
     const int n = n0 + wn * 32 + (lane & 31);
 #pragma unroll
-    for (int i = 0; i < TM; i++) epilogue_tile(T1[i], m0 + i * 32, n, M, N, bias, res, Y, ldy, ymap, nullptr, 0, lane);
+    for (int i = 0; i < TM; i++) epilogue_tile(T1[i], m0 + i * 32, n, M, N, bias, res, Y, ldy, ymap, nullptr, 0, lane, epi);
 }
 
 // ---------------------------------------------------------------------------
@@ -475,7 +496,7 @@ template <int TM, int TN, int D>
 __global__ void __launch_bounds__(256, TM * TN >= 4 ? 1 : 2)
 k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__ act, int M,
       const float * __restrict__ bias, const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
-      int n_tiles, int m_tiles, float * __restrict__ ws) {
+      int n_tiles, int m_tiles, float * __restrict__ ws, int epi) {
 #pragma clang fp contract(off)
     constexpr int BM = TM * 32, BN = 4 * TN * 32;
     constexpr int BST = 24;                  // LDS halves per row of 16 block sums
@@ -689,7 +710,7 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
 #pragma unroll
         for (int i = 0; i < TM; i++)
             epilogue_tile(T[i][t], m0 + i * 32, n0 + (wv * TN + t) * 32 + l32, M, N, bias, res, Y, ldy, ymap, ws, z,
-                          lane);
+                          lane, epi);
 }
 
 // ---------------------------------------------------------------------------
@@ -724,7 +745,7 @@ template <int TM, int TN, int DEPTH>
 __global__ void __launch_bounds__(256, TN == 1 ? 2 : 1)
 k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__ act, int M,
         const float * __restrict__ bias, const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
-        int n_tiles, int m_tiles, float * __restrict__ ws) {
+        int n_tiles, int m_tiles, float * __restrict__ ws, int epi) {
 #pragma clang fp contract(off)
     constexpr int BM = 32 * TM, BN = 128 * TN, WSZ = 2048 * TN;   // WSZ: nibble bytes per wave and step
     constexpr int NA = 2 * TM;                                     // A operand copies per wave and step
@@ -989,7 +1010,7 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
 #pragma unroll
         for (int i = 0; i < TM; i++)
             epilogue_tile(T[i][t], m0 + i * 32, n0 + (wv * TN + t) * 32 + l32, M, N, bias, res, Y, ldy, ymap, ws, z,
-                          lane);
+                          lane, epi);
 }
 
 // ---------------------------------------------------------------------------
@@ -1046,7 +1067,7 @@ template <int TM, int TN, int D>
 __global__ void __launch_bounds__(256, TM * TN >= 4 ? 1 : 2)
 k_q6k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__ act, int M,
       const float * __restrict__ bias, const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
-      int n_tiles, int m_tiles, float * __restrict__ ws) {
+      int n_tiles, int m_tiles, float * __restrict__ ws, int epi) {
 #pragma clang fp contract(off)
     constexpr int BM = TM * 32, BN = 4 * TN * 32;
     constexpr int A_PER_T = BM * 16 / 256;
@@ -1229,7 +1250,7 @@ k_q6k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
 #pragma unroll
         for (int i = 0; i < TM; i++)
             epilogue_tile(T[i][t], m0 + i * 32, n0 + (wv * TN + t) * 32 + l32, M, N, bias, res, Y, ldy, ymap, ws, z,
-                          lane);
+                          lane, epi);
 }
 
 // ---------------------------------------------------------------------------
@@ -1239,7 +1260,7 @@ template <int TM>
 __global__ void __launch_bounds__(256, 2)
 k_gemm_f16(const uint8_t * __restrict__ W, int N, int K, const half_t * __restrict__ A, int M,
            const float * __restrict__ bias, const float * res, float * Y, int64_t ldy,
-           const int32_t * __restrict__ ymap, float * __restrict__ ws, int kt_per_split) {
+           const int32_t * __restrict__ ymap, float * __restrict__ ws, int kt_per_split, int epi) {
     constexpr int BM = TM * 32, BN = 128, WSTR = wstride<DFX_TYPE_F16>();
     __shared__ __attribute__((aligned(16))) uint8_t Ws[BN * WSTR];
     __shared__ __attribute__((aligned(16))) half_t As[BM * ASTR];
@@ -1278,7 +1299,7 @@ k_gemm_f16(const uint8_t * __restrict__ W, int N, int K, const half_t * __restri
 #pragma unroll
     for (int i = 0; i < TM; i++)
         epilogue_tile(acc[i], m0 + i * 32, n, M, N, bias, res, Y, ldy, ymap, split ? ws : nullptr, (int)blockIdx.z,
-                      lane);
+                      lane, epi);
 }
 
 // ---------------------------------------------------------------------------
@@ -1295,7 +1316,7 @@ template <int TM>
 __global__ void __launch_bounds__(256, 2)
 k_gemm_f32(const float * __restrict__ W, int N, int K, const float * __restrict__ A, int M,
            const float * __restrict__ bias, const float * res, float * Y, int64_t ldy,
-           const int32_t * __restrict__ ymap) {
+           const int32_t * __restrict__ ymap, int epi) {
     constexpr int BM = TM * 32, BN = 128;
     __shared__ float Ws[BN * FSTR];
     __shared__ float As[BM * FSTR];
@@ -1347,7 +1368,7 @@ k_gemm_f32(const float * __restrict__ W, int N, int K, const float * __restrict_
     const int n = n0 + wn * 32 + l32;
 #pragma unroll
     for (int i = 0; i < TM; i++)
-        epilogue_tile(acc[i], m0 + i * 32, n, M, N, bias, res, Y, ldy, ymap, nullptr, 0, lane);
+        epilogue_tile(acc[i], m0 + i * 32, n, M, N, bias, res, Y, ldy, ymap, nullptr, 0, lane, epi);
 }
 
 // Fixed-order reduction of split-K partials plus epilogue: y = ((0 + p_0) + p_1 ...) + bias + res.
@@ -1356,8 +1377,27 @@ k_gemm_f32(const float * __restrict__ W, int N, int K, const float * __restrict_
 // addresses; elements past MN are not stored.
 #define REDUCE_R 4
 __global__ void k_gemm_reduce(const float * __restrict__ ws, int S, int64_t MN, int N, const float * bias,
-                              const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap) {
+                              const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
+                              int epi) {
+#pragma clang fp contract(off)
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    if (epi == DFX_EPI_SWIGLU) {
+        // one output h[m][f] per element: gate and up column sums (slice order), then silu * up
+        const int F = N / 2;
+        const int64_t MF = MN / 2;
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < MF; i += stride) {
+            const int64_t m = i / F;
+            const int f = (int)(i - m * F);
+            const int64_t cg = m * N + (int64_t)(f >> 4) * 32 + (f & 15);
+            float g = 0.0f, u = 0.0f;
+            for (int s = 0; s < S; s++) {
+                g = g + ws[(int64_t)s * MN + cg];
+                u = u + ws[(int64_t)s * MN + cg + 16];
+            }
+            Y[m * ldy + f] = silu_mul(g, u);
+        }
+        return;
+    }
     for (int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i0 < MN; i0 += REDUCE_R * stride) {
         int64_t idx[REDUCE_R];
         float v[REDUCE_R];
@@ -1465,7 +1505,7 @@ extern "C" size_t dfx_gemm_ws_bytes(int64_t M, int64_t N, int64_t K) {
 // into Y, or, with defer, leaves the slices for the consumer of Y (the next RMSNorm,
 // which then adds them and the residual itself) and reports S.
 static int reduce_or_defer(const void * ws, int S, int M, int N, const float * bias, const float * res, float * y,
-                           int64_t ldy, const int32_t * ymap, hipStream_t st, int * defer) {
+                           int64_t ldy, const int32_t * ymap, hipStream_t st, int * defer, int epi) {
     if (defer) {
         *defer = S;
         return DFX_OK;
@@ -1473,14 +1513,15 @@ static int reduce_or_defer(const void * ws, int S, int M, int N, const float * b
     const int64_t MN = (int64_t)M * N;
     const int64_t blocks = std::min<int64_t>((MN + 256 * REDUCE_R - 1) / (256 * REDUCE_R), 8192);
     hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)blocks), dim3(256), 0, st, (const float *)ws, S, MN, N, bias, res,
-                       y, ldy, ymap);
+                       y, ldy, ymap, epi);
     DFX_CHECK_LAUNCH("dfx_gemm reduce");
     return DFX_OK;
 }
 
 template <int TM>
 static int launch_f16(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                      float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer) {
+                      float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer,
+                      int epi) {
     constexpr int BM = TM * 32, BN = 128;
     const int gx = (N + BN - 1) / BN, gy = (M + BM - 1) / BM;
     const int n_kt = K / BK;
@@ -1496,36 +1537,37 @@ static int launch_f16(const void * w, int N, int K, const void * act, int M, con
     const int per = (n_kt + S - 1) / S;
     S = (n_kt + per - 1) / per;
     hipLaunchKernelGGL((k_gemm_f16<TM>), dim3(gx, gy, S), dim3(256), 0, st, (const uint8_t *)w, N, K,
-                       (const half_t *)act, M, bias, res, y, ldy, ymap, (float *)ws, per);
+                       (const half_t *)act, M, bias, res, y, ldy, ymap, (float *)ws, per, epi);
     DFX_CHECK_LAUNCH("dfx_gemm f16");
-    if (S > 1) return reduce_or_defer(ws, S, M, N, bias, res, y, ldy, ymap, st, defer);
+    if (S > 1) return reduce_or_defer(ws, S, M, N, bias, res, y, ldy, ymap, st, defer, epi);
     return DFX_OK;
 }
 
 template <int TM>
 static int launch_f32(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                      float * y, int64_t ldy, const int32_t * ymap, hipStream_t st) {
+                      float * y, int64_t ldy, const int32_t * ymap, hipStream_t st, int epi) {
     const dim3 grid((N + 127) / 128, (M + 32 * TM - 1) / (32 * TM));
     hipLaunchKernelGGL((k_gemm_f32<TM>), grid, dim3(256), 0, st, (const float *)w, N, K, (const float *)act, M, bias,
-                       res, y, ldy, ymap);
+                       res, y, ldy, ymap, epi);
     DFX_CHECK_LAUNCH("dfx_gemm f32");
     return DFX_OK;
 }
 
 template <int WT, int TM>
 static int launch_mmq(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                      float * y, int64_t ldy, const int32_t * ymap, hipStream_t st) {
+                      float * y, int64_t ldy, const int32_t * ymap, hipStream_t st, int epi) {
     constexpr int BM = TM * 32, BN = 128;
     const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
     hipLaunchKernelGGL((k_mmq<WT, TM>), grid, dim3(256), 0, st, (const uint8_t *)w, N, K, (const uint8_t *)act, M,
-                       bias, res, y, ldy, ymap);
+                       bias, res, y, ldy, ymap, epi);
     DFX_CHECK_LAUNCH("dfx_gemm");
     return DFX_OK;
 }
 
 template <int TM, int TN, int D>
 static int launch_q4k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                      float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st, int * defer) {
+                      float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st, int * defer,
+                      int epi) {
     constexpr int BM = TM * 32, BN = 4 * TN * 32;
     const int n_tiles = (N + BN - 1) / BN, m_tiles = (M + BM - 1) / BM;
     const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
@@ -1539,15 +1581,16 @@ static int launch_q4k(const void * w, int N, int K, const void * act, int M, con
         return DFX_ERR_ARG;
     }
     hipLaunchKernelGGL((k_q4k<TM, TN, D>), dim3((unsigned)(per_pass * passes)), dim3(256), 0, st,
-                       (const uint8_t *)w, N, K, (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles, ws);
+                       (const uint8_t *)w, N, K, (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles, ws, epi);
     DFX_CHECK_LAUNCH("dfx_gemm q4_k");
-    if (ws) return reduce_or_defer(ws, chunks, M, N, bias, res, y, ldy, ymap, st, defer);
+    if (ws) return reduce_or_defer(ws, chunks, M, N, bias, res, y, ldy, ymap, st, defer, epi);
     return DFX_OK;
 }
 
 template <int TM, int TN, int DEPTH>
 static int launch_q4k_w(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                        float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st, int * defer) {
+                        float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st, int * defer,
+                      int epi) {
     const int n_tiles = (N + 128 * TN - 1) / (128 * TN), m_tiles = (M + 32 * TM - 1) / (32 * TM);
     const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
     const int chunks = dot_chunks(K), passes = ws ? chunks : 1;
@@ -1557,15 +1600,16 @@ static int launch_q4k_w(const void * w, int N, int K, const void * act, int M, c
         return DFX_ERR_ARG;
     }
     hipLaunchKernelGGL((k_q4k_w<TM, TN, DEPTH>), dim3((unsigned)(per_pass * passes)), dim3(256), 0, st, (const uint8_t *)w, N,
-                       K, (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles, ws);
+                       K, (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles, ws, epi);
     DFX_CHECK_LAUNCH("dfx_gemm q4_k");
-    if (ws) return reduce_or_defer(ws, chunks, M, N, bias, res, y, ldy, ymap, st, defer);
+    if (ws) return reduce_or_defer(ws, chunks, M, N, bias, res, y, ldy, ymap, st, defer, epi);
     return DFX_OK;
 }
 
 template <int TM, int TN, int D>
 static int launch_q6k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                      float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st, int * defer) {
+                      float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st, int * defer,
+                      int epi) {
     constexpr int BM = TM * 32, BN = 4 * TN * 32;
     const int n_tiles = (N + BN - 1) / BN, m_tiles = (M + BM - 1) / BM;
     const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
@@ -1576,16 +1620,17 @@ static int launch_q6k(const void * w, int N, int K, const void * act, int M, con
         return DFX_ERR_ARG;
     }
     hipLaunchKernelGGL((k_q6k<TM, TN, D>), dim3((unsigned)(per_pass * passes)), dim3(256), 0, st,
-                       (const uint8_t *)w, N, K, (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles, ws);
+                       (const uint8_t *)w, N, K, (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles, ws, epi);
     DFX_CHECK_LAUNCH("dfx_gemm q6_k");
-    if (ws) return reduce_or_defer(ws, chunks, M, N, bias, res, y, ldy, ymap, st, defer);
+    if (ws) return reduce_or_defer(ws, chunks, M, N, bias, res, y, ldy, ymap, st, defer, epi);
     return DFX_OK;
 }
 
 // Q6_K: 64x128 workgroup tiles (2-deep weight ring), split K when the grid is small.
 // A forced tile "<TM>x<TN>[x<D>][s|n]" (dfx_gemm_force_tile) overrides the choice.
 static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                        float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer) {
+                        float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer,
+                        int epi) {
     int tm = M > 48 ? 2 : 1, tn = 1;
     const int chunks = dot_chunks(K);
     const int64_t tiles = (int64_t)((M + 32 * tm - 1) / (32 * tm)) * ((N + 128 * tn - 1) / (128 * tn));
@@ -1602,17 +1647,18 @@ static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, c
     if (sb_last % 2) d = 2;
     float * wsf = split ? (float *)ws : nullptr;
     if (tm == 2)
-        return d == 4 ? launch_q6k<2, 1, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer)
-                      : launch_q6k<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer);
-    return d == 4 ? launch_q6k<1, 1, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer)
-                  : launch_q6k<1, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer);
+        return d == 4 ? launch_q6k<2, 1, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi)
+                      : launch_q6k<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi);
+    return d == 4 ? launch_q6k<1, 1, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi)
+                  : launch_q6k<1, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi);
 }
 
 // Tile of the Q4_K kernel (TM x TN 32x32 tiles per wave, D = K steps in flight).
 // When the grid leaves the SIMDs short of two waves each, K is split at chunk
 // borders (workspace permitting).
 static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                        float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer) {
+                        float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer,
+                        int epi) {
     struct cand { int tm, tn, d; };
     // (a 96-row tile, TM = 3, spills its sums at two workgroups per CU and is not built)
     static const cand cands[] = {{2, 2, 2}, {4, 1, 2}, {2, 1, 2}, {1, 2, 2}, {1, 1, 4}, {1, 1, 2}, {2, 1, 4}, {2, 2, 4}};
@@ -1676,10 +1722,10 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
     if (f.on && f.w) {
         // "w": 64 x 64 per wave; "w1": 64 x 32 per wave, two workgroups per CU
         float * wsw = split ? (float *)ws : nullptr;
-        if (f.w1) return launch_q4k_w<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
-        if (f.w3) return launch_q4k_w<3, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
-        if (sb_last % 2) return launch_q4k_w<2, 2, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
-        return launch_q4k_w<2, 2, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer);
+        if (f.w1) return launch_q4k_w<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer, epi);
+        if (f.w3) return launch_q4k_w<3, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer, epi);
+        if (sb_last % 2) return launch_q4k_w<2, 2, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer, epi);
+        return launch_q4k_w<2, 2, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer, epi);
     }
     // 96-row tiles (k_q4k_w<3, 1, 2>): each dequantised weight feeds three MFMAs instead of
     // two, but a workgroup takes 1.5x longer, so they only pay when the chosen kernel's grid
@@ -1693,19 +1739,19 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
         const int64_t t_def = (int64_t)n_col * (dma ? (M + 63) / 64 : (M + 31) / 32);
         if (rounds(t3 * (split3 ? chunks : 1)) < rounds(t_def * (split ? chunks : 1)))
             return launch_q4k_w<3, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, split3 ? (float *)ws : nullptr, st,
-                                         defer);
+                                         defer, epi);
     }
-    if (dma) return launch_q4k_w<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, split ? (float *)ws : nullptr, st, defer);
+    if (dma) return launch_q4k_w<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, split ? (float *)ws : nullptr, st, defer, epi);
     if (cands[pick].d == 4 && (sb_last % 2))
         for (int c = 0; c < n_cand; c++)
             if (cands[c].tm == cands[pick].tm && cands[c].tn == cands[pick].tn && cands[c].d == 2) { pick = c; break; }
     float * wsf = split ? (float *)ws : nullptr;
 #define Q4K_CASE(c, TM_, TN_, D_) \
-    case c: return launch_q4k<TM_, TN_, D_>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer);
+    case c: return launch_q4k<TM_, TN_, D_>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi);
     switch (pick) {
         Q4K_CASE(0, 2, 2, 2) Q4K_CASE(1, 4, 1, 2) Q4K_CASE(2, 2, 1, 2) Q4K_CASE(3, 1, 2, 2) Q4K_CASE(4, 1, 1, 4)
         Q4K_CASE(6, 2, 1, 4) Q4K_CASE(7, 2, 2, 4)
-        default: return launch_q4k<1, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer);
+        default: return launch_q4k<1, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi);
     }
 #undef Q4K_CASE
 }
@@ -1725,8 +1771,8 @@ static int pick_tm(int M, int max_tm) {
 // MI355X: 2-5x slower with 64 or 96 rows per workgroup at M = 96..768).
 template <int WT>
 static int dispatch_mmq(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                        float * y, int64_t ldy, const int32_t * ymap, hipStream_t st) {
-    return launch_mmq<WT, 1>(w, N, K, act, M, bias, res, y, ldy, ymap, st);
+                        float * y, int64_t ldy, const int32_t * ymap, hipStream_t st, int epi) {
+    return launch_mmq<WT, 1>(w, N, K, act, M, bias, res, y, ldy, ymap, st, epi);
 }
 
 // Internal form: output row m goes to row ymap[m] (or m) of Y with leading dimension
@@ -1734,13 +1780,18 @@ static int dispatch_mmq(const void * w, int N, int K, const void * act, int M, c
 // is large enough.
 int dfx_gemm_ex(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
                 const float * bias, const float * residual, float * y, int64_t ldy, const int32_t * ymap,
-                void * ws, size_t ws_bytes, void * stream, int * n_partials) {
+                void * ws, size_t ws_bytes, void * stream, int * n_partials, int epi) {
     // n_partials: if K gets split, leave the partial slices ws[s][m][n] for the caller
     // to add (calls without bias or row map, ldy = N) and report their number; 0 = Y
     // was written
     if (n_partials) *n_partials = 0;
-    int * defer = n_partials && !bias && !ymap && ldy == N ? n_partials : nullptr;
-    if (N <= 0 || K <= 0 || M < 0 || (K % 256) || N > INT32_MAX || M > INT32_MAX || K > INT32_MAX || ldy < N) {
+    if (epi != DFX_EPI_PLAIN && (epi != DFX_EPI_SWIGLU || bias || residual || ymap || N % 32)) {
+        dfx_set_error("dfx_gemm: the SwiGLU epilogue takes N a multiple of 32, no bias, residual or row map");
+        return DFX_ERR_ARG;
+    }
+    int * defer = n_partials && !bias && !ymap && ldy == N && epi == DFX_EPI_PLAIN ? n_partials : nullptr;
+    if (N <= 0 || K <= 0 || M < 0 || (K % 256) || N > INT32_MAX || M > INT32_MAX || K > INT32_MAX ||
+        ldy < (epi == DFX_EPI_SWIGLU ? N / 2 : N)) {
         dfx_set_error("dfx_gemm: bad shape M=%lld N=%lld K=%lld ldy=%lld (K must be a multiple of 256)",
                       (long long)M, (long long)N, (long long)K, (long long)ldy);
         return DFX_ERR_ARG;
@@ -1749,19 +1800,19 @@ int dfx_gemm_ex(int wtype, const void * w, int64_t N, int64_t K, const void * ac
     hipStream_t st = (hipStream_t)stream;
     const int n = (int)N, k = (int)K, m = (int)M;
     switch (wtype) {
-        case DFX_TYPE_Q4_K: return dispatch_q4k(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer);
-        case DFX_TYPE_Q6_K: return dispatch_q6k(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer);
-        case DFX_TYPE_Q8_0: return dispatch_mmq<DFX_TYPE_Q8_0>(w, n, k, act, m, bias, residual, y, ldy, ymap, st);
+        case DFX_TYPE_Q4_K: return dispatch_q4k(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer, epi);
+        case DFX_TYPE_Q6_K: return dispatch_q6k(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer, epi);
+        case DFX_TYPE_Q8_0: return dispatch_mmq<DFX_TYPE_Q8_0>(w, n, k, act, m, bias, residual, y, ldy, ymap, st, epi);
         case DFX_TYPE_F16:
             switch (pick_tm(m, 4)) {
-                case 1: return launch_f16<1>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer);
-                case 2: return launch_f16<2>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer);
-                case 3: return launch_f16<3>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer);
-                default: return launch_f16<4>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer);
+                case 1: return launch_f16<1>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer, epi);
+                case 2: return launch_f16<2>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer, epi);
+                case 3: return launch_f16<3>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer, epi);
+                default: return launch_f16<4>(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer, epi);
             }
         case DFX_TYPE_F32:
-            if (m <= 32) return launch_f32<1>(w, n, k, act, m, bias, residual, y, ldy, ymap, st);
-            return launch_f32<2>(w, n, k, act, m, bias, residual, y, ldy, ymap, st);
+            if (m <= 32) return launch_f32<1>(w, n, k, act, m, bias, residual, y, ldy, ymap, st, epi);
+            return launch_f32<2>(w, n, k, act, m, bias, residual, y, ldy, ymap, st, epi);
     }
     dfx_set_error("dfx_gemm: unsupported weight type %d", wtype);
     return DFX_ERR_UNSUPPORTED;
@@ -1770,7 +1821,13 @@ int dfx_gemm_ex(int wtype, const void * w, int64_t N, int64_t K, const void * ac
 extern "C" int dfx_gemm(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
                         const float * bias, const float * residual, float * y, void * ws, void * stream) {
     return dfx_gemm_ex(wtype, w, N, K, act, M, bias, residual, y, N, nullptr, ws,
-                       ws ? dfx_gemm_ws_bytes(M, N, K) : 0, stream, nullptr);
+                       ws ? dfx_gemm_ws_bytes(M, N, K) : 0, stream, nullptr, DFX_EPI_PLAIN);
+}
+
+extern "C" int dfx_gemm_swiglu(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
+                               float * y, int64_t ldy, void * ws, void * stream) {
+    return dfx_gemm_ex(wtype, w, N, K, act, M, nullptr, nullptr, y, ldy, nullptr, ws,
+                       ws ? dfx_gemm_ws_bytes(M, N, K) : 0, stream, nullptr, DFX_EPI_SWIGLU);
 }
 
 // ---------------------------------------------------------------------------
@@ -1820,5 +1877,5 @@ extern "C" int dfx_gemm_noalloc(int wtype, const void * w, int64_t N, int64_t K,
     // the same workspace size as dfx_gemm's (when it fits), so the same split is chosen
     const size_t ws_bytes = std::min<size_t>(dfx_gemm_ws_bytes(M, N, K), DFX_GEMM_SCRATCH_BYTES);
     return dfx_gemm_ex(wtype, w, N, K, act, M, bias, residual, y, N, nullptr, scratch_ptr[dev], ws_bytes, stream,
-                       nullptr);
+                       nullptr, DFX_EPI_PLAIN);
 }

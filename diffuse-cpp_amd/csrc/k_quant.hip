@@ -268,9 +268,6 @@ __global__ void __launch_bounds__(1024) k_rmsnorm_convert(int mode, float * x, c
     }
 }
 
-// exp inside GGML ops (silu, soft_max) is taken correctly rounded: (float)exp((double)x).
-__device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
-
 // silu(gate) * up, then conversion.  gu row m = [gate F | up F]; one wave per (row, block).
 // GGML ggml_silu_f32: x / (1 + exp(-x)).
 __global__ void k_swiglu_convert(int mode, const float * gu, int64_t M, int64_t F, uint8_t * act) {
@@ -283,8 +280,7 @@ __global__ void k_swiglu_convert(int mode, const float * gu, int64_t M, int64_t 
     const int64_t k = b * 256 + 4 * lane;
     const float4 g = *(const float4 *)(gu + m * 2 * F + k);
     const float4 u = *(const float4 *)(gu + m * 2 * F + F + k);
-    auto silu = [](float a) { return (float)((double)a / (double)(1.0f + exp_cr(-a))); };
-    const float v[4] = {silu(g.x) * u.x, silu(g.y) * u.y, silu(g.z) * u.z, silu(g.w) * u.w};
+    const float v[4] = {silu_mul(g.x, u.x), silu_mul(g.y, u.y), silu_mul(g.z, u.z), silu_mul(g.w, u.w)};
     const act_layout Lay = act_layout_of(mode, M, F);
     convert_block256(v, lane, mode, act, Lay, m, F, b);
 }

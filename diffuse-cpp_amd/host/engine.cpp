@@ -163,22 +163,25 @@ hipEvent_t take_event(diffuse_context * c) {
 // With n_partials, a split-K GEMM may leave its chunk sums in c->ws (see dfx_gemm_ex)
 // for the next RMSNorm to add.
 int gemm(diffuse_context * c, const dev_matrix & w, int64_t N, int64_t K, int64_t M, const float * bias,
-         const float * res, float * y, int64_t ldy, const int32_t * ymap, bool split_ok, int * n_partials = nullptr) {
+         const float * res, float * y, int64_t ldy, const int32_t * ymap, bool split_ok, int * n_partials = nullptr,
+         int epi = DFX_EPI_PLAIN) {
     void * ws = split_ok ? c->ws : nullptr;
     const size_t wsb = split_ok ? c->ws_bytes : 0;
     if (n_partials) *n_partials = 0;
     if (!c->prof || M == 0)
-        return dfx_gemm_ex(w.type, w.data, N, K, c->act, M, bias, res, y, ldy, ymap, ws, wsb, c->stream, n_partials);
+        return dfx_gemm_ex(w.type, w.data, N, K, c->act, M, bias, res, y, ldy, ymap, ws, wsb, c->stream, n_partials,
+                           epi);
     diffuse_context::gemm_rec r;
     r.a = take_event(c);
     r.b = take_event(c);
     r.type = w.type;
     r.M = M;
     r.flops = 2.0 * (double)M * N * K;
-    r.bytes = (double)dfx_device_row_bytes(w.type, K) * N + (double)M * K * 2 + (double)M * N * 4;
+    r.bytes = (double)dfx_device_row_bytes(w.type, K) * N + (double)M * K * 2 +
+              (double)M * N * (epi == DFX_EPI_SWIGLU ? 2 : 4);
     if (!r.a || !r.b) return hip_ok(hipErrorOutOfMemory, "hipEventCreate");
     TRY(hip_ok(hipEventRecord(r.a, c->stream), "event"));
-    TRY(dfx_gemm_ex(w.type, w.data, N, K, c->act, M, bias, res, y, ldy, ymap, ws, wsb, c->stream, n_partials));
+    TRY(dfx_gemm_ex(w.type, w.data, N, K, c->act, M, bias, res, y, ldy, ymap, ws, wsb, c->stream, n_partials, epi));
     TRY(hip_ok(hipEventRecord(r.b, c->stream), "event"));
     c->prof_pending.push_back(r);
     return DFX_OK;
@@ -215,6 +218,11 @@ int run_group(diffuse_context * c, const proj_group & g, const float * norm, int
         return dfx_rmsnorm_convert_add(type, c->x, nullptr, (const float *)c->ws, np, M, norm, M, K, eps, c->act,
                                        c->stream);
     };
+    if (g.swiglu) {   // out[M][n_out / 2] = silu(gate) * up
+        TRY(norm_convert(g.all.type));
+        return gemm(c, g.all, g.n_out, K, M, nullptr, nullptr, out, g.n_out / 2, nullptr, true, nullptr,
+                    DFX_EPI_SWIGLU);
+    }
     if (g.fused) {
         TRY(norm_convert(g.all.type));
         return gemm(c, g.all, g.n_out, K, M, g.bias, nullptr, out, g.n_out, nullptr, true);
@@ -262,7 +270,10 @@ int forward_layers(diffuse_context * c, int M, int n_keys, const pass_opts & o, 
         TRY(dfx_act_convert(L.o.type, c->att, M, D.d, c->act, c->stream));
         TRY(gemm(c, L.o, D.d, D.d, M, nullptr, c->x, c->x, D.d, nullptr, true, defer));
         TRY(run_group(c, L.gu, L.ffn_norm, M, D.d, c->gu, pending));
-        TRY(dfx_swiglu_convert(L.down.type, c->gu, M, D.F, c->act, c->stream));
+        if (L.gu.swiglu)
+            TRY(dfx_act_convert(L.down.type, c->gu, M, D.F, c->act, c->stream));
+        else
+            TRY(dfx_swiglu_convert(L.down.type, c->gu, M, D.F, c->act, c->stream));
         TRY(gemm(c, L.down, D.d, D.F, M, nullptr, c->x, c->x, D.d, nullptr, true, defer));
         if (o.impact_rows) TRY(dfx_layer_impact(c->x, c->x_prev, M, D.d, o.impact_rows + il * M, c->stream));
     }

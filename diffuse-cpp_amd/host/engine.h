@@ -12,10 +12,16 @@
 
 #define DIFFUSE_LOG(fmt, ...) fprintf(stderr, "[diffuse] " fmt "\n", ##__VA_ARGS__)
 
+// GEMM epilogues (the same values as in the device header csrc/dfx_device.h)
+#define DFX_EPI_PLAIN 0
+#define DFX_EPI_SWIGLU 1
+
 // Internal kernel entry points with row maps (k_gemm.hip, k_quant.hip, k_sampler.hip).
+// epi: DFX_EPI_PLAIN, or DFX_EPI_SWIGLU (gate|up rows interleaved in blocks of 16: y[m][f] =
+// silu(gate) * up with row stride ldy >= N / 2; no bias, residual or row map).
 int dfx_gemm_ex(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M, const float * bias,
                 const float * residual, float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes,
-                void * stream, int * n_partials);
+                void * stream, int * n_partials, int epi = DFX_EPI_PLAIN);
 int dfx_rmsnorm_convert_ex(int wtype, const float * x, const int32_t * xmap, const float * w, int64_t M, int64_t K,
                            float eps, void * act, void * stream);
 // RMSNorm + conversion of x after adding a deferred split-K result: row r (= xmap[m] or m)
@@ -43,6 +49,9 @@ struct proj_group {
     bool                    fused = false;
     dev_matrix              all;        // valid when fused
     float *                 bias = nullptr;   // [n_out] f32 or null
+    // gate|up fused with rows interleaved in blocks of 16 (16 gate rows, then the 16 up rows
+    // of the same F-indices): its GEMM applies SwiGLU in the epilogue (DFX_EPI_SWIGLU)
+    bool                    swiglu = false;
 };
 
 struct dev_layer {

@@ -134,6 +134,34 @@ struct loader {
         return upload(dst, host.data(), host.size());
     }
 
+    // gate and up (same type and shape, rows a multiple of 16) repacked with their rows
+    // interleaved in blocks of 16, so that one 32-column tile of the GEMM holds the gate and
+    // up values of 16 F-indices and its epilogue forms silu(gate) * up.
+    bool swiglu_group(const gguf::tensor_info * gate, const gguf::tensor_info * up, proj_group & g) {
+        const int64_t F = gate->ne[1], K = gate->ne[0];
+        const int64_t drb = dfx_device_row_bytes(gate->type, K);
+        std::vector<uint8_t> hg((size_t)(drb * F)), hu((size_t)(drb * F)), both((size_t)(2 * drb * F));
+        if (dfx_repack_rows(gate->type, gate->data, F, K, hg.data()) != DFX_OK ||
+            dfx_repack_rows(up->type, up->data, F, K, hu.data()) != DFX_OK) {
+            err = dfx_last_error();
+            return false;
+        }
+        for (int64_t j = 0; j < F / 16; j++) {
+            memcpy(both.data() + (size_t)(32 * j) * drb, hg.data() + (size_t)(16 * j) * drb, (size_t)(16 * drb));
+            memcpy(both.data() + (size_t)(32 * j + 16) * drb, hu.data() + (size_t)(16 * j) * drb, (size_t)(16 * drb));
+        }
+        uint8_t * base = (uint8_t *)dalloc(both.size());
+        if (!base || !upload(base, both.data(), both.size())) return false;
+        g.all.type = dfx_device_type(gate->type);
+        g.all.rows = 2 * F;
+        g.all.cols = K;
+        g.all.data = base;
+        g.n_out = 2 * F;   // parts stay empty: the two matrices are not contiguous
+        g.fused = true;
+        g.swiglu = true;
+        return true;
+    }
+
     bool group(const std::vector<const gguf::tensor_info *> & ts, const std::vector<const gguf::tensor_info *> & biases,
                proj_group & g) {
         size_t total = 0;
@@ -268,7 +296,11 @@ struct loader {
                 return false;
             if (!(L.attn_norm = vec_f32(an, d)) || !(L.ffn_norm = vec_f32(fn, d))) return false;
             if (!group({wq, wk, wv}, {bq, bk, bv}, L.qkv)) return false;
-            if (!group({wg, wu}, {nullptr, nullptr}, L.gu)) return false;
+            if (dfx_device_type(wg->type) == dfx_device_type(wu->type) && wg->ne[1] % 16 == 0) {
+                if (!swiglu_group(wg, wu, L.gu)) return false;
+            } else if (!group({wg, wu}, {nullptr, nullptr}, L.gu)) {
+                return false;
+            }
             uint8_t * p = (uint8_t *)dalloc((size_t)(dfx_device_row_bytes(wo->type, d) * d));
             if (!p || !put_matrix(wo, p, L.o)) return false;
             p = (uint8_t *)dalloc((size_t)(dfx_device_row_bytes(wd->type, F) * d));

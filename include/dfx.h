@@ -122,12 +122,24 @@ size_t dfx_gemm_ws_bytes(int64_t M, int64_t N, int64_t K);
 int dfx_gemm(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
              const float * bias, const float * residual, float * y, void * ws, void * stream);
 
+/* GEMM of a fused gate|up matrix with the SwiGLU of the FFN (src/diffuse-graph.cpp:136-139:
+ * silu(gate) * up of two ggml_mul_mat results) applied to the accumulators before they are
+ * stored.  W: device-layout [N][K] whose rows are gate and up interleaved in blocks of 16
+ * (rows 32j..32j+15 = gate rows 16j..16j+15, rows 32j+16..32j+31 = the up rows of the same
+ * indices), N = 2F a multiple of 32.  y[m][f] (row stride ldy >= F) = silu(g) * u with g, u
+ * the dfx_gemm values of gate row f and up row f (same K order, same split-K choice) and
+ * silu(x) = x / (1 + exp(-x)) as GGML's f32 silu: the same bits as dfx_gemm followed by
+ * dfx_swiglu_convert's products, without writing or reading the [M][2F] gate|up block.
+ * ws: as in dfx_gemm. */
+int dfx_gemm_swiglu(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M, float * y,
+                    int64_t ldy, void * ws, void * stream);
+
 /* Force the tile and split-K choice of the Q4_K or Q6_K GEMM for every later call in the
  * process (tuning and tests; every choice gives the same bits): "<TM>x<TN>[x<D>]" picks a
- * register tile, "s" splits K where possible, "n" never splits, "w" / "w1" pick the Q4_K
- * LDS-DMA kernel; NULL or "" restores the built-in choice.  DFX_Q4K_TILE and DFX_Q6K_TILE
- * in the environment are read once, before the first call.  No counterpart in the
- * reference (GGML has no tile choice). */
+ * register tile, "s" splits K where possible, "n" never splits, "w" / "w1" / "w3" pick the
+ * Q4_K LDS-DMA kernel (w3: 96 rows per tile); NULL or "" restores the built-in choice.
+ * DFX_Q4K_TILE and DFX_Q6K_TILE in the environment are read once, before the first call.
+ * No counterpart in the reference (GGML has no tile choice). */
 int dfx_gemm_force_tile(int wtype, const char * spec);
 
 /* dfx_gemm without a workspace argument and without any allocation: the split-K partial
@@ -238,7 +250,8 @@ int dfx_step_unmask(int N, int use_cache, int step, int32_t * seq, int32_t * pre
  * state (device int32 [4 + repeat_last_n]): [0] next token, [1] its position, [2] number
  * of recent tokens, [3] ring start, then the ring of recent tokens.  The chosen token is
  * written to state[0] and token_out[0], state[1] advances by one and the token enters
- * the ring (src/ar-sampler.cpp:236-242 keeps the last repeat_last_n tokens). */
+ * the ring (src/ar-sampler.cpp:236-242 keeps the last repeat_last_n tokens).  repeat_last_n
+ * is at most 4096 (DFX_ERR_ARG otherwise). */
 int dfx_ar_greedy(float * row, int64_t V, int32_t * state, int repeat_last_n, float repeat_penalty,
                   int32_t * token_out, void * stream);
 

@@ -235,6 +235,63 @@ def test_gemm_bias_and_residual_epilogue(gpu):
     assert np.array_equal(rb.download(np.float32, shape=(M, N)), p + res)
 
 
+def interleave16(typ, gate, up, F, K):
+    """gate|up GGML rows interleaved in blocks of 16 (the fused SwiGLU GEMM's weight order)."""
+    rb = O.row_bytes(typ, K)
+    g = np.frombuffer(gate, np.uint8).reshape(F // 16, 1, 16 * rb)
+    u = np.frombuffer(up, np.uint8).reshape(F // 16, 1, 16 * rb)
+    return np.concatenate([g, u], axis=1).reshape(-1)
+
+
+def oracle_swiglu(g, u):
+    silu = np.vectorize(lambda v: O.oracle().orc_silu(float(v)), otypes=[np.float32])
+    return silu(g) * u
+
+
+@pytest.mark.parametrize("typ,F,K,M,tile", [
+    (dfx.TYPE_Q4_K, 512, 4096, 77, None), (dfx.TYPE_Q4_K, 512, 4096, 77, "2x1x2s"),
+    (dfx.TYPE_Q4_K, 1024, 4096, 130, "w"), (dfx.TYPE_Q4_K, 1024, 4096, 130, "ws"),
+    (dfx.TYPE_Q4_K, 1024, 3584, 150, "w3"), (dfx.TYPE_Q4_K, 512, 12288, 5, "1x1x4s"),
+    (dfx.TYPE_Q4_K, 2048, 4096, 1, None), (dfx.TYPE_Q6_K, 512, 12288, 40, "2x1s"),
+    (dfx.TYPE_Q6_K, 512, 4096, 66, "2x1n"), (dfx.TYPE_Q8_0, 512, 4096, 33, None),
+    (dfx.TYPE_F16, 512, 4096, 33, None), (dfx.TYPE_F32, 256, 512, 20, None)])
+def test_gemm_swiglu_epilogue_bit_exact(gpu, typ, F, K, M, tile):
+    """dfx_gemm_swiglu on an interleaved gate|up matrix: the same bits as the plain GEMM's
+    gate and up values put through GGML's silu(gate) * up, for every tile and with split K
+    (the reduction applies the epilogue); for the integer-dot types also the oracle's
+    mul_mat values.  Padding columns of a wider output row stay untouched."""
+    gate, up = quant(typ, F, K), quant(typ, F, K)
+    W = interleave16(typ, gate, up, F, K)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    wd = to_device_weights(typ, W, 2 * F, K)
+    ldy = F + 32
+    xb, ab = dfx.Buf.of(X), dfx.Buf(L().dfx_act_bytes(typ, M, K))
+    dfx.check(L().dfx_act_convert(typ, xb.ptr, M, K, ab.ptr, None), "convert")
+    yb = dfx.Buf.of(np.full((M, ldy), 7.0, np.float32))
+    wsb = dfx.Buf(L().dfx_gemm_ws_bytes(M, 2 * F, K))
+    with forced_tile(typ, tile) if tile else contextlib.nullcontext():
+        dfx.check(L().dfx_gemm_swiglu(typ, wd.ptr, 2 * F, K, ab.ptr, M, yb.ptr, ldy, wsb.ptr, None), "swiglu")
+        plain = gpu_gemm(typ, W, 2 * F, K, X)
+    y = yb.download(np.float32, shape=(M, ldy))
+    assert np.all(y[:, F:] == 7.0)
+    pg = plain.reshape(M, F // 16, 2, 16)
+    ref = oracle_swiglu(pg[:, :, 0, :].reshape(M, F), pg[:, :, 1, :].reshape(M, F))
+    assert np.array_equal(y[:, :F].view(np.uint32), ref.view(np.uint32)), rel_l2(y[:, :F], ref)
+    if typ in (dfx.TYPE_Q4_K, dfx.TYPE_Q6_K, dfx.TYPE_Q8_0):
+        og = O.mul_mat(typ, gate, F, K, X)
+        ou = O.mul_mat(typ, up, F, K, X)
+        oref = oracle_swiglu(og, ou)
+        assert np.array_equal(y[:, :F].view(np.uint32), oref.view(np.uint32)), rel_l2(y[:, :F], oref)
+
+
+def test_gemm_swiglu_rejects_bad_shapes(gpu):
+    typ, F, K, M = dfx.TYPE_Q4_K, 256, 256, 4
+    wd = to_device_weights(typ, quant(typ, 2 * F, K), 2 * F, K)
+    ab, yb = dfx.Buf(L().dfx_act_bytes(typ, M, K)), dfx.Buf(M * F * 4)
+    assert L().dfx_gemm_swiglu(typ, wd.ptr, 2 * F - 16, K, ab.ptr, M, yb.ptr, F, None, None) != 0
+    assert L().dfx_gemm_swiglu(typ, wd.ptr, 2 * F, K, ab.ptr, M, yb.ptr, F - 1, None, None) != 0
+
+
 # ---------------------------------------------------------------- RoPE + attention
 @pytest.mark.parametrize("M,H,Hkv,hd,n_ctx", [(23, 8, 2, 128, 64), (77, 4, 4, 64, 96), (65, 28, 4, 128, 300)])
 def test_rope_store_matches_oracle(gpu, M, H, Hkv, hd, n_ctx):
