@@ -304,7 +304,7 @@ def main():
     dfx.sync()
     elapsed_prof = time.perf_counter() - t0
     prof = {t: ctx.profile_read(t) for t in (dfx.TYPE_Q4_K, dfx.TYPE_Q6_K)}
-    q4_big = ctx.profile_read(dfx.TYPE_Q4_K, 1)     # M > 96: MFMA-bound shapes (mostly k_q4k_w<1, 2>)
+    q4_big = ctx.profile_read(dfx.TYPE_Q4_K, 1)     # M > 96: MFMA-bound shapes (mostly k_q4k_w<2, 1, 2>)
     q4_small = ctx.profile_read(dfx.TYPE_Q4_K, 2)   # M <= 96: weight-bandwidth-bound shapes
     ctx.profile(False)
     ctx.close()
@@ -365,9 +365,10 @@ def main():
         "ms_per_denoise_step_cached_mean": round(float(np.mean(step_ms[1:])), 3) if len(step_ms) > 1 else None,
         "step_forward_ms": step_ms,
         "roofline": {
-            "kernel": "Q4_K GEMM calls over more than 96 rows: k_q4k_w<1, 2> (exact dequant-fused MFMA GEMM, "
-                      "LDS-DMA fed), with k_q4k<1, 1, 4> / <1, 1, 2> where the row count favours 32-row tiles; "
-                      "a split-K reduction is included when one is launched",
+            "kernel": "Q4_K GEMM calls over more than 96 rows: k_q4k_w<2, 1, 2> (exact dequant-fused MFMA GEMM, "
+                      "LDS-DMA fed, 64-row tiles; the gate|up call with SwiGLU in its epilogue), k_q4k_w<3, 1, 2> "
+                      "(96-row tiles) where that saves a round of workgroups, k_q4k<1, 1, 4> / <1, 1, 2> where the "
+                      "row count favours 32-row tiles; a split-K reduction is included when one is launched",
             "bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": committed_traffic(),
             "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
