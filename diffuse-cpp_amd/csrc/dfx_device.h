@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 #include "dfx.h"
+#include "dfx_epi.h"
 
 typedef _Float16 half_t;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -121,11 +122,6 @@ __host__ __device__ inline act_layout act_layout_of(int mode, int64_t M, int64_t
     return L;
 }
 
-// GEMM epilogues: plain (y = (v + bias) + residual), or SwiGLU over gate|up columns
-// interleaved in blocks of 32 (columns 32j + i, i < 16: gate of F-index 16j + i; i >= 16:
-// up of 16j + i - 16), written as h[m][f] = silu(gate) * up with row stride ldy.
-#define DFX_EPI_PLAIN 0
-#define DFX_EPI_SWIGLU 1
 
 // exp inside GGML ops (silu, soft_max) is taken correctly rounded: (float)exp((double)x).
 __device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }

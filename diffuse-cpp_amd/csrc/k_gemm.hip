@@ -135,6 +135,39 @@ __device__ __forceinline__ half8 to_half8(const int v[8]) {
 // Row of register r of a 32x32 MFMA tile held by `lane` (its column is lane % 32).
 __device__ __forceinline__ int tile_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
+// RoPE epilogue of one 32 x 32 tile (DFX_EPI_ROPE): v[r] is this lane's value of row
+// m0 + tile_row(r, lane) at GEMM column n, w[r] the value of the paired column n ^ 16,
+// p[r] the row's position.  The rotation is the NEOX one of ggml_rope_ext, as the RoPE
+// kernel computes it: y0 = x0 * cos - x1 * sin, y1 = x0 * sin + x1 * cos.
+__device__ __forceinline__ void rope_tile(const float (&v)[16], const float (&w)[16], const int (&p)[16], int m0,
+                                          int n, bool live, int M, int lane, const dfx_epi & epi) {
+#pragma clang fp contract(off)
+    const int hd = epi.hd, half = hd >> 1;
+    const int g = n + epi.col0, hh = g / hd, cc = g - hh * hd;
+    if (hh < epi.H + epi.Hkv) {
+        const bool first = (cc & 16) == 0;
+        const int d0 = 16 * (cc >> 5) + (cc & 15), d = first ? d0 : half + d0;
+        float2 cs[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) cs[r] = *(const float2 *)(epi.tab + ((int64_t)p[r] * half + d0) * 2);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = m0 + tile_row(r, lane);
+            if (!live || m >= M) continue;
+            const float x0 = first ? v[r] : w[r], x1 = first ? w[r] : v[r];
+            const float y = first ? x0 * cs[r].x - x1 * cs[r].y : x0 * cs[r].y + x1 * cs[r].x;
+            float * dst = hh < epi.H ? epi.q_out + ((int64_t)m * epi.H + hh) * hd
+                                     : epi.kc + ((int64_t)p[r] * epi.Hkv + (hh - epi.H)) * hd;
+            dst[d] = y;
+        }
+    } else {
+        float * col = epi.vt + ((int64_t)(hh - epi.H - epi.Hkv) * hd + cc) * epi.v_ld;
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+            if (live && m0 + tile_row(r, lane) < M) col[p[r]] = v[r];
+    }
+}
+
 // Epilogue of one 32x32 MFMA tile held by `lane`: register r is row m0 + tile_row(r, lane),
 // column n.  Every read (row map, bias, residual) is issued before any is used, at clamped
 // (always valid) addresses, so the wave waits once per kind of read rather than once per
@@ -144,9 +177,9 @@ __device__ __forceinline__ int tile_row(int r, int lane) { return 8 * (r >> 2) +
 template <typename V16>
 __device__ __forceinline__ void epilogue_tile(const V16 & acc, int m0, int n, int M, int N, const float * bias,
                                               const float * res, float * Y, int64_t ldy, const int32_t * ymap,
-                                              float * ws, int z, int lane, int epi) {
+                                              float * ws, int z, int lane, dfx_epi epi) {
 #pragma clang fp contract(off)
-    if (!ws && epi == DFX_EPI_SWIGLU) {
+    if (!ws && epi.kind == DFX_EPI_SWIGLU) {
         // lane ^ 16 holds the same rows of column n ^ 16 (n is 32j + lane % 32): a gate lane
         // and its up lane share F-index f.  The pair splits the 16 rows: the gate lane forms
         // h for registers 0..7, the up lane for registers 8..15 (rows 16 further down), each
@@ -172,6 +205,23 @@ __device__ __forceinline__ void epilogue_tile(const V16 & acc, int m0, int n, in
                 const int m = m0 + tile_row(r, lane);
                 if (m < M) ws[((int64_t)z * M + m) * N + n] = acc[r];
             }
+        return;
+    }
+    if (epi.kind == DFX_EPI_ROPE) {
+        const int nc = min(n, N - 1);
+        const float b = bias ? bias[nc] : 0.0f;
+        float v[16], w[16];
+        int p[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            v[r] = acc[r];
+            if (bias) v[r] = v[r] + b;
+            p[r] = epi.pos[min(m0 + tile_row(r, lane), M - 1)];
+        }
+        // lane ^ 16 holds the same rows of the other dim of this lane's NEOX pair
+#pragma unroll
+        for (int r = 0; r < 16; r++) w[r] = __shfl_xor(v[r], 16, WAVE);
+        rope_tile(v, w, p, m0, nc, n < N, M, lane, epi);
         return;
     }
     const int nc = min(n, N - 1);
@@ -208,7 +258,7 @@ template <int WT, int TM>
 __global__ void __launch_bounds__(256, 2)
 k_mmq(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__ act, int M,
       const float * __restrict__ bias, const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
-      int epi) {
+      dfx_epi epi) {
 #pragma clang fp contract(off)
     constexpr int BM = TM * 32, BN = 128, WSTR = wstride<WT>();
     constexpr bool KQ = WT != DFX_TYPE_Q8_0;     // Q8_K activations: d per 256, bsums per 16
@@ -496,7 +546,7 @@ template <int TM, int TN, int D>
 __global__ void __launch_bounds__(256, TM * TN >= 4 ? 1 : 2)
 k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__ act, int M,
       const float * __restrict__ bias, const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
-      int n_tiles, int m_tiles, float * __restrict__ ws, int epi) {
+      int n_tiles, int m_tiles, float * __restrict__ ws, dfx_epi epi) {
 #pragma clang fp contract(off)
     constexpr int BM = TM * 32, BN = 4 * TN * 32;
     constexpr int BST = 24;                  // LDS halves per row of 16 block sums
@@ -745,7 +795,7 @@ template <int TM, int TN, int DEPTH>
 __global__ void __launch_bounds__(256, TN == 1 ? 2 : 1)
 k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__ act, int M,
         const float * __restrict__ bias, const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
-        int n_tiles, int m_tiles, float * __restrict__ ws, int epi) {
+        int n_tiles, int m_tiles, float * __restrict__ ws, dfx_epi epi) {
 #pragma clang fp contract(off)
     constexpr int BM = 32 * TM, BN = 128 * TN, WSZ = 2048 * TN;   // WSZ: nibble bytes per wave and step
     constexpr int NA = 2 * TM;                                     // A operand copies per wave and step
@@ -1067,7 +1117,7 @@ template <int TM, int TN, int D>
 __global__ void __launch_bounds__(256, TM * TN >= 4 ? 1 : 2)
 k_q6k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__ act, int M,
       const float * __restrict__ bias, const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
-      int n_tiles, int m_tiles, float * __restrict__ ws, int epi) {
+      int n_tiles, int m_tiles, float * __restrict__ ws, dfx_epi epi) {
 #pragma clang fp contract(off)
     constexpr int BM = TM * 32, BN = 4 * TN * 32;
     constexpr int A_PER_T = BM * 16 / 256;
@@ -1260,7 +1310,7 @@ template <int TM>
 __global__ void __launch_bounds__(256, 2)
 k_gemm_f16(const uint8_t * __restrict__ W, int N, int K, const half_t * __restrict__ A, int M,
            const float * __restrict__ bias, const float * res, float * Y, int64_t ldy,
-           const int32_t * __restrict__ ymap, float * __restrict__ ws, int kt_per_split, int epi) {
+           const int32_t * __restrict__ ymap, float * __restrict__ ws, int kt_per_split, dfx_epi epi) {
     constexpr int BM = TM * 32, BN = 128, WSTR = wstride<DFX_TYPE_F16>();
     __shared__ __attribute__((aligned(16))) uint8_t Ws[BN * WSTR];
     __shared__ __attribute__((aligned(16))) half_t As[BM * ASTR];
@@ -1316,7 +1366,7 @@ template <int TM>
 __global__ void __launch_bounds__(256, 2)
 k_gemm_f32(const float * __restrict__ W, int N, int K, const float * __restrict__ A, int M,
            const float * __restrict__ bias, const float * res, float * Y, int64_t ldy,
-           const int32_t * __restrict__ ymap, int epi) {
+           const int32_t * __restrict__ ymap, dfx_epi epi) {
     constexpr int BM = TM * 32, BN = 128;
     __shared__ float Ws[BN * FSTR];
     __shared__ float As[BM * FSTR];
@@ -1378,10 +1428,10 @@ k_gemm_f32(const float * __restrict__ W, int N, int K, const float * __restrict_
 #define REDUCE_R 4
 __global__ void k_gemm_reduce(const float * __restrict__ ws, int S, int64_t MN, int N, const float * bias,
                               const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
-                              int epi) {
+                              dfx_epi epi) {
 #pragma clang fp contract(off)
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    if (epi == DFX_EPI_SWIGLU) {
+    if (epi.kind == DFX_EPI_SWIGLU) {
         // one output h[m][f] per element: gate and up column sums (slice order), then silu * up
         const int F = N / 2;
         const int64_t MF = MN / 2;
@@ -1395,6 +1445,38 @@ __global__ void k_gemm_reduce(const float * __restrict__ ws, int S, int64_t MN, 
                 u = u + ws[(int64_t)s * MN + cg + 16];
             }
             Y[m * ldy + f] = silu_mul(g, u);
+        }
+        return;
+    }
+    if (epi.kind == DFX_EPI_ROPE) {
+        // one element per thread: its chunk sums and its pair partner's (column n ^ 16)
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < MN; i += stride) {
+            const int64_t m = i / N;
+            const int n = (int)(i - m * N), np = n ^ 16;
+            float v = 0.0f, w = 0.0f;
+            for (int s = 0; s < S; s++) {
+                v = v + ws[(int64_t)s * MN + m * N + n];
+                w = w + ws[(int64_t)s * MN + m * N + np];
+            }
+            if (bias) {
+                v = v + bias[n];
+                w = w + bias[np];
+            }
+            const int p = epi.pos[m];
+            const int hd = epi.hd, half = hd >> 1;
+            const int g = n + epi.col0, hh = g / hd, cc = g - hh * hd;
+            if (hh < epi.H + epi.Hkv) {
+                const bool first = (cc & 16) == 0;
+                const int d0 = 16 * (cc >> 5) + (cc & 15), d = first ? d0 : half + d0;
+                const float2 cs = *(const float2 *)(epi.tab + ((int64_t)p * half + d0) * 2);
+                const float x0 = first ? v : w, x1 = first ? w : v;
+                const float y = first ? x0 * cs.x - x1 * cs.y : x0 * cs.y + x1 * cs.x;
+                float * dst = hh < epi.H ? epi.q_out + (m * epi.H + hh) * hd
+                                         : epi.kc + ((int64_t)p * epi.Hkv + (hh - epi.H)) * hd;
+                dst[d] = y;
+            } else {
+                epi.vt[((int64_t)(hh - epi.H - epi.Hkv) * hd + cc) * epi.v_ld + p] = v;
+            }
         }
         return;
     }
@@ -1505,7 +1587,7 @@ extern "C" size_t dfx_gemm_ws_bytes(int64_t M, int64_t N, int64_t K) {
 // into Y, or, with defer, leaves the slices for the consumer of Y (the next RMSNorm,
 // which then adds them and the residual itself) and reports S.
 static int reduce_or_defer(const void * ws, int S, int M, int N, const float * bias, const float * res, float * y,
-                           int64_t ldy, const int32_t * ymap, hipStream_t st, int * defer, int epi) {
+                           int64_t ldy, const int32_t * ymap, hipStream_t st, int * defer, dfx_epi epi) {
     if (defer) {
         *defer = S;
         return DFX_OK;
@@ -1521,7 +1603,7 @@ static int reduce_or_defer(const void * ws, int S, int M, int N, const float * b
 template <int TM>
 static int launch_f16(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                       float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer,
-                      int epi) {
+                      dfx_epi epi) {
     constexpr int BM = TM * 32, BN = 128;
     const int gx = (N + BN - 1) / BN, gy = (M + BM - 1) / BM;
     const int n_kt = K / BK;
@@ -1545,7 +1627,7 @@ static int launch_f16(const void * w, int N, int K, const void * act, int M, con
 
 template <int TM>
 static int launch_f32(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                      float * y, int64_t ldy, const int32_t * ymap, hipStream_t st, int epi) {
+                      float * y, int64_t ldy, const int32_t * ymap, hipStream_t st, dfx_epi epi) {
     const dim3 grid((N + 127) / 128, (M + 32 * TM - 1) / (32 * TM));
     hipLaunchKernelGGL((k_gemm_f32<TM>), grid, dim3(256), 0, st, (const float *)w, N, K, (const float *)act, M, bias,
                        res, y, ldy, ymap, epi);
@@ -1555,7 +1637,7 @@ static int launch_f32(const void * w, int N, int K, const void * act, int M, con
 
 template <int WT, int TM>
 static int launch_mmq(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                      float * y, int64_t ldy, const int32_t * ymap, hipStream_t st, int epi) {
+                      float * y, int64_t ldy, const int32_t * ymap, hipStream_t st, dfx_epi epi) {
     constexpr int BM = TM * 32, BN = 128;
     const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
     hipLaunchKernelGGL((k_mmq<WT, TM>), grid, dim3(256), 0, st, (const uint8_t *)w, N, K, (const uint8_t *)act, M,
@@ -1567,7 +1649,7 @@ static int launch_mmq(const void * w, int N, int K, const void * act, int M, con
 template <int TM, int TN, int D>
 static int launch_q4k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                       float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st, int * defer,
-                      int epi) {
+                      dfx_epi epi) {
     constexpr int BM = TM * 32, BN = 4 * TN * 32;
     const int n_tiles = (N + BN - 1) / BN, m_tiles = (M + BM - 1) / BM;
     const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
@@ -1590,7 +1672,7 @@ static int launch_q4k(const void * w, int N, int K, const void * act, int M, con
 template <int TM, int TN, int DEPTH>
 static int launch_q4k_w(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                         float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st, int * defer,
-                      int epi) {
+                      dfx_epi epi) {
     const int n_tiles = (N + 128 * TN - 1) / (128 * TN), m_tiles = (M + 32 * TM - 1) / (32 * TM);
     const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
     const int chunks = dot_chunks(K), passes = ws ? chunks : 1;
@@ -1609,7 +1691,7 @@ static int launch_q4k_w(const void * w, int N, int K, const void * act, int M, c
 template <int TM, int TN, int D>
 static int launch_q6k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                       float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st, int * defer,
-                      int epi) {
+                      dfx_epi epi) {
     constexpr int BM = TM * 32, BN = 4 * TN * 32;
     const int n_tiles = (N + BN - 1) / BN, m_tiles = (M + BM - 1) / BM;
     const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
@@ -1630,7 +1712,7 @@ static int launch_q6k(const void * w, int N, int K, const void * act, int M, con
 // A forced tile "<TM>x<TN>[x<D>][s|n]" (dfx_gemm_force_tile) overrides the choice.
 static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                         float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer,
-                        int epi) {
+                        dfx_epi epi) {
     int tm = M > 48 ? 2 : 1, tn = 1;
     const int chunks = dot_chunks(K);
     const int64_t tiles = (int64_t)((M + 32 * tm - 1) / (32 * tm)) * ((N + 128 * tn - 1) / (128 * tn));
@@ -1658,7 +1740,7 @@ static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, c
 // borders (workspace permitting).
 static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                         float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer,
-                        int epi) {
+                        dfx_epi epi) {
     struct cand { int tm, tn, d; };
     // (a 96-row tile, TM = 3, spills its sums at two workgroups per CU and is not built)
     static const cand cands[] = {{2, 2, 2}, {4, 1, 2}, {2, 1, 2}, {1, 2, 2}, {1, 1, 4}, {1, 1, 2}, {2, 1, 4}, {2, 2, 4}};
@@ -1771,7 +1853,7 @@ static int pick_tm(int M, int max_tm) {
 // MI355X: 2-5x slower with 64 or 96 rows per workgroup at M = 96..768).
 template <int WT>
 static int dispatch_mmq(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
-                        float * y, int64_t ldy, const int32_t * ymap, hipStream_t st, int epi) {
+                        float * y, int64_t ldy, const int32_t * ymap, hipStream_t st, dfx_epi epi) {
     return launch_mmq<WT, 1>(w, N, K, act, M, bias, res, y, ldy, ymap, st, epi);
 }
 
@@ -1780,18 +1862,34 @@ static int dispatch_mmq(const void * w, int N, int K, const void * act, int M, c
 // is large enough.
 int dfx_gemm_ex(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
                 const float * bias, const float * residual, float * y, int64_t ldy, const int32_t * ymap,
-                void * ws, size_t ws_bytes, void * stream, int * n_partials, int epi) {
+                void * ws, size_t ws_bytes, void * stream, int * n_partials, const dfx_epi * epi_p) {
     // n_partials: if K gets split, leave the partial slices ws[s][m][n] for the caller
     // to add (calls without bias or row map, ldy = N) and report their number; 0 = Y
     // was written
     if (n_partials) *n_partials = 0;
-    if (epi != DFX_EPI_PLAIN && (epi != DFX_EPI_SWIGLU || bias || residual || ymap || N % 32)) {
+    dfx_epi epi{};
+    if (epi_p) epi = *epi_p;
+    if (epi.kind == DFX_EPI_SWIGLU && (bias || residual || ymap || N % 32)) {
         dfx_set_error("dfx_gemm: the SwiGLU epilogue takes N a multiple of 32, no bias, residual or row map");
         return DFX_ERR_ARG;
     }
-    int * defer = n_partials && !bias && !ymap && ldy == N && epi == DFX_EPI_PLAIN ? n_partials : nullptr;
+    if (epi.kind == DFX_EPI_ROPE) {
+        const int64_t width = ((int64_t)epi.H + 2 * (int64_t)epi.Hkv) * epi.hd;
+        if (residual || ymap || N % 32 || epi.H <= 0 || epi.Hkv <= 0 || epi.H % epi.Hkv || epi.hd <= 0 ||
+            epi.hd % 32 || epi.col0 < 0 || epi.col0 % 32 || epi.col0 + N > width || !epi.pos || !epi.tab ||
+            !epi.q_out || !epi.kc || !epi.vt || epi.v_ld <= 0) {
+            dfx_set_error("dfx_gemm: bad RoPE epilogue (N=%lld col0=%d H=%d Hkv=%d hd=%d; no residual or row map)",
+                          (long long)N, epi.col0, epi.H, epi.Hkv, epi.hd);
+            return DFX_ERR_ARG;
+        }
+        ldy = N;   // Y is not written
+    } else if (epi.kind != DFX_EPI_PLAIN && epi.kind != DFX_EPI_SWIGLU) {
+        dfx_set_error("dfx_gemm: unknown epilogue %d", epi.kind);
+        return DFX_ERR_ARG;
+    }
+    int * defer = n_partials && !bias && !ymap && ldy == N && epi.kind == DFX_EPI_PLAIN ? n_partials : nullptr;
     if (N <= 0 || K <= 0 || M < 0 || (K % 256) || N > INT32_MAX || M > INT32_MAX || K > INT32_MAX ||
-        ldy < (epi == DFX_EPI_SWIGLU ? N / 2 : N)) {
+        ldy < (epi.kind == DFX_EPI_SWIGLU ? N / 2 : N)) {
         dfx_set_error("dfx_gemm: bad shape M=%lld N=%lld K=%lld ldy=%lld (K must be a multiple of 256)",
                       (long long)M, (long long)N, (long long)K, (long long)ldy);
         return DFX_ERR_ARG;
@@ -1821,13 +1919,35 @@ int dfx_gemm_ex(int wtype, const void * w, int64_t N, int64_t K, const void * ac
 extern "C" int dfx_gemm(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
                         const float * bias, const float * residual, float * y, void * ws, void * stream) {
     return dfx_gemm_ex(wtype, w, N, K, act, M, bias, residual, y, N, nullptr, ws,
-                       ws ? dfx_gemm_ws_bytes(M, N, K) : 0, stream, nullptr, DFX_EPI_PLAIN);
+                       ws ? dfx_gemm_ws_bytes(M, N, K) : 0, stream, nullptr, nullptr);
 }
 
 extern "C" int dfx_gemm_swiglu(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
                                float * y, int64_t ldy, void * ws, void * stream) {
+    dfx_epi e{};
+    e.kind = DFX_EPI_SWIGLU;
     return dfx_gemm_ex(wtype, w, N, K, act, M, nullptr, nullptr, y, ldy, nullptr, ws,
-                       ws ? dfx_gemm_ws_bytes(M, N, K) : 0, stream, nullptr, DFX_EPI_SWIGLU);
+                       ws ? dfx_gemm_ws_bytes(M, N, K) : 0, stream, nullptr, &e);
+}
+
+extern "C" int dfx_gemm_rope(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
+                             const float * bias, int col0, const int32_t * pos, int H, int Hkv, int hd,
+                             const float * tab, float * q_out, float * kc, float * vt, int64_t v_ld, void * ws,
+                             void * stream) {
+    dfx_epi e{};
+    e.kind = DFX_EPI_ROPE;
+    e.col0 = col0;
+    e.H = H;
+    e.Hkv = Hkv;
+    e.hd = hd;
+    e.pos = pos;
+    e.tab = tab;
+    e.q_out = q_out;
+    e.kc = kc;
+    e.vt = vt;
+    e.v_ld = v_ld;
+    return dfx_gemm_ex(wtype, w, N, K, act, M, bias, nullptr, nullptr, N, nullptr, ws,
+                       ws ? dfx_gemm_ws_bytes(M, N, K) : 0, stream, nullptr, &e);
 }
 
 // ---------------------------------------------------------------------------
@@ -1877,5 +1997,5 @@ extern "C" int dfx_gemm_noalloc(int wtype, const void * w, int64_t N, int64_t K,
     // the same workspace size as dfx_gemm's (when it fits), so the same split is chosen
     const size_t ws_bytes = std::min<size_t>(dfx_gemm_ws_bytes(M, N, K), DFX_GEMM_SCRATCH_BYTES);
     return dfx_gemm_ex(wtype, w, N, K, act, M, bias, residual, y, N, nullptr, scratch_ptr[dev], ws_bytes, stream,
-                       nullptr, DFX_EPI_PLAIN);
+                       nullptr, nullptr);
 }

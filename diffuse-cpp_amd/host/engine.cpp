@@ -164,7 +164,7 @@ hipEvent_t take_event(diffuse_context * c) {
 // for the next RMSNorm to add.
 int gemm(diffuse_context * c, const dev_matrix & w, int64_t N, int64_t K, int64_t M, const float * bias,
          const float * res, float * y, int64_t ldy, const int32_t * ymap, bool split_ok, int * n_partials = nullptr,
-         int epi = DFX_EPI_PLAIN) {
+         const dfx_epi * epi = nullptr) {
     void * ws = split_ok ? c->ws : nullptr;
     const size_t wsb = split_ok ? c->ws_bytes : 0;
     if (n_partials) *n_partials = 0;
@@ -178,7 +178,7 @@ int gemm(diffuse_context * c, const dev_matrix & w, int64_t N, int64_t K, int64_
     r.M = M;
     r.flops = 2.0 * (double)M * N * K;
     r.bytes = (double)dfx_device_row_bytes(w.type, K) * N + (double)M * K * 2 +
-              (double)M * N * (epi == DFX_EPI_SWIGLU ? 2 : 4);
+              (double)M * N * (epi && epi->kind == DFX_EPI_SWIGLU ? 2 : 4);
     if (!r.a || !r.b) return hip_ok(hipErrorOutOfMemory, "hipEventCreate");
     TRY(hip_ok(hipEventRecord(r.a, c->stream), "event"));
     TRY(dfx_gemm_ex(w.type, w.data, N, K, c->act, M, bias, res, y, ldy, ymap, ws, wsb, c->stream, n_partials, epi));
@@ -209,7 +209,7 @@ void prof_collect(diffuse_context * c) {
 // RMSNorm of x + conversion, then the group's GEMM(s).  `pending` split-K partial sums of
 // the GEMM that produced x (left in c->ws) are added to x by the first RMSNorm.
 int run_group(diffuse_context * c, const proj_group & g, const float * norm, int64_t M, int64_t K, float * out,
-              int & pending) {
+              int & pending, const dfx_epi * rope = nullptr) {
     const float eps = c->model->hparams.rms_norm_eps;
     auto norm_convert = [&](int type) -> int {
         if (pending == 0) return dfx_rmsnorm_convert_ex(type, c->x, nullptr, norm, M, K, eps, c->act, c->stream);
@@ -220,8 +220,13 @@ int run_group(diffuse_context * c, const proj_group & g, const float * norm, int
     };
     if (g.swiglu) {   // out[M][n_out / 2] = silu(gate) * up
         TRY(norm_convert(g.all.type));
-        return gemm(c, g.all, g.n_out, K, M, nullptr, nullptr, out, g.n_out / 2, nullptr, true, nullptr,
-                    DFX_EPI_SWIGLU);
+        dfx_epi e{};
+        e.kind = DFX_EPI_SWIGLU;
+        return gemm(c, g.all, g.n_out, K, M, nullptr, nullptr, out, g.n_out / 2, nullptr, true, nullptr, &e);
+    }
+    if (rope) {       // Q|K|V rotated and stored by the GEMM's epilogue (rows permuted at load)
+        TRY(norm_convert(g.all.type));
+        return gemm(c, g.all, g.n_out, K, M, g.bias, nullptr, nullptr, g.n_out, nullptr, true, nullptr, rope);
     }
     if (g.fused) {
         TRY(norm_convert(g.all.type));
@@ -258,9 +263,24 @@ int forward_layers(diffuse_context * c, int M, int n_keys, const pass_opts & o, 
         if (o.impact_rows)
             TRY(hip_ok(hipMemcpyAsync(c->x_prev, c->x, (size_t)M * D.d * 4, hipMemcpyDeviceToDevice, c->stream),
                        "layer input copy"));
-        TRY(run_group(c, L.qkv, L.attn_norm, M, D.d, c->qkv, pending));
-        TRY(dfx_rope_store(c->qkv, pos, M, (int)D.H, (int)D.Hkv, (int)D.hd, c->rope_tab, c->qr, kc, vc, c->cap,
-                           c->stream));
+        if (L.qkv.rope) {
+            dfx_epi e{};
+            e.kind = DFX_EPI_ROPE;
+            e.H = (int)D.H;
+            e.Hkv = (int)D.Hkv;
+            e.hd = (int)D.hd;
+            e.pos = pos;
+            e.tab = c->rope_tab;
+            e.q_out = c->qr;
+            e.kc = kc;
+            e.vt = vc;
+            e.v_ld = c->cap;
+            TRY(run_group(c, L.qkv, L.attn_norm, M, D.d, nullptr, pending, &e));
+        } else {
+            TRY(run_group(c, L.qkv, L.attn_norm, M, D.d, c->qkv, pending));
+            TRY(dfx_rope_store(c->qkv, pos, M, (int)D.H, (int)D.Hkv, (int)D.hd, c->rope_tab, c->qr, kc, vc, c->cap,
+                               c->stream));
+        }
         if (o.q_pos0 >= 0)
             TRY(dfx_attention_causal(c->qr, kc, vc, c->cap, M, n_keys, (int)D.H, (int)D.Hkv, (int)D.hd, o.q_pos0,
                                      o.window, c->att, c->stream));

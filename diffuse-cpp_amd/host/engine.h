@@ -8,20 +8,19 @@
 #include <vector>
 
 #include "dfx.h"
+#include "dfx_epi.h"
 #include "diffuse.h"
 
 #define DIFFUSE_LOG(fmt, ...) fprintf(stderr, "[diffuse] " fmt "\n", ##__VA_ARGS__)
 
-// GEMM epilogues (the same values as in the device header csrc/dfx_device.h)
-#define DFX_EPI_PLAIN 0
-#define DFX_EPI_SWIGLU 1
-
 // Internal kernel entry points with row maps (k_gemm.hip, k_quant.hip, k_sampler.hip).
-// epi: DFX_EPI_PLAIN, or DFX_EPI_SWIGLU (gate|up rows interleaved in blocks of 16: y[m][f] =
-// silu(gate) * up with row stride ldy >= N / 2; no bias, residual or row map).
+// epi: null (plain), DFX_EPI_SWIGLU (gate|up rows interleaved in blocks of 16: y[m][f] =
+// silu(gate) * up with row stride ldy >= N / 2; no bias, residual or row map) or DFX_EPI_ROPE
+// (Q|K|V columns rotated and stored into q_out and the caches; bias allowed, no residual, row
+// map or y).
 int dfx_gemm_ex(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M, const float * bias,
                 const float * residual, float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes,
-                void * stream, int * n_partials, int epi = DFX_EPI_PLAIN);
+                void * stream, int * n_partials, const dfx_epi * epi = nullptr);
 int dfx_rmsnorm_convert_ex(int wtype, const float * x, const int32_t * xmap, const float * w, int64_t M, int64_t K,
                            float eps, void * act, void * stream);
 // RMSNorm + conversion of x after adding a deferred split-K result: row r (= xmap[m] or m)
@@ -52,6 +51,10 @@ struct proj_group {
     // gate|up fused with rows interleaved in blocks of 16 (16 gate rows, then the 16 up rows
     // of the same F-indices): its GEMM applies SwiGLU in the epilogue (DFX_EPI_SWIGLU)
     bool                    swiglu = false;
+    // Q|K|V fused with the rows of every Q and K head permuted in blocks of 32 (16 dims of the
+    // first half, then the 16 dims hd/2 later that they rotate with): its GEMM applies RoPE and
+    // stores Q and the K/V cache in the epilogue (DFX_EPI_ROPE)
+    bool                    rope = false;
 };
 
 struct dev_layer {

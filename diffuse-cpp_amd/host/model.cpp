@@ -162,6 +162,61 @@ struct loader {
         return true;
     }
 
+    // Q|K|V (one device type; head size hd a multiple of 32) stacked into one matrix with the
+    // rows of every Q and K head permuted: row 32j + i of a head is dim 16j + i (i < 16) or
+    // dim hd/2 + 16j + i - 16 (i >= 16), so that one 32-column tile of the GEMM holds both
+    // dims of 16 NEOX pairs and its epilogue can rotate them.  Biases follow the rows.
+    bool rope_group(const gguf::tensor_info * wq, const gguf::tensor_info * wk, const gguf::tensor_info * wv,
+                    const gguf::tensor_info * bq, const gguf::tensor_info * bk, const gguf::tensor_info * bv,
+                    int64_t hd, proj_group & g) {
+        const int64_t K = wq->ne[0];
+        const int64_t drb = dfx_device_row_bytes(wq->type, K);
+        const int64_t nq = wq->ne[1], nk = wk->ne[1], nv = wv->ne[1], n = nq + nk + nv;
+        std::vector<uint8_t> plain((size_t)(drb * n)), both((size_t)(drb * n));
+        if (dfx_repack_rows(wq->type, wq->data, nq, K, plain.data()) != DFX_OK ||
+            dfx_repack_rows(wk->type, wk->data, nk, K, plain.data() + (size_t)(drb * nq)) != DFX_OK ||
+            dfx_repack_rows(wv->type, wv->data, nv, K, plain.data() + (size_t)(drb * (nq + nk))) != DFX_OK) {
+            err = dfx_last_error();
+            return false;
+        }
+        // source row of every device row
+        std::vector<int64_t> src((size_t)n);
+        for (int64_t r = 0; r < n; r++) {
+            if (r >= nq + nk) {
+                src[(size_t)r] = r;
+                continue;
+            }
+            const int64_t head = r / hd, i = r % hd, j = i / 32, c = i % 32;
+            src[(size_t)r] = head * hd + (c < 16 ? 16 * j + c : hd / 2 + 16 * j + c - 16);
+        }
+        for (int64_t r = 0; r < n; r++)
+            memcpy(both.data() + (size_t)(r * drb), plain.data() + (size_t)(src[(size_t)r] * drb), (size_t)drb);
+        uint8_t * base = (uint8_t *)dalloc(both.size());
+        if (!base || !upload(base, both.data(), both.size())) return false;
+        g.all.type = dfx_device_type(wq->type);
+        g.all.rows = n;
+        g.all.cols = K;
+        g.all.data = base;
+        g.n_out = n;   // parts stay empty: the rows are not in Q|K|V order
+        g.fused = true;
+        g.rope = true;
+        if (bq || bk || bv) {
+            std::vector<float> bias((size_t)n, 0.0f), perm((size_t)n);
+            const gguf::tensor_info * bs[3] = {bq, bk, bv};
+            const int64_t off[3] = {0, nq, nq + nk}, rows[3] = {nq, nk, nv};
+            for (int i = 0; i < 3; i++) {
+                if (!bs[i]) continue;
+                std::vector<float> v;
+                if (!to_f32(bs[i], rows[i], v)) return false;
+                memcpy(bias.data() + off[i], v.data(), v.size() * 4);
+            }
+            for (int64_t r = 0; r < n; r++) perm[(size_t)r] = bias[(size_t)src[(size_t)r]];
+            g.bias = (float *)dalloc(perm.size() * 4);
+            if (!g.bias || !upload(g.bias, perm.data(), perm.size() * 4)) return false;
+        }
+        return true;
+    }
+
     bool group(const std::vector<const gguf::tensor_info *> & ts, const std::vector<const gguf::tensor_info *> & biases,
                proj_group & g) {
         size_t total = 0;
@@ -295,7 +350,12 @@ struct loader {
                 !check_matrix(wo, d, d) || !check_matrix(wg, d, F) || !check_matrix(wu, d, F) || !check_matrix(wd, F, d))
                 return false;
             if (!(L.attn_norm = vec_f32(an, d)) || !(L.ffn_norm = vec_f32(fn, d))) return false;
-            if (!group({wq, wk, wv}, {bq, bk, bv}, L.qkv)) return false;
+            const int dq = dfx_device_type(wq->type);
+            if (dq == dfx_device_type(wk->type) && dq == dfx_device_type(wv->type) && hd % 32 == 0) {
+                if (!rope_group(wq, wk, wv, bq, bk, bv, hd, L.qkv)) return false;
+            } else if (!group({wq, wk, wv}, {bq, bk, bv}, L.qkv)) {
+                return false;
+            }
             if (dfx_device_type(wg->type) == dfx_device_type(wu->type) && wg->ne[1] % 16 == 0) {
                 if (!swiglu_group(wg, wu, L.gu)) return false;
             } else if (!group({wg, wu}, {nullptr, nullptr}, L.gu)) {

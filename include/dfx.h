@@ -134,6 +134,20 @@ int dfx_gemm(int wtype, const void * w, int64_t N, int64_t K, const void * act, 
 int dfx_gemm_swiglu(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M, float * y,
                     int64_t ldy, void * ws, void * stream);
 
+/* GEMM of a fused Q|K|V matrix with the NEOX RoPE and the cache store of dfx_rope_store
+ * (src/diffuse-graph.cpp:61-79, 466-469: the Q/K/V projections, their biases and
+ * ggml_rope_ext) applied to the accumulators: no [M][(H + 2 Hkv) hd] block is written.
+ * W: device-layout [N][K], a slice of the Q|K|V layout starting at column col0 (a multiple of
+ * 32), in which the rows of every Q and K head are permuted in blocks of 32: rows 32j..32j+15
+ * of a head are its dims 16j..16j+15 and rows 32j+16..32j+31 the dims hd/2 + 16j.. they rotate
+ * with (hd a multiple of 32); V rows are in order.  bias (or NULL) follows W's rows.  The
+ * rotated rows are stored as dfx_rope_store stores them: q_out [M][H][hd], kc[pos][Hkv][hd],
+ * vt[Hkv][hd][v_ld] at column pos[m]; the same bits as dfx_gemm (+bias) followed by
+ * dfx_rope_store on the unpermuted rows.  ws: as in dfx_gemm. */
+int dfx_gemm_rope(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M, const float * bias,
+                  int col0, const int32_t * pos, int H, int Hkv, int hd, const float * tab, float * q_out,
+                  float * kc, float * vt, int64_t v_ld, void * ws, void * stream);
+
 /* Force the tile and split-K choice of the Q4_K or Q6_K GEMM for every later call in the
  * process (tuning and tests; every choice gives the same bits): "<TM>x<TN>[x<D>]" picks a
  * register tile, "s" splits K where possible, "n" never splits, "w" / "w1" / "w3" pick the

@@ -292,6 +292,107 @@ def test_gemm_swiglu_rejects_bad_shapes(gpu):
     assert L().dfx_gemm_swiglu(typ, wd.ptr, 2 * F, K, ab.ptr, M, yb.ptr, F - 1, None, None) != 0
 
 
+def rope_row_order(H, Hkv, hd):
+    """Device row order of the fused RoPE GEMM: in each Q and K head, blocks of 32 rows hold
+    dims 16j..16j+15 and then hd/2 + 16j..; V rows stay in order."""
+    src = []
+    for r in range((H + 2 * Hkv) * hd):
+        if r >= (H + Hkv) * hd:
+            src.append(r)
+            continue
+        head, i = divmod(r, hd)
+        j, c = divmod(i, 32)
+        src.append(head * hd + (16 * j + c if c < 16 else hd // 2 + 16 * j + c - 16))
+    return np.array(src)
+
+
+@pytest.mark.parametrize("typ,H,Hkv,hd,K,M,tile,bias", [
+    (dfx.TYPE_Q4_K, 8, 2, 128, 2048, 77, None, False), (dfx.TYPE_Q4_K, 8, 8, 128, 4096, 130, "w", True),
+    (dfx.TYPE_Q4_K, 4, 4, 128, 4096, 150, "w3", False), (dfx.TYPE_Q4_K, 6, 2, 64, 4096, 40, "2x1x2s", True),
+    (dfx.TYPE_Q4_K, 4, 2, 128, 4096, 200, "ws", False), (dfx.TYPE_Q4_K, 8, 8, 128, 4096, 3, None, False),
+    (dfx.TYPE_Q6_K, 4, 2, 128, 4096, 66, "2x1s", True), (dfx.TYPE_Q6_K, 4, 4, 64, 2048, 100, "2x1n", False),
+    (dfx.TYPE_Q8_0, 4, 2, 128, 2048, 33, None, True), (dfx.TYPE_F16, 4, 1, 128, 2048, 45, None, True),
+    (dfx.TYPE_F32, 2, 1, 64, 512, 20, None, False)])
+def test_gemm_rope_epilogue_bit_exact(gpu, typ, H, Hkv, hd, K, M, tile, bias):
+    """dfx_gemm_rope on the row-permuted Q|K|V matrix stores the same q, K-cache and
+    transposed V-cache bits as dfx_gemm (+bias) on the unpermuted matrix followed by
+    dfx_rope_store, for every tile, with split K (the reduction applies the epilogue), and
+    when Q and K|V are two calls (col0); cache positions outside pos stay untouched."""
+    N = (H + 2 * Hkv) * hd
+    n_ctx = M + 37
+    raw = quant(typ, N, K)
+    rb = O.row_bytes(typ, K)
+    order = rope_row_order(H, Hkv, hd)
+    perm = np.frombuffer(raw, np.uint8).reshape(N, rb)[order].reshape(-1)
+    b = rng.standard_normal(N).astype(np.float32) if bias else None
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    pos = rng.permutation(n_ctx)[:M].astype(np.int32)
+    tab = O.rope_table(n_ctx, hd, 500000.0)
+    xb, ab = dfx.Buf.of(X), dfx.Buf(L().dfx_act_bytes(typ, M, K))
+    dfx.check(L().dfx_act_convert(typ, xb.ptr, M, K, ab.ptr, None), "convert")
+    pb, tb = dfx.Buf.of(pos), dfx.Buf.of(tab)
+    ws = dfx.Buf(L().dfx_gemm_ws_bytes(M, N, K))
+
+    def outputs():
+        q, k, v = dfx.Buf(M * H * hd * 4), dfx.Buf(n_ctx * Hkv * hd * 4), dfx.Buf(n_ctx * Hkv * hd * 4)
+        k.upload(np.full(n_ctx * Hkv * hd, 5.0, np.float32))
+        v.upload(np.full(n_ctx * Hkv * hd, 5.0, np.float32))
+        return q, k, v
+
+    def fetch(q, k, v):
+        return (q.download(np.float32, shape=(M, H, hd)), k.download(np.float32, shape=(n_ctx, Hkv, hd)),
+                v.download(np.float32, shape=(Hkv, hd, n_ctx)))
+
+    with forced_tile(typ, tile) if tile else contextlib.nullcontext():
+        # reference: plain GEMM (+bias) on the unpermuted rows, then the RoPE kernel
+        wd = to_device_weights(typ, raw, N, K)
+        yb = dfx.Buf(M * N * 4)
+        bb = dfx.Buf.of(b) if bias else None
+        dfx.check(L().dfx_gemm(typ, wd.ptr, N, K, ab.ptr, M, bb.ptr if bias else None, None, yb.ptr, ws.ptr, None),
+                  "gemm")
+        r = outputs()
+        dfx.check(L().dfx_rope_store(yb.ptr, pb.ptr, M, H, Hkv, hd, tb.ptr, r[0].ptr, r[1].ptr, r[2].ptr, n_ctx,
+                                     None), "rope")
+        ref = fetch(*r)
+        # fused, one call
+        wp = to_device_weights(typ, perm, N, K)
+        pbias = dfx.Buf.of(b[order]) if bias else None
+        g = outputs()
+        dfx.check(L().dfx_gemm_rope(typ, wp.ptr, N, K, ab.ptr, M, pbias.ptr if bias else None, 0, pb.ptr, H, Hkv, hd,
+                                    tb.ptr, g[0].ptr, g[1].ptr, g[2].ptr, n_ctx, ws.ptr, None), "gemm_rope")
+        got = fetch(*g)
+        # fused, Q and K|V as two calls over row slices of the same matrix
+        nq = H * hd
+        wq = to_device_weights(typ, perm[:nq * rb], nq, K)
+        wkv = to_device_weights(typ, perm[nq * rb:], N - nq, K)
+        bq = dfx.Buf.of(b[order][:nq]) if bias else None
+        bkv = dfx.Buf.of(b[order][nq:]) if bias else None
+        h = outputs()
+        dfx.check(L().dfx_gemm_rope(typ, wq.ptr, nq, K, ab.ptr, M, bq.ptr if bias else None, 0, pb.ptr, H, Hkv, hd,
+                                    tb.ptr, h[0].ptr, h[1].ptr, h[2].ptr, n_ctx, ws.ptr, None), "gemm_rope q")
+        dfx.check(L().dfx_gemm_rope(typ, wkv.ptr, N - nq, K, ab.ptr, M, bkv.ptr if bias else None, nq, pb.ptr, H,
+                                    Hkv, hd, tb.ptr, h[0].ptr, h[1].ptr, h[2].ptr, n_ctx, ws.ptr, None), "gemm_rope kv")
+        two = fetch(*h)
+    for a, e in ((got, ref), (two, ref)):
+        for x, y in zip(a, e):
+            assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+    untouched = np.setdiff1d(np.arange(n_ctx), pos)
+    assert np.all(got[1][untouched] == 5.0) and np.all(got[2][:, :, untouched] == 5.0)
+
+
+def test_gemm_rope_rejects_bad_arguments(gpu):
+    typ, H, Hkv, hd, K, M = dfx.TYPE_Q4_K, 2, 1, 128, 256, 4
+    N = (H + 2 * Hkv) * hd
+    wd = to_device_weights(typ, quant(typ, N, K), N, K)
+    ab, pb, tb = dfx.Buf(L().dfx_act_bytes(typ, M, K)), dfx.Buf(M * 4), dfx.Buf(64 * hd * 4)
+    q, k, v = dfx.Buf(M * H * hd * 4), dfx.Buf(64 * Hkv * hd * 4), dfx.Buf(64 * Hkv * hd * 4)
+    ok = (typ, wd.ptr, N, K, ab.ptr, M, None, 0, pb.ptr, H, Hkv, hd, tb.ptr, q.ptr, k.ptr, v.ptr, 64, None, None)
+    for i, bad in ((7, 16), (7, 32), (11, 48), (10, 3), (15, None), (2, N - 16)):
+        args = list(ok)
+        args[i] = bad
+        assert L().dfx_gemm_rope(*args) != 0, (i, bad)
+
+
 # ---------------------------------------------------------------- RoPE + attention
 @pytest.mark.parametrize("M,H,Hkv,hd,n_ctx", [(23, 8, 2, 128, 64), (77, 4, 4, 64, 96), (65, 28, 4, 128, 300)])
 def test_rope_store_matches_oracle(gpu, M, H, Hkv, hd, n_ctx):
