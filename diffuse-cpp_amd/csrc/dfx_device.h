@@ -105,8 +105,11 @@ __host__ __device__ inline int64_t act_frag_off(int64_t m, int64_t sl, int64_t K
 
 // The d of the permuted modes is stored super-block major, d[K/256][ceil(M/32)*32]
 // (the scales of consecutive rows of one super-block are adjacent).
+// With at most DFX_GEMV_M rows, the permuted modes also keep the int8 quants in natural
+// order, i8 [M][K], for the matrix-vector kernels (integer dot products).
+#define DFX_GEMV_M 4
 struct act_layout {
-    size_t q, d, bs, bytes;
+    size_t q, d, bs, i8, bytes;   // i8 = 0: no int8 plane
     int64_t mq;   // rows of q (and, for the permuted modes, the row stride of d)
 };
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -119,6 +122,11 @@ __host__ __device__ inline act_layout act_layout_of(int mode, int64_t M, int64_t
     L.bs = align256(L.d + nd * 4);
     const size_t nbs = conv_is_q8k(mode) ? (size_t)M * (K / 16) : 0;
     L.bytes = align256(L.bs + nbs * 2);
+    L.i8 = 0;
+    if (conv_is_frag(mode) && M <= DFX_GEMV_M) {
+        L.i8 = L.bytes;
+        L.bytes = align256(L.i8 + (size_t)M * K);
+    }
     return L;
 }
 

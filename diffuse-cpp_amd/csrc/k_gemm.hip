@@ -1857,6 +1857,233 @@ static int dispatch_mmq(const void * w, int N, int K, const void * act, int M, c
     return launch_mmq<WT, 1>(w, N, K, act, M, bias, res, y, ldy, ymap, st, epi);
 }
 
+// ---------------------------------------------------------------------------
+// Q4_K / Q6_K matrix-vector kernels: at most DFX_GEMV_M activation rows (decoding)
+// ---------------------------------------------------------------------------
+// One wave per pair of output columns (n, n + 16), n = 32 (p / 16) + p % 16 for pair p:
+// the pairs the SwiGLU and RoPE epilogues combine.  Lane l takes the 64-element group
+// l % 4 of super-block l / 4 of each pass of 16 super-blocks, for both columns and all
+// rows.  Its integer dot products come from v_dot4_i32_i8 on the natural-order int8
+// activation plane (nibbles and 6-bit quants are non-negative bytes), exactly, in int32;
+// the four lanes of a super-block add them (xor shuffles), and every lane then runs the
+// exact float order over the super-blocks of each chunk of 2048 (shuffled from the lanes
+// that hold them): x = d_w*isum (Q4_K: x = fma(-dmin_w, msum, x)); S = fma(d_a, x, S);
+// T = T + S per chunk.  No MFMA: at these row counts the weights' HBM stream sets the time.
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// One output of the matrix-vector kernels through the epilogue: v = row m at column n,
+// w = row m at the paired column n ^ 16 (the SwiGLU up value, or the other dim of the RoPE
+// pair).  Float expressions as in epilogue_tile / rope_tile / k_gemm_reduce.
+__device__ __forceinline__ void gemv_store(float v, float w, int m, int n, int N, const float * bias, const float * res,
+                                           float * Y, int64_t ldy, const int32_t * ymap, const dfx_epi & epi) {
+#pragma clang fp contract(off)
+    if (epi.kind == DFX_EPI_SWIGLU) {
+        if ((n & 16) == 0) Y[(int64_t)m * ldy + (n >> 5) * 16 + (n & 15)] = silu_mul(v, w);
+        return;
+    }
+    if (bias) {
+        v = v + bias[n];
+        w = w + bias[n ^ 16];
+    }
+    if (epi.kind == DFX_EPI_ROPE) {
+        const int p = epi.pos[m];
+        const int hd = epi.hd, half = hd >> 1;
+        const int g = n + epi.col0, hh = g / hd, cc = g - hh * hd;
+        if (hh < epi.H + epi.Hkv) {
+            const bool first = (cc & 16) == 0;
+            const int d0 = 16 * (cc >> 5) + (cc & 15), d = first ? d0 : half + d0;
+            const float2 cs = *(const float2 *)(epi.tab + ((int64_t)p * half + d0) * 2);
+            const float x0 = first ? v : w, x1 = first ? w : v;
+            const float y = first ? x0 * cs.x - x1 * cs.y : x0 * cs.y + x1 * cs.x;
+            float * dst = hh < epi.H ? epi.q_out + ((int64_t)m * epi.H + hh) * hd
+                                     : epi.kc + ((int64_t)p * epi.Hkv + (hh - epi.H)) * hd;
+            dst[d] = y;
+        } else {
+            epi.vt[((int64_t)(hh - epi.H - epi.Hkv) * hd + cc) * epi.v_ld + p] = v;
+        }
+        return;
+    }
+    const int64_t o = (int64_t)(ymap ? ymap[m] : m) * ldy + n;
+    if (res) v = v + res[o];
+    Y[o] = v;
+}
+
+template <int WT, int MR>
+__global__ void __launch_bounds__(256) k_gemv(const uint8_t * __restrict__ W, int N, int K,
+                                              const uint8_t * __restrict__ act, int M, const float * __restrict__ bias,
+                                              const float * res, float * Y, int64_t ldy,
+                                              const int32_t * __restrict__ ymap, dfx_epi epi) {
+#pragma clang fp contract(off)
+    constexpr bool Q4 = WT == DFX_TYPE_Q4_K;
+    constexpr int SB = Q4 ? SB_Q4_K : SB_Q6_K;
+    const int lane = threadIdx.x & 63;
+    const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (p >= N / 2) return;                              // the whole wave
+    const int ncol[2] = {32 * (p >> 4) + (p & 15), 32 * (p >> 4) + (p & 15) + 16};
+    const int nsb = K >> 8, g = lane & 3, sbl = lane >> 2;
+    const act_layout Lay = act_layout_of(Q4 ? CONV_Q8_K_P4 : CONV_Q8_K_P6, M, K);
+    const int8_t * a8 = (const int8_t *)(act + Lay.i8);
+    const float * ad = (const float *)(act + Lay.d);     // [nsb][mq]
+    const uint16_t * abs = (const uint16_t *)(act + Lay.bs);   // [M][K/16], exact small integers
+    const int64_t rb = (int64_t)nsb * SB;
+    float T[2][MR];
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) T[c][m] = 0.0f;
+
+    for (int sb0 = 0; sb0 < nsb; sb0 += 16) {
+        const int sbc = min(sb0 + sbl, nsb - 1);          // clamped: lanes past the end add nothing
+        const bool live = sb0 + sbl < nsb;
+        float x[2][MR];
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const uint8_t * blk = W + (int64_t)ncol[c] * rb + (int64_t)sbc * SB;
+            int isum[MR], msum[MR];
+            float dw, dmw = 0.0f;
+            if constexpr (Q4) {
+                // header {d, dmin, scales[12]}, then 32 nibble bytes of group g (sub-blocks 2g, 2g+1)
+                const u32x4 h = *(const u32x4 *)blk;
+                const u32x4 q0 = *(const u32x4 *)(blk + 16 + 32 * g), q1 = *(const u32x4 *)(blk + 32 + 32 * g);
+                const q4k_sm sm = q4k_unpack(h);
+                const uint32_t scw = g < 2 ? sm.sc_lo : sm.sc_hi, mnw = g < 2 ? sm.mn_lo : sm.mn_hi;
+                const int sh = 16 * (g & 1);
+                const int sc0 = (scw >> sh) & 0xFF, sc1 = (scw >> (sh + 8)) & 0xFF;
+                const int mn0 = (mnw >> sh) & 0xFF, mn1 = (mnw >> (sh + 8)) & 0xFF;
+                dw = h2f((uint16_t)(h.x & 0xFFFFu));
+                dmw = h2f((uint16_t)(h.x >> 16));
+                const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    const int mm = min(m, M - 1);
+                    const int8_t * ar = a8 + (int64_t)mm * K + (int64_t)sbc * 256 + 64 * g;
+                    const u32x4 a0 = *(const u32x4 *)ar, a1 = *(const u32x4 *)(ar + 16);
+                    const u32x4 a2 = *(const u32x4 *)(ar + 32), a3 = *(const u32x4 *)(ar + 48);
+                    const uint32_t aw[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
+                                             a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+                    int slo = 0, shi = 0;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        slo = sdot4(qw[i] & 0x0F0F0F0Fu, aw[i], slo);
+                        shi = sdot4((qw[i] >> 4) & 0x0F0F0F0Fu, aw[8 + i], shi);
+                    }
+                    isum[m] = sc0 * slo + sc1 * shi;
+                    const uint2 bsw = *(const uint2 *)(abs + (int64_t)mm * (K / 16) + sbc * 16 + 4 * g);
+                    const int b0 = (int)h2f((uint16_t)(bsw.x & 0xFFFFu)), b1 = (int)h2f((uint16_t)(bsw.x >> 16));
+                    const int b2 = (int)h2f((uint16_t)(bsw.y & 0xFFFFu)), b3 = (int)h2f((uint16_t)(bsw.y >> 16));
+                    msum[m] = mn0 * (b0 + b1) + mn1 * (b2 + b3);
+                }
+            } else {
+                // group g: half hf = g / 2, quants l = 16 (g % 2) .. +15 of each of the four
+                // 32-element strips k (elements 128 hf + 32 k + l, sub-block 8 hf + 2 k + g % 2)
+                const int hf = g >> 1, lh = 16 * (g & 1);
+                const u32x4 la = *(const u32x4 *)(blk + 64 * hf + lh), lb = *(const u32x4 *)(blk + 64 * hf + 32 + lh);
+                const u32x4 qh = *(const u32x4 *)(blk + 128 + 32 * hf + lh);
+                const u32x4 scv = *(const u32x4 *)(blk + 192);
+                dw = h2f(*(const uint16_t *)(blk + 208));
+                const uint32_t law[4] = {la.x, la.y, la.z, la.w}, lbw[4] = {lb.x, lb.y, lb.z, lb.w};
+                const uint32_t qhw[4] = {qh.x, qh.y, qh.z, qh.w};
+                uint32_t u[4][4];
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    u[0][t] = (law[t] & 0x0F0F0F0Fu) | ((qhw[t] << 4) & 0x30303030u);
+                    u[1][t] = (lbw[t] & 0x0F0F0F0Fu) | ((qhw[t] << 2) & 0x30303030u);
+                    u[2][t] = ((law[t] >> 4) & 0x0F0F0F0Fu) | (qhw[t] & 0x30303030u);
+                    u[3][t] = ((lbw[t] >> 4) & 0x0F0F0F0Fu) | ((qhw[t] >> 2) & 0x30303030u);
+                }
+                int sck[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int j = 8 * hf + 2 * k + (g & 1);
+                    sck[k] = (int)(int8_t)((scv[j >> 2] >> (8 * (j & 3))) & 0xFFu);
+                }
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    const int mm = min(m, M - 1);
+                    const int8_t * ar = a8 + (int64_t)mm * K + (int64_t)sbc * 256 + 128 * hf + lh;
+                    const uint16_t * br = abs + (int64_t)mm * (K / 16) + sbc * 16 + 8 * hf + (g & 1);
+                    int acc = 0;
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const u32x4 a = *(const u32x4 *)(ar + 32 * k);
+                        int us = 0;
+                        us = sdot4(u[k][0], a.x, us);
+                        us = sdot4(u[k][1], a.y, us);
+                        us = sdot4(u[k][2], a.z, us);
+                        us = sdot4(u[k][3], a.w, us);
+                        const int bsum = (int)h2f(br[2 * k]);
+                        acc += sck[k] * (us - 32 * bsum);
+                    }
+                    isum[m] = acc;
+                    msum[m] = 0;
+                }
+            }
+            // the super-block's four lanes (consecutive) hold its four groups
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                int is = isum[m], ms = msum[m];
+                is += __shfl_xor(is, 1, WAVE);
+                is += __shfl_xor(is, 2, WAVE);
+                if constexpr (Q4) {
+                    ms += __shfl_xor(ms, 1, WAVE);
+                    ms += __shfl_xor(ms, 2, WAVE);
+                    x[c][m] = fmaf(-dmw, (float)ms, dw * (float)is);
+                } else {
+                    x[c][m] = dw * (float)is;
+                }
+                if (!live) x[c][m] = 0.0f;
+            }
+        }
+        // the pass's two chunks of 8 super-blocks: S = fma(d_a, x, S) in order, T = T + S
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int first = sb0 + 8 * h;
+            if (first >= nsb) break;
+            float S[2][MR];
+#pragma unroll
+            for (int c = 0; c < 2; c++)
+#pragma unroll
+                for (int m = 0; m < MR; m++) S[c][m] = 0.0f;
+            for (int i = 0; i < 8 && first + i < nsb; i++) {
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    const float da = ad[(int64_t)(first + i) * Lay.mq + min(m, M - 1)];
+#pragma unroll
+                    for (int c = 0; c < 2; c++) S[c][m] = fmaf(da, __shfl(x[c][m], 32 * h + 4 * i, WAVE), S[c][m]);
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < 2; c++)
+#pragma unroll
+                for (int m = 0; m < MR; m++) T[c][m] = T[c][m] + S[c][m];
+        }
+    }
+    // lane 2m + c stores row m of column c
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+            if (lane == 2 * m + c && m < M) gemv_store(T[c][m], T[c ^ 1][m], m, ncol[c], N, bias, res, Y, ldy, ymap, epi);
+}
+
+template <int WT>
+static int launch_gemv(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
+                       float * y, int64_t ldy, const int32_t * ymap, hipStream_t st, dfx_epi epi) {
+    const dim3 grid((unsigned)((N / 2 + 3) / 4));
+    const uint8_t * W = (const uint8_t *)w;
+    const uint8_t * A = (const uint8_t *)act;
+    switch (M) {
+        case 1: hipLaunchKernelGGL((k_gemv<WT, 1>), grid, dim3(256), 0, st, W, N, K, A, M, bias, res, y, ldy, ymap, epi); break;
+        case 2: hipLaunchKernelGGL((k_gemv<WT, 2>), grid, dim3(256), 0, st, W, N, K, A, M, bias, res, y, ldy, ymap, epi); break;
+        default: hipLaunchKernelGGL((k_gemv<WT, 4>), grid, dim3(256), 0, st, W, N, K, A, M, bias, res, y, ldy, ymap, epi); break;
+    }
+    DFX_CHECK_LAUNCH("dfx_gemm (matrix-vector)");
+    return DFX_OK;
+}
+
 // Internal form: output row m goes to row ymap[m] (or m) of Y with leading dimension
 // ldy; the residual is read at the same place it is written.  Split K uses ws when it
 // is large enough.
@@ -1897,6 +2124,16 @@ int dfx_gemm_ex(int wtype, const void * w, int64_t N, int64_t K, const void * ac
     if (M == 0) return DFX_OK;
     hipStream_t st = (hipStream_t)stream;
     const int n = (int)N, k = (int)K, m = (int)M;
+    // the matrix-vector kernels (unless a tile is forced) where they beat the matrix-core
+    // kernels: one row; two Q4_K rows; up to DFX_GEMV_M rows of a matrix of at most
+    // 4096 x 4096 (measured at the LLaDA-8B shapes: the integer dot products grow with the
+    // rows, the matrix-core kernels' time does not below 32 rows)
+    const bool gemv_rows = m == 1 || (m == 2 && wtype == DFX_TYPE_Q4_K) || (m <= DFX_GEMV_M && N * K <= 4096 * 4096);
+    if (gemv_rows && N % 32 == 0 && (wtype == DFX_TYPE_Q4_K || wtype == DFX_TYPE_Q6_K) &&
+        !forced_tile(wtype == DFX_TYPE_Q4_K ? 0 : 1).on) {
+        return wtype == DFX_TYPE_Q4_K ? launch_gemv<DFX_TYPE_Q4_K>(w, n, k, act, m, bias, residual, y, ldy, ymap, st, epi)
+                                      : launch_gemv<DFX_TYPE_Q6_K>(w, n, k, act, m, bias, residual, y, ldy, ymap, st, epi);
+    }
     switch (wtype) {
         case DFX_TYPE_Q4_K: return dispatch_q4k(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer, epi);
         case DFX_TYPE_Q6_K: return dispatch_q6k(w, n, k, act, m, bias, residual, y, ldy, ymap, ws, ws_bytes, st, defer, epi);

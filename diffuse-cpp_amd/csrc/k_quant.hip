@@ -148,6 +148,11 @@ __device__ __forceinline__ void convert_block256(const float v[4], int lane, int
         } else {
             store_q4(q, o);
         }
+        if (Lay.i8) {   // natural-order int8 copy for the matrix-vector kernels
+            const uint32_t w = (uint32_t)(qi[0] & 0xFF) | ((uint32_t)(qi[1] & 0xFF) << 8) |
+                               ((uint32_t)(qi[2] & 0xFF) << 16) | ((uint32_t)(qi[3] & 0xFF) << 24);
+            *(uint32_t *)(act + Lay.i8 + m * K + b * 256 + 4 * lane) = w;
+        }
         int s = qi[0] + qi[1] + qi[2] + qi[3];
         s += __shfl_xor(s, 1, WAVE);
         s += __shfl_xor(s, 2, WAVE);

@@ -106,8 +106,11 @@ int ensure_capacity(diffuse_context * c, int N) {
     auto A = [&](void ** p, size_t bytes) { return hip_ok(hipMalloc(p, bytes ? bytes : 1), "context hipMalloc"); };
     TRY(A((void **)&c->x, n * D.d * 4));
     const int64_t kmax = std::max(D.d, D.F);
-    TRY(A((void **)&c->act, std::max({dfx_act_bytes(DFX_TYPE_Q4_K, n, kmax), dfx_act_bytes(DFX_TYPE_Q8_0, n, kmax),
-                                      dfx_act_bytes(DFX_TYPE_F16, n, kmax), dfx_act_bytes(DFX_TYPE_F32, n, kmax)})));
+    // passes of at most 4 rows also keep an int8 plane (matrix-vector kernels)
+    TRY(A((void **)&c->act, std::max({dfx_act_bytes(DFX_TYPE_Q4_K, n, kmax),
+                                      dfx_act_bytes(DFX_TYPE_Q4_K, std::min<int64_t>(n, 4), kmax),
+                                      dfx_act_bytes(DFX_TYPE_Q8_0, n, kmax), dfx_act_bytes(DFX_TYPE_F16, n, kmax),
+                                      dfx_act_bytes(DFX_TYPE_F32, n, kmax)})));
     TRY(A((void **)&c->qkv, n * D.nqkv * 4));
     TRY(A((void **)&c->qr, n * D.d * 4));
     TRY(A((void **)&c->att, n * D.d * 4));

@@ -235,6 +235,58 @@ def test_gemm_bias_and_residual_epilogue(gpu):
     assert np.array_equal(rb.download(np.float32, shape=(M, N)), p + res)
 
 
+GEMV_CASES = [(t, N, K, M) for t in (dfx.TYPE_Q4_K, dfx.TYPE_Q6_K)
+              for (N, K) in ((64, 2304), (4608, 3584), (4096, 12288), (1024, 18944)) for M in (1, 2, 3, 4)]
+GEMV_CASES += [(dfx.TYPE_Q6_K, 152064, 3584, 1), (dfx.TYPE_Q4_K, 37888, 3584, 1)]
+
+
+@pytest.mark.parametrize("typ,N,K,M", GEMV_CASES)
+def test_gemv_bit_exact(gpu, typ, N, K, M):
+    """At most four rows the matrix-vector kernels run (integer dot products on the int8
+    plane, the exact float order over super-blocks and chunks, a short last chunk at
+    K = 2304 / 3584 / 18944): the oracle's values bit for bit, and the same bits as the
+    matrix-core kernel forced by a tile override."""
+    raw = quant(typ, N, K)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    got = gpu_gemm(typ, raw, N, K, X)
+    ref = O.mul_mat(typ, raw, N, K, X)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
+    with forced_tile(typ, "1x1x2"):
+        mfma = gpu_gemm(typ, raw, N, K, X)
+    assert np.array_equal(got.view(np.uint32), mfma.view(np.uint32))
+
+
+def test_gemv_epilogues_and_row_map(gpu):
+    """Bias, in-place residual and a row map through the matrix-vector kernel."""
+    typ, N, K, M = dfx.TYPE_Q4_K, 1024, 4096, 3
+    raw = quant(typ, N, K)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    w = to_device_weights(typ, raw, N, K)
+    xb, ab = dfx.Buf.of(X), dfx.Buf(L().dfx_act_bytes(typ, M, K))
+    dfx.check(L().dfx_act_convert(typ, xb.ptr, M, K, ab.ptr, None), "convert")
+    ref = O.mul_mat(typ, raw, N, K, X)
+    bias = rng.standard_normal(N).astype(np.float32)
+    res = rng.standard_normal((M, N)).astype(np.float32)
+    bb, rb = dfx.Buf.of(bias), dfx.Buf.of(res)
+    dfx.check(L().dfx_gemm(typ, w.ptr, N, K, ab.ptr, M, bb.ptr, rb.ptr, rb.ptr, None, None), "gemm")
+    assert np.array_equal(rb.download(np.float32, shape=(M, N)), (ref + bias) + res)
+
+
+def test_act_convert_int8_plane(gpu):
+    """At most four rows the Q4_K/Q6_K activation buffer also holds the int8 quants in
+    natural order, equal to the f16 ones."""
+    K = 4096
+    for typ in (dfx.TYPE_Q4_K, dfx.TYPE_Q6_K):
+        for M in (1, 4):
+            x = rng.standard_normal((M, K)).astype(np.float32)
+            xb, ab = dfx.Buf.of(x), dfx.Buf(L().dfx_act_bytes(typ, M, K))
+            dfx.check(L().dfx_act_convert(typ, xb.ptr, M, K, ab.ptr, None), "convert")
+            q, _, _ = dfx.act_parts(ab, typ, M, K)
+            raw = ab.download(np.uint8)
+            i8 = raw[len(raw) - (M * K + 255) // 256 * 256:][:M * K].view(np.int8).reshape(M, K)
+            assert np.array_equal(i8.astype(np.float32), q.astype(np.float32))
+
+
 def interleave16(typ, gate, up, F, K):
     """gate|up GGML rows interleaved in blocks of 16 (the fused SwiGLU GEMM's weight order)."""
     rb = O.row_bytes(typ, K)
@@ -252,7 +304,8 @@ def oracle_swiglu(g, u):
     (dfx.TYPE_Q4_K, 512, 4096, 77, None), (dfx.TYPE_Q4_K, 512, 4096, 77, "2x1x2s"),
     (dfx.TYPE_Q4_K, 1024, 4096, 130, "w"), (dfx.TYPE_Q4_K, 1024, 4096, 130, "ws"),
     (dfx.TYPE_Q4_K, 1024, 3584, 150, "w3"), (dfx.TYPE_Q4_K, 512, 12288, 5, "1x1x4s"),
-    (dfx.TYPE_Q4_K, 2048, 4096, 1, None), (dfx.TYPE_Q6_K, 512, 12288, 40, "2x1s"),
+    (dfx.TYPE_Q4_K, 2048, 4096, 1, None), (dfx.TYPE_Q4_K, 1024, 4096, 4, None), (dfx.TYPE_Q6_K, 512, 4096, 2, None),
+    (dfx.TYPE_Q6_K, 512, 12288, 40, "2x1s"),
     (dfx.TYPE_Q6_K, 512, 4096, 66, "2x1n"), (dfx.TYPE_Q8_0, 512, 4096, 33, None),
     (dfx.TYPE_F16, 512, 4096, 33, None), (dfx.TYPE_F32, 256, 512, 20, None)])
 def test_gemm_swiglu_epilogue_bit_exact(gpu, typ, F, K, M, tile):
@@ -310,6 +363,7 @@ def rope_row_order(H, Hkv, hd):
     (dfx.TYPE_Q4_K, 8, 2, 128, 2048, 77, None, False), (dfx.TYPE_Q4_K, 8, 8, 128, 4096, 130, "w", True),
     (dfx.TYPE_Q4_K, 4, 4, 128, 4096, 150, "w3", False), (dfx.TYPE_Q4_K, 6, 2, 64, 4096, 40, "2x1x2s", True),
     (dfx.TYPE_Q4_K, 4, 2, 128, 4096, 200, "ws", False), (dfx.TYPE_Q4_K, 8, 8, 128, 4096, 3, None, False),
+    (dfx.TYPE_Q4_K, 4, 2, 128, 3584, 1, None, True), (dfx.TYPE_Q6_K, 4, 4, 64, 4096, 2, None, False),
     (dfx.TYPE_Q6_K, 4, 2, 128, 4096, 66, "2x1s", True), (dfx.TYPE_Q6_K, 4, 4, 64, 2048, 100, "2x1n", False),
     (dfx.TYPE_Q8_0, 4, 2, 128, 2048, 33, None, True), (dfx.TYPE_F16, 4, 1, 128, 2048, 45, None, True),
     (dfx.TYPE_F32, 2, 1, 64, 512, 20, None, False)])
