@@ -10,8 +10,9 @@ ids drawn uniformly from [0, 126000) with seed 1.  Prints one JSON line.
 
 Beside the headline: the other single-GPU workloads of the benchmark set (LLaDA-8B
 32 + 64 low_confidence without cache; Dream-7B 64 + 64 entropy_exit with cache; the
-sampler over a [256 x 126464] logits block), and the CPU baseline (the oracle, a
-restatement of the reference's CPU path, timed on this host).
+sampler over a [256 x 126464] logits block; 8 x (512 + 256) sequences on LLaDA-8B Q8_0
+generating concurrently; Dream-7B ar_generate decode), and the CPU baseline (the oracle,
+a restatement of the reference's CPU path, timed on this host).
 """
 import argparse
 import ctypes as C
@@ -193,6 +194,55 @@ def config_ar(reps=3):
             "decode_weight_gbs": round(gbs, 1), "decode_frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def config_batched():
+    """The batched long-context workload: 8 independent sequences of a 512-token prompt + B=256
+    masks on LLaDA-8B Q8_0 (seed 5), 16 steps, low_confidence with the inter-step cache (the
+    header's default policy).  The sequences run at the same time, one context each (own
+    stream) on one shared model, from 8 host threads; tok/s = 8 x 256 / the wall time of the
+    whole batch.  One warm-up batch, then one timed batch; a single sequence alone is timed
+    beside it."""
+    import threading
+    path = ensure_model("llada8b", dfx.LLADA_8B, "q8_0", 5)
+    model = dfx.Model(path)
+    S, P, Bm = 8, 512, 256
+    prompts = [np.random.default_rng(50 + i).integers(0, 126000, P).astype(np.int32) for i in range(S)]
+    ctxs = [dfx.Context(model, P + Bm) for _ in range(S)]
+    params = dfx.SamplerParams.make(n_steps=16, remasking=dfx.LOW_CONFIDENCE, use_cache=True, seed=42)
+    stats = [dfx.GenStats() for _ in range(S)]
+
+    def batch():
+        errors = []
+
+        def run(i):
+            try:
+                ctxs[i].generate(prompts[i], Bm, params, stats[i])
+            except Exception as e:   # noqa: BLE001 - re-raised below
+                errors.append(e)
+        th = [threading.Thread(target=run, args=(i,)) for i in range(S)]
+        dfx.sync()
+        t0 = time.perf_counter()
+        for t in th:
+            t.start()
+        for t in th:
+            t.join()
+        dfx.sync()
+        if errors:
+            raise errors[0]
+        return time.perf_counter() - t0
+    batch()
+    sec = batch()
+    one, st1 = time_generations(ctxs[0], prompts[0], Bm, params, 1, 0)
+    for c in ctxs:
+        c.close()
+    model.close()
+    return {"workload": "8 x (512 + 256) LLaDA-8B Q8_0, 16 steps, low_confidence + inter-step KV cache, "
+                        "8 contexts generating concurrently",
+            "tok_s": round(S * Bm / sec, 2), "ms_per_batch": round(1000 * sec, 1),
+            "single_sequence_ms": round(1000 * one, 1),
+            "single_ms_per_denoise_step_full": round(st1.step_ms[0], 3),
+            "rows_per_step": [st1.rows_per_step[i] for i in range(st1.actual_steps)]}
+
+
 def config_sampler():
     """The sampler over [256 x 126464] f32 logits N(0, sigma), sigma in {0.5, 2, 8} (seed 4):
     row statistics (softmax max / sum, entropy, top-2), candidate records and the selection
@@ -335,6 +385,9 @@ def main():
         t = time.time()
         configs["ar_dream7b_q4km_decode"] = config_ar()
         log(f"AR workload took {time.time() - t:.1f}s")
+        t = time.time()
+        configs["batched_8x768_llada8b_q8_0"] = config_batched()
+        log(f"batched long-context workload took {time.time() - t:.1f}s")
 
     cpu = None
     if not args.no_cpu:

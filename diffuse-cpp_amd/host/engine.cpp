@@ -145,7 +145,9 @@ int ensure_capacity(diffuse_context * c, int N) {
     TRY(hip_ok(hipMemsetAsync(c->vc, 0, D.L * n * D.dkv * 4, c->stream), "memset"));
     std::vector<float> tab;
     rope_table(N, (int)D.hd, c->model->hparams.rope_theta, tab);
-    TRY(hip_ok(hipMemcpy(c->rope_tab, tab.data(), tab.size() * 4, hipMemcpyHostToDevice), "rope table upload"));
+    TRY(hip_ok(hipMemcpyAsync(c->rope_tab, tab.data(), tab.size() * 4, hipMemcpyHostToDevice, c->stream),
+               "rope table upload"));
+    TRY(hip_ok(hipStreamSynchronize(c->stream), "rope table upload"));
     c->cap = N;
     return DFX_OK;
 }
@@ -159,6 +161,13 @@ hipEvent_t take_event(diffuse_context * c) {
     hipEvent_t e = nullptr;
     if (hipEventCreate(&e) != hipSuccess) return nullptr;
     return e;
+}
+
+// Device -> host copy on the context's stream, waited for.  The engine never touches the
+// legacy stream: another host thread may be capturing its own context's stream meanwhile.
+static int d2h_sync(diffuse_context * c, void * dst, const void * src, size_t bytes) {
+    TRY(hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream), "D2H"));
+    return hip_ok(hipStreamSynchronize(c->stream), "D2H");
 }
 
 // Every GEMM of the forward goes through here; with profiling on, a pair of events
@@ -514,7 +523,7 @@ int generate_device(diffuse_context * c, const int32_t * prompt, int n_prompt, i
         if (callback && *callback) {
             TRY(step_unmasked(s));
             std::vector<int32_t> seq(N);
-            TRY(hip_ok(hipMemcpy(seq.data(), d_seq, (size_t)N * 4, hipMemcpyDeviceToHost), "D2H"));
+            TRY(d2h_sync(c, seq.data(), d_seq, (size_t)N * 4));
             (*callback)(s + 1, p.n_steps, seq);
         }
     }
@@ -523,7 +532,7 @@ int generate_device(diffuse_context * c, const int32_t * prompt, int n_prompt, i
     const double gen_ms = std::chrono::duration<double, std::milli>(clk::now() - gen_start).count();
     // the device's own row counts must be the ones the host launched with
     std::vector<int32_t> counts((size_t)4 * S);
-    TRY(hip_ok(hipMemcpy(counts.data(), c->d_counts, (size_t)4 * S * 4, hipMemcpyDeviceToHost), "D2H"));
+    TRY(d2h_sync(c, counts.data(), c->d_counts, (size_t)4 * S * 4));
     for (int t = 0; t < actual_steps; t++)
         if (counts[4 * t] != rows[t] || counts[4 * t + 3] != full_v[t] ||
             counts[4 * t + 2] != masked_start[t] || (!shift && counts[4 * t + 1] != masked_start[t])) {
@@ -532,11 +541,11 @@ int generate_device(diffuse_context * c, const int32_t * prompt, int n_prompt, i
             return DFX_ERR_HIP;
         }
     std::vector<int32_t> seq(N);
-    TRY(hip_ok(hipMemcpy(seq.data(), d_seq, (size_t)N * 4, hipMemcpyDeviceToHost), "D2H"));
+    TRY(d2h_sync(c, seq.data(), d_seq, (size_t)N * 4));
     memcpy(out, seq.data() + n_prompt, (size_t)n_generate * 4);
     if (unmask_step) {
         std::vector<int32_t> us(N);
-        TRY(hip_ok(hipMemcpy(us.data(), d_ustep, (size_t)N * 4, hipMemcpyDeviceToHost), "D2H"));
+        TRY(d2h_sync(c, us.data(), d_ustep, (size_t)N * 4));
         memcpy(unmask_step, us.data() + n_prompt, (size_t)n_generate * 4);
     }
     double total_fwd = 0;
@@ -575,7 +584,10 @@ int engine_context_new(const diffuse_model * m, int n_ctx, int n_threads, diffus
     c->model = m;
     c->n_ctx = n_ctx;
     c->n_threads = n_threads;
-    int rc = hip_ok(hipStreamCreate(&c->stream), "hipStreamCreate");
+    // non-blocking: no implicit ordering with the legacy stream, so a synchronous copy made by
+    // another context (host thread) never has to wait for, or join, this stream while it is
+    // being captured into a graph; every host read of this stream's results waits for it first
+    int rc = hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
     if (rc == DFX_OK) rc = hip_ok(hipEventCreate(&c->ev0), "hipEventCreate");
     if (rc == DFX_OK) rc = hip_ok(hipEventCreate(&c->ev1), "hipEventCreate");
     if (rc == DFX_OK) rc = hip_ok(hipEventCreate(&c->ev2), "hipEventCreate");
@@ -856,12 +868,10 @@ int engine_generate(diffuse_context * c, const int32_t * prompt, int n_prompt, i
             // Stochastic path stays on the host like the reference (src/diffuse-sampler.cpp:256-269).
             std::vector<dfx_row_stat> st(n_cand);
             std::vector<float> rowbuf((size_t)V);
-            TRY(hip_ok(hipMemcpy(st.data(), c->d_stats, (size_t)n_cand * sizeof(dfx_row_stat), hipMemcpyDeviceToHost),
-                       "D2H"));
+            TRY(d2h_sync(c, st.data(), c->d_stats, (size_t)n_cand * sizeof(dfx_row_stat)));
             std::vector<float> probs((size_t)V);
             for (int j = 0; j < n_cand; j++) {
-                TRY(hip_ok(hipMemcpy(rowbuf.data(), c->logits + (size_t)srows[j] * V, (size_t)V * 4,
-                                     hipMemcpyDeviceToHost), "D2H"));
+                TRY(d2h_sync(c, rowbuf.data(), c->logits + (size_t)srows[j] * V, (size_t)V * 4));
                 const float mx = *std::max_element(rowbuf.begin(), rowbuf.end());
                 float sum = 0.0f;
                 for (int v = 0; v < V; v++) {

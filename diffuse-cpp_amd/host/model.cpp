@@ -59,8 +59,20 @@ struct loader {
         m->device_bytes += bytes;
         return p;
     }
+    // Uploads go through a non-blocking stream of the loader's own (waited for): the legacy
+    // stream is never used, so a load may run while another thread captures a context's stream.
+    hipStream_t st = nullptr;
+    ~loader() {
+        if (st) (void)hipStreamDestroy(st);
+    }
     bool upload(void * dst, const void * src, size_t bytes) {
-        if (hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+        if (!st && hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) {
+            st = nullptr;
+            err = "hipStreamCreate failed";
+            return false;
+        }
+        if (hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st) != hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess) {
             err = "hipMemcpy upload failed";
             return false;
         }

@@ -432,3 +432,46 @@ def test_contexts_generate_concurrently(gpu, tiny_models):
     for c in ctxs:
         c.close()
     model.close()
+
+
+def test_generate_with_legacy_stream_copies_from_another_thread(gpu, tiny_models):
+    """A context captures each new step shape into a graph on its own stream while another
+    host thread keeps copying on the legacy stream: the context's stream is non-blocking, so
+    neither has to join the other (a blocking stream under capture refuses such copies), and
+    the tokens equal an undisturbed generation's."""
+    import threading
+    path = tiny_models[("llada", "q4_k_m")]
+    model = dfx.Model(path)
+    V = model.hparams.n_vocab
+    params = dfx.SamplerParams.make(n_steps=8, remasking=dfx.ENTROPY_EXIT, use_cache=True, entropy_threshold=1.5)
+    prompt = np.random.default_rng(61).integers(0, V - 64, 40).astype(np.int32)
+    ref_ctx = dfx.Context(model, 40 + 48)
+    ref = ref_ctx.generate(prompt, 48, params)
+    ctx = dfx.Context(model, 40 + 48)             # fresh: every step shape is captured anew
+    buf = dfx.Buf.of(np.arange(4096, dtype=np.float32))
+    done, errors, got = threading.Event(), [], [None]
+
+    def copier():
+        try:
+            while not done.is_set():
+                assert buf.download(np.float32)[100] == 100.0
+        except Exception as e:   # noqa: BLE001 - reported below
+            errors.append(e)
+
+    def gen():
+        try:
+            got[0] = ctx.generate(prompt, 48, params)
+        except Exception as e:   # noqa: BLE001 - reported below
+            errors.append(e)
+        finally:
+            done.set()
+    th = [threading.Thread(target=copier), threading.Thread(target=gen)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join(timeout=120)
+    assert not errors, errors
+    assert np.array_equal(got[0], ref)
+    ctx.close()
+    ref_ctx.close()
+    model.close()
