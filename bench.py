@@ -302,6 +302,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-configs", action="store_true", help="skip the other workloads")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--launch", choices=("graphs", "direct"), default="graphs",
+                    help="per-step layer stacks replayed from captured HIP graphs (default) or launched "
+                         "kernel by kernel (the same kernels; for tools that trace launches one by one)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 3 device-to-device copies of 512 MiB (reference kernel for the "
                          "FETCH_SIZE / WRITE_SIZE counter scale) and exit")
@@ -327,6 +330,7 @@ def main():
     t = time.time()
     model = dfx.Model(path)
     ctx = dfx.Context(model, PROMPT + B)
+    ctx.set_device_loop(True, graphs=args.launch == "graphs")
     log(f"model loaded in {time.time() - t:.1f}s")
     prompt = np.random.default_rng(1).integers(0, 126000, PROMPT).astype(np.int32)
     params = dfx.SamplerParams.make(n_steps=STEPS, remasking=dfx.ENTROPY_EXIT, use_cache=True, seed=42,
@@ -412,7 +416,7 @@ def main():
         "config": {"workload": "LLaDA-8B arch Q4_K_M, prompt 32 + B=256 masks, 16 steps, entropy_exit + "
                                "inter-step KV cache (diffuse_generate)",
                    "prompt": PROMPT, "B": B, "denoise_steps": STEPS, "actual_steps": steps_done,
-                   "rows_per_step": rows},
+                   "rows_per_step": rows, "layer_launch": args.launch},
         "ms_per_denoise_step": round(stats.forward_ms / max(steps_done, 1), 3),
         "ms_per_denoise_step_full": step_ms[0] if step_ms else None,
         "ms_per_denoise_step_cached_mean": round(float(np.mean(step_ms[1:])), 3) if len(step_ms) > 1 else None,
