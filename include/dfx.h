@@ -110,9 +110,13 @@ int dfx_rmsnorm_convert(int wtype, const float * x, const float * w, int64_t M, 
  * gu is the [M][2F] output of the fused gate|up GEMM: row m holds gate then up. */
 int dfx_swiglu_convert(int wtype, const float * gu, int64_t M, int64_t F, void * act, void * stream);
 
-/* GEMM on MFMA (src/diffuse-graph.cpp:61-63, 122, 136-140, 154):
+/* GEMM (src/diffuse-graph.cpp:61-63, 122, 136-140, 154):
  *   y[m][n] = sum_k x[m][k] * W[n][k]  (+ bias[n])  (+ residual[m][n])
- * act: the converted activations of x (dfx_*_convert with the same wtype);
+ * on the matrix cores, or for one or two rows of Q4_K / Q6_K weights (and up to four rows of a
+ * matrix of at most 4096 x 4096) on integer dot products over the int8 copy that the conversions
+ * keep for up to four rows.
+ * act: the converted activations of x (dfx_*_convert with the same wtype and the same M: the
+ * layout depends on M);
  * W: device-layout [N][K]; y f32 [M][N].  For Q4_K / Q6_K / Q8_0 the result
  * equals GGML's integer block dot products scaled and summed in a fixed K order
  * (chunks of 2048 elements, chunk sums added in order), i.e. the CPU mul_mat value
