@@ -113,3 +113,75 @@ def test_dream7b_q4km_autoregressive_prefill_and_decode(gpu):
     finally:
         ctx.close()
         model.close()
+
+
+def test_llada8b_q4km_benchmark_generation_replays_through_oracle(gpu):
+    """The benchmark's own generation end to end: LLaDA-8B Q4_K_M (the bench's model file and
+    prompt), 32 + 256 masks, 16 steps, entropy_exit with the inter-step cache, through the
+    default device-resident loop with graph replays, replayed step by step through the
+    oracle's loop on the GPU's choices (teacher forcing): the same rows every step, the same
+    number unmasked, each unmasked token the oracle's argmax, and the unmasked positions the
+    oracle's lowest-entropy ones except where two entropies lie within the entropy tolerance
+    at the cut.  At this vocabulary (126464) and sigma (0.02) every row is close to uniform, so
+    the entropies of different rows differ in the fifth or sixth digit, where the reference's
+    sequential float sums and the GPU's double sums (more accurate) part; the step-0 entropies
+    are compared directly (relative difference below 1e-4)."""
+    from test_gpu_forward import Replay, key_of
+    path = big_model("llada8b", dfx.LLADA_8B, "q4_k_m", 0)
+    om = O.OracleModel(path)
+    P, B, S = 32, 256, 16
+    prompt = np.random.default_rng(1).integers(0, 126000, P).astype(np.int32)
+    params = dfx.SamplerParams.make(n_steps=S, remasking=dfx.ENTROPY_EXIT, use_cache=True, seed=42,
+                                    entropy_threshold=1.5)
+    model = dfx.Model(path)
+    ctx = dfx.Context(model, P + B)
+    try:
+        st = dfx.GenStats()
+        toks, when = ctx.generate_trace(prompt, B, params, st)
+        # step-0 entropies: the GPU's row statistics of the step-0 logits against the reference's
+        # float formula (the oracle), every masked row
+        seq0 = np.concatenate([prompt, np.full(B, int(om.m.mask_token_id), np.int32)])
+        lg = ctx.forward(seq0)[P:]
+        V = lg.shape[1]
+        lb, rb, sb = dfx.Buf.of(lg), dfx.Buf.of(np.arange(B, dtype=np.int32)), dfx.Buf(B * 16)
+        dfx.check(dfx.lib().dfx_row_stats(lb.ptr, V, rb.ptr, B, V, sb.ptr, None), "row_stats")
+        ent_gpu = sb.download(np.float32).reshape(B, 4)[:, 3]
+        ent_ref = np.array([O.entropy(r) for r in lg], np.float32)
+        rel = float(np.max(np.abs(ent_gpu - ent_ref) / np.abs(ent_ref)))
+        spread = float(np.max(ent_ref) - np.min(ent_ref))
+        print(f"[fullsize] step-0 entropy: max rel diff GPU vs reference formula {rel:.2e}, "
+              f"rows span {np.min(ent_ref):.6f}..{np.max(ent_ref):.6f}", flush=True)
+        assert rel < 1e-4
+        pd = dict(use_cache=True, cache_refresh=0, cache_keep_active=0, remasking=dfx.ENTROPY_EXIT)
+        rep = Replay(om, prompt, B, pd)
+        n_masked, n_cut_diff = B, 0
+        for s in range(S):
+            if n_masked == 0:
+                break
+            cand = rep.step(s)
+            assert st.rows_per_step[s] == rep.rows[-1], (s, st.rows_per_step[s], rep.rows[-1])
+            n_sched = O.tokens_to_unmask(s, S, n_masked, 0)
+            n_easy = sum(1 for c in cand if c[3] < 1.5)
+            n_un = min(max(n_sched, n_easy), len(cand))
+            gpu_set = set((np.nonzero(when == s)[0] + P).tolist())
+            assert len(gpu_set) == n_un, (s, len(gpu_set), n_un)
+            keys = sorted(cand, key=lambda c: (key_of(c, dfx.ENTROPY_EXIT), c[0]))
+            ora_set = {c[0] for c in keys[:n_un]}
+            cut = key_of(keys[n_un - 1], dfx.ENTROPY_EXIT)
+            for i in gpu_set ^ ora_set:
+                c = next(c for c in cand if c[0] == i)
+                assert abs(key_of(c, dfx.ENTROPY_EXIT) - cut) <= 1e-4 * abs(cut), (s, i, key_of(c, 2), cut)
+                n_cut_diff += 1
+            for i in gpu_set:
+                c = next(c for c in cand if c[0] == i)
+                assert toks[i - P] == c[1], (s, i, toks[i - P], c[1])   # the logits are the oracle's floats
+                rep.seq[i] = toks[i - P]
+                rep.masked[i] = False
+            n_masked -= len(gpu_set)
+            print(f"[fullsize] replayed step {s}: {rep.rows[-1]} rows, {len(gpu_set)} unmasked", flush=True)
+        assert n_masked == 0
+        print(f"[fullsize] benchmark generation replayed: {st.actual_steps} steps, positions chosen across "
+              f"entropy near-ties at the cut: {n_cut_diff}", flush=True)
+    finally:
+        ctx.close()
+        model.close()
