@@ -137,25 +137,29 @@ __device__ __forceinline__ double4v mfma_f64(double a, double b, double4v c) {
     return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
 }
 
-// Matrix-core attention: one head and 16 query rows per workgroup (4 waves).
-// Phase 1: S = Q K^T on the f64 MFMA; each wave takes key tiles of 16 (t = wave + 4j),
-// the next tile's keys are loaded while the current one multiplies, and the 128
-// head dims are reduced in two independent accumulation chains (dims 16s+4g+c to
-// MFMA c for step s, chains s even / odd), added at the end.
+// Matrix-core attention: one head and 16 query rows per workgroup of NW waves.
+// Phase 1: S = Q K^T on the f64 MFMA; each wave takes key tiles of 16 (t = wave + NW j),
+// the next tiles' keys are loaded while the current one multiplies (KR-slot ring), and
+// the head dims are reduced in four independent accumulation chains (dims 16s+4g+c to
+// MFMA c for step s), added at the end as (c0 + c1) + (c2 + c3).
 // Phase 2: softmax, one wave per row, scores resident in LDS.
-// Phase 3: O = P V on the f64 MFMA; wave w owns head-dim columns 16w+64ct+(0..15),
+// Phase 3: O = P V on the f64 MFMA; wave w owns head-dim columns 16w+16 NW ct+(0..15),
 // keys are the reduction: lane group g supplies keys 16s+4g+c to MFMA c, read as one
-// float4 of the transposed value cache, two key steps ahead.
+// float4 of the transposed value cache, four key steps ahead; two chains (c even / odd).
+// Every output element's sums are the same for every NW: the wave count only decides which
+// wave computes them.  With eight waves (and at most 128 VGPRs) two workgroups share a CU
+// at four waves per SIMD, and each workgroup finishes in about half the time of four waves.
 // Workgroups are numbered so that all query tiles of head h run on XCD h % 8.
-template <int HD, int KR>
-__global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q, const float * __restrict__ kc,
-                                                   const float * __restrict__ vt, int64_t v_ld, int M, int n_keys,
-                                                   int H, int Hkv, int sstride, int q_tiles, int q_pos0, int window,
-                                                   float * __restrict__ out) {
+template <int HD, int KR, int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 4 : 1)))
+k_attn_mfma(const float * __restrict__ q, const float * __restrict__ kc, const float * __restrict__ vt, int64_t v_ld,
+            int M, int n_keys, int H, int Hkv, int sstride, int q_tiles, int q_pos0, int window,
+            float * __restrict__ out) {
 #pragma clang fp contract(off)
     extern __shared__ float S[];       // [16][sstride] scores, then probabilities
     constexpr int SS = HD / 16;        // reduction steps of 16 head dims
-    constexpr int CT = HD / 64;        // phase-3 column tiles per wave (HD=128: 2, HD=64: 1)
+    constexpr int CT = HD / (16 * NW); // phase-3 column tiles per wave
+    static_assert(CT >= 1 && CT * 16 * NW == HD, "head dims split evenly over the waves");
     const int L = blockIdx.x, xcd = L & 7, j = L >> 3;
     const int h = 8 * (j / q_tiles) + xcd, qt = j % q_tiles;
     if (h >= H) return;
@@ -182,7 +186,7 @@ __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q,
 #pragma unroll
         for (int s = 0; s < SS; s++) kf[s] = ld4_or0(kr + 16 * s, n < n_keys);
     };
-    // key tiles t = wv + 4j in a KR-slot register ring, KR - 1 tiles in flight ahead
+    // key tiles t = wv + NW j in a KR-slot register ring, KR - 1 tiles in flight ahead
     // of the one being multiplied (slot roles fixed by unrolling, so no copies)
     float4 kr[KR][SS];
     auto tile = [&](float4 (&kf)[SS], int t) __attribute__((always_inline)) {
@@ -190,7 +194,13 @@ __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q,
 #pragma unroll
         for (int s = 0; s < SS; s++) {
             const float kb[4] = {kf[s].x, kf[s].y, kf[s].z, kf[s].w};
-            const float qa[4] = {qf[s].x, qf[s].y, qf[s].z, qf[s].w};
+            float qa[4] = {qf[s].x, qf[s].y, qf[s].z, qf[s].w};
+            if constexpr (NW == 8) {
+                // converted to double at each use, not once for the whole kernel: the 64
+                // VGPRs of a hoisted double copy do not fit four waves per SIMD
+#pragma unroll
+                for (int c = 0; c < 4; c++) asm volatile("" : "+v"(qa[c]));
+            }
 #pragma unroll
             for (int c = 0; c < 4; c++) a[c] = mfma_f64((double)qa[c], (double)kb[c], a[c]);
         }
@@ -205,21 +215,21 @@ __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q,
     };
 #pragma unroll
     for (int u = 0; u < KR; u++)
-        if (wv + 4 * u < ntiles) load_k(kr[u], wv + 4 * u);
-    for (int t0 = wv; t0 < ntiles; t0 += 4 * KR) {
+        if (wv + NW * u < ntiles) load_k(kr[u], wv + NW * u);
+    for (int t0 = wv; t0 < ntiles; t0 += NW * KR) {
 #pragma unroll
         for (int u = 0; u < KR; u++) {
-            const int t = t0 + 4 * u;
+            const int t = t0 + NW * u;
             if (t < ntiles) {
                 tile(kr[u], t);
-                if (t + 4 * KR < ntiles) load_k(kr[u], t + 4 * KR);
+                if (t + NW * KR < ntiles) load_k(kr[u], t + NW * KR);
             }
         }
     }
     __syncthreads();
 
     // ---- phase 2
-    for (int r = wv; r < 16; r += 4) {
+    for (int r = wv; r < 16; r += NW) {
         float * sr = S + r * sstride;
         float mx = -INFINITY;
         for (int n = lane; n < n_keys; n += 64) mx = fmaxf(mx, sr[n]);
@@ -241,13 +251,13 @@ __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q,
     double4v o[CT][2];                              // chains: column tile x MFMA parity
 #pragma unroll
     for (int ct = 0; ct < CT; ct++) o[ct][0] = o[ct][1] = 0.0;
-    // value column of this lane for column tile ct: 16*wv + 64*ct + li; keys 16s+4g..+3
+    // value column of this lane for column tile ct: 16*wv + 16*NW*ct + li; keys 16s+4g..+3
     const float * vb = vt + ((int64_t)kvh * HD + 16 * wv + li) * v_ld + 4 * lg;
     auto load_v = [&](float4 (&vf)[CT], int s) {
         const int n = 16 * s + 4 * lg;                 // first of this lane's 4 keys
 #pragma unroll
         for (int ct = 0; ct < CT; ct++) {
-            const float * p = vb + (int64_t)64 * ct * v_ld + 16 * min(s, ntiles - 1);
+            const float * p = vb + (int64_t)16 * NW * ct * v_ld + 16 * min(s, ntiles - 1);
             // v_ld and n are multiples of 4 and n_keys <= v_ld: the load stays in the row;
             // keys past the end of the sequence count as 0
             const f32x4 v = *(const f32x4 *)p;
@@ -288,7 +298,8 @@ __global__ void __launch_bounds__(256) k_attn_mfma(const float * __restrict__ q,
         if (row >= M) continue;
 #pragma unroll
         for (int ct = 0; ct < CT; ct++)
-            out[(int64_t)row * H * HD + (int64_t)h * HD + 16 * wv + 64 * ct + li] = (float)(o[ct][0][i] + o[ct][1][i]);
+            out[(int64_t)row * H * HD + (int64_t)h * HD + 16 * wv + 16 * NW * ct + li] =
+                (float)(o[ct][0][i] + o[ct][1][i]);
     }
 }
 
@@ -730,8 +741,8 @@ static inline int attn_sstride(int64_t n_keys) { return (int)(((n_keys + 15) / 1
 // Score-row stride of the split-bf16 kernel: whole 32-key tiles, plus 4 floats.
 static inline int attn_split_sstride(int64_t n_keys) { return (int)(((n_keys + 31) / 32) * 32 + 4); }
 
-#ifndef ATTN_KR
-#define ATTN_KR 2   // key-tile ring of the 128-wide kernel: two slots keep it at two waves per SIMD
+#ifndef ATTN_NW
+#define ATTN_NW 8   // waves per workgroup of the 128-wide exact kernel
 #endif
 
 // The exact (f64-summed) kernels: scores kept in LDS when a 16-row tile of them fits,
@@ -743,11 +754,16 @@ static int attn_exact(const float * q, const float * kc, const float * vt, int64
     const int q_tiles = (M + 15) / 16;
     const dim3 grid((unsigned)(8 * ((H + 7) / 8) * q_tiles));
     if (lds <= attn_lds_limit()) {
-        if (hd == 128)
-            hipLaunchKernelGGL((k_attn_mfma<128, ATTN_KR>), grid, dim3(256), lds, st, q, kc, vt, v_ld, M, n_keys, H, Hkv,
+        // 128 dims: eight waves, a one-slot key ring (at most 128 VGPRs: four waves per SIMD);
+        // 64 dims: four waves, three slots
+        if (hd == 128 && ATTN_NW == 8)
+            hipLaunchKernelGGL((k_attn_mfma<128, 1, 8>), grid, dim3(512), lds, st, q, kc, vt, v_ld, M, n_keys, H, Hkv,
+                               sstride, q_tiles, q_pos0, window, out);
+        else if (hd == 128)
+            hipLaunchKernelGGL((k_attn_mfma<128, 2, 4>), grid, dim3(256), lds, st, q, kc, vt, v_ld, M, n_keys, H, Hkv,
                                sstride, q_tiles, q_pos0, window, out);
         else
-            hipLaunchKernelGGL((k_attn_mfma<64, 3>), grid, dim3(256), lds, st, q, kc, vt, v_ld, M, n_keys, H, Hkv,
+            hipLaunchKernelGGL((k_attn_mfma<64, 3, 4>), grid, dim3(256), lds, st, q, kc, vt, v_ld, M, n_keys, H, Hkv,
                                sstride, q_tiles, q_pos0, window, out);
     } else if (hd == 128) {   // score rows longer than the LDS holds: recomputed in three passes
         hipLaunchKernelGGL((k_attn_long<128>), grid, dim3(256), 0, st, q, kc, vt, v_ld, M, n_keys, H, Hkv, q_tiles,
