@@ -135,6 +135,39 @@ __device__ __forceinline__ half8 to_half8(const int v[8]) {
 // Row of register r of a 32x32 MFMA tile held by `lane` (its column is lane % 32).
 __device__ __forceinline__ int tile_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
+// Block flushes over one lane's 16 outputs of a 32x32 tile, written as passes of 16
+// independent operations (an empty asm on every value between passes keeps the compiler
+// from folding them back into one dependent chain per output).  Each output sees the same
+// operations in the same order as the chain, so the bits are the same; the VALU then
+// pipelines the 16 outputs instead of waiting out each output's chain (measured on MI355X:
+// the Q4_K super-block flush 25 % shorter).
+__device__ __forceinline__ void pass_barrier(float (&x)[16]) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) asm volatile("" : "+v"(x[r]));
+}
+// Q4_K super-block: x = d_w*isum; x = fma(-dmin_w, msum, x); S = fma(d_a, x, S)
+__device__ __forceinline__ void flush_dmin(float16v & S, const float16v & P, const float16v & Q, float dw, float dmw,
+                                           const float (&da)[16]) {
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) x[r] = dw * P[r];
+    pass_barrier(x);
+#pragma unroll
+    for (int r = 0; r < 16; r++) x[r] = fmaf(-dmw, Q[r], x[r]);
+    pass_barrier(x);
+#pragma unroll
+    for (int r = 0; r < 16; r++) S[r] = fmaf(da[r], x[r], S[r]);
+}
+// Q6_K super-block, Q8_0 block: S = fma(d_a, d_w*isum, S)
+__device__ __forceinline__ void flush_d(float16v & S, const float16v & P, float dw, const float (&da)[16]) {
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) x[r] = dw * P[r];
+    pass_barrier(x);
+#pragma unroll
+    for (int r = 0; r < 16; r++) S[r] = fmaf(da[r], x[r], S[r]);
+}
+
 // RoPE epilogue of one 32 x 32 tile (DFX_EPI_ROPE): v[r] is this lane's value of row
 // m0 + tile_row(r, lane) at GEMM column n, w[r] the value of the paired column n ^ 16,
 // p[r] the row's position.  The rotation is the NEOX one of ggml_rope_ext, as the RoPE
@@ -381,13 +414,14 @@ k_mmq(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
                 const int bl = kk >> 1;
                 const float dw = h2f(*(const uint16_t *)(wp + 2 * (4 * h + bl)));
 #pragma unroll
-                for (int i = 0; i < TM; i++)
+                for (int i = 0; i < TM; i++) {
+                    float dav[16];
 #pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const float da = Ad[(i * 32 + tile_row(r, lane)) * 4 + bl];
-                        S1[i][r] = fmaf(da, dw * P[i][r], S1[i][r]);
-                        P[i][r] = 0.0f;
-                    }
+                    for (int r = 0; r < 16; r++) dav[r] = Ad[(i * 32 + tile_row(r, lane)) * 4 + bl];
+                    flush_d(S1[i], P[i], dw, dav);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) P[i][r] = 0.0f;
+                }
             }
         }
         if (!KQ && ((kt + 1) % (DFX_DOT_CHUNK / BK) == 0 || kt + 1 == n_kt)) {
@@ -418,24 +452,24 @@ k_mmq(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
 #pragma unroll
                     for (int r = 0; r < 16; r++) Q[r] = 0.0f;
                     Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bm, Q, 0, 0, 0);
+                    float dav[16];
 #pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const float da = Ad[i * 32 + tile_row(r, lane)];
-                        const float x = fmaf(-dmw, Q[r], dw * P[i][r]);
-                        S1[i][r] = fmaf(da, x, S1[i][r]);
-                        P[i][r] = 0.0f;
-                    }
+                    for (int r = 0; r < 16; r++) dav[r] = Ad[i * 32 + tile_row(r, lane)];
+                    flush_dmin(S1[i], P[i], Q, dw, dmw, dav);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) P[i][r] = 0.0f;
                 }
             } else {
                 const float dw = h2f(*(const uint16_t *)(wp + 112));
 #pragma unroll
-                for (int i = 0; i < TM; i++)
+                for (int i = 0; i < TM; i++) {
+                    float dav[16];
 #pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const float da = Ad[i * 32 + tile_row(r, lane)];
-                        S1[i][r] = fmaf(da, dw * P[i][r], S1[i][r]);
-                        P[i][r] = 0.0f;
-                    }
+                    for (int r = 0; r < 16; r++) dav[r] = Ad[i * 32 + tile_row(r, lane)];
+                    flush_d(S1[i], P[i], dw, dav);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) P[i][r] = 0.0f;
+                }
             }
             if (((kt >> 1) + 1) % (DFX_DOT_CHUNK / 256) == 0 || kt + 1 == n_kt) {
                 // chunk complete: T = T + S
@@ -709,17 +743,13 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
                 for (int i = 0; i < TM; i++) {
                     const half8 a = *(const half8 *)(&Abs[mbuf][(i * 32 + l32) * BST + 8 * hl]);
                     const float16v Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bm, zero16, 0, 0, 0);
+                    float dav[16];
 #pragma unroll
                     for (int q4 = 0; q4 < 4; q4++) {
                         const float4 da = *(const float4 *)(&Ad[mbuf][i * 32 + 8 * q4 + 4 * hl]);
-                        const float dav[4] = {da.x, da.y, da.z, da.w};
-#pragma unroll
-                        for (int rr = 0; rr < 4; rr++) {
-                            const int r = 4 * q4 + rr;
-                            const float x = fmaf(-dmw, Q[r], dw * P[i][t][r]);
-                            S[i][t][r] = fmaf(dav[rr], x, S[i][t][r]);
-                        }
+                        dav[4 * q4] = da.x; dav[4 * q4 + 1] = da.y; dav[4 * q4 + 2] = da.z; dav[4 * q4 + 3] = da.w;
                     }
+                    flush_dmin(S[i][t], P[i][t], Q, dw, dmw, dav);
                 }
             }
         }
@@ -1023,17 +1053,13 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
                 for (int i = 0; i < TM; i++) {
                     const half8 av = *(const half8 *)(Abs + (i * 32 + l32) * 16 + 8 * hl);
                     const float16v Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bm, zero16, 0, 0, 0);
+                    float dav[16];
 #pragma unroll
                     for (int q4 = 0; q4 < 4; q4++) {
                         const float4 da = *(const float4 *)(Ad + i * 32 + 8 * q4 + 4 * hl);
-                        const float dav[4] = {da.x, da.y, da.z, da.w};
-#pragma unroll
-                        for (int rr = 0; rr < 4; rr++) {
-                            const int r = 4 * q4 + rr;
-                            const float x = fmaf(-dmw[t], Q[r], dw[t] * P[i][t][r]);
-                            S[i][t][r] = fmaf(dav[rr], x, S[i][t][r]);
-                        }
+                        dav[4 * q4] = da.x; dav[4 * q4 + 1] = da.y; dav[4 * q4 + 2] = da.z; dav[4 * q4 + 3] = da.w;
                     }
+                    flush_dmin(S[i][t], P[i][t], Q, dw[t], dmw[t], dav);
                 }
             }
         }
@@ -1266,16 +1292,13 @@ k_q6k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
                 const float dw = h2f((uint16_t)(dwh[t] & 0xFFFFu));
 #pragma unroll
                 for (int ii = 0; ii < TM; ii++) {
+                    float dav[16];
 #pragma unroll
                     for (int q4 = 0; q4 < 4; q4++) {
                         const float4 da = *(const float4 *)(&Ad[mbuf][ii * 32 + 8 * q4 + 4 * hl]);
-                        const float dav[4] = {da.x, da.y, da.z, da.w};
-#pragma unroll
-                        for (int rr = 0; rr < 4; rr++) {
-                            const int r = 4 * q4 + rr;
-                            S[ii][t][r] = fmaf(dav[rr], dw * P[ii][t][r], S[ii][t][r]);
-                        }
+                        dav[4 * q4] = da.x; dav[4 * q4 + 1] = da.y; dav[4 * q4 + 2] = da.z; dav[4 * q4 + 3] = da.w;
                     }
+                    flush_d(S[ii][t], P[ii][t], dw, dav);
                 }
             }
         }
