@@ -228,22 +228,65 @@ k_attn_mfma(const float * __restrict__ q, const float * __restrict__ kc, const f
     }
     __syncthreads();
 
-    // ---- phase 2
-    for (int r = wv; r < 16; r += NW) {
-        float * sr = S + r * sstride;
-        float mx = -INFINITY;
-        for (int n = lane; n < n_keys; n += 64) mx = fmaxf(mx, sr[n]);
-        mx = wave_max(mx);
-        double sum = 0.0;
-        for (int n = lane; n < n_keys; n += 64) {
-            const float e = (float)exp((double)(sr[n] - mx));
-            sr[n] = e;
-            sum += (double)e;
+    // ---- phase 2: the wave's RPW rows (wv, wv + NW, ..) together, four keys per lane and
+    // row at a time, so that RPW * 4 exponentials and the rows' reductions are in flight at
+    // once.  Each lane sums its keys lane, lane + 64, .. in increasing order and the lanes
+    // are added by the xor butterfly, one row as another.
+    {
+        constexpr int RPW = 16 / NW;
+        float mx[RPW];
+#pragma unroll
+        for (int q = 0; q < RPW; q++) mx[q] = -INFINITY;
+        for (int n0 = lane; n0 < n_keys; n0 += 256)
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int n = n0 + 64 * u;
+#pragma unroll
+                for (int q = 0; q < RPW; q++)
+                    if (n < n_keys) mx[q] = fmaxf(mx[q], S[(wv + NW * q) * sstride + n]);
+            }
+#pragma unroll
+        for (int q = 0; q < RPW; q++) mx[q] = wave_max(mx[q]);
+        double sum[RPW];
+#pragma unroll
+        for (int q = 0; q < RPW; q++) sum[q] = 0.0;
+        for (int n0 = lane; n0 < n_keys; n0 += 256) {
+            float e[RPW][4];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int q = 0; q < RPW; q++) {
+                    const int n = min(n0 + 64 * u, n_keys - 1);
+                    e[q][u] = (float)exp((double)(S[(wv + NW * q) * sstride + n] - mx[q]));
+                }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int n = n0 + 64 * u;
+                if (n < n_keys)
+#pragma unroll
+                    for (int q = 0; q < RPW; q++) {
+                        S[(wv + NW * q) * sstride + n] = e[q][u];
+                        sum[q] += (double)e[q][u];
+                    }
+            }
         }
-        sum = wave_sum_d(sum);
-        const float inv = (float)(1.0 / sum);
-        for (int n = lane; n < n_keys; n += 64) sr[n] = sr[n] * inv;
-        for (int n = n_keys + lane; n < 16 * ntiles; n += 64) sr[n] = 0.0f;
+        float inv[RPW];
+#pragma unroll
+        for (int q = 0; q < RPW; q++) {
+            sum[q] = wave_sum_d(sum[q]);
+            inv[q] = (float)(1.0 / sum[q]);
+        }
+        for (int n0 = lane; n0 < n_keys; n0 += 256)
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int n = n0 + 64 * u;
+                if (n < n_keys)
+#pragma unroll
+                    for (int q = 0; q < RPW; q++) S[(wv + NW * q) * sstride + n] *= inv[q];
+            }
+#pragma unroll
+        for (int q = 0; q < RPW; q++)
+            for (int n = n_keys + lane; n < 16 * ntiles; n += 64) S[(wv + NW * q) * sstride + n] = 0.0f;
     }
     __syncthreads();
 
