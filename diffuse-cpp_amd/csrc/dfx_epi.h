@@ -27,4 +27,9 @@ struct dfx_epi {
     float * kc;
     float * vt;
     int64_t v_ld;
+    // Completion counters of tiles whose K range is split over two workgroups inside one
+    // launch (the later of the two adds the halves and applies the epilogue); one int per
+    // tile, 128 bytes apart, zero before the call and left zero after it.  Null: no such
+    // split (any epilogue kind may use it).
+    int32_t * tile_cnt;
 };

@@ -32,6 +32,7 @@
 #include "dfx_device.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -826,7 +827,7 @@ template <int TM, int TN, int DEPTH>
 __global__ void __launch_bounds__(256, TN == 1 ? 2 : 1)
 k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__ act, int M,
         const float * __restrict__ bias, const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
-        int n_tiles, int m_tiles, float * __restrict__ ws, dfx_epi epi) {
+        int n_tiles, int m_tiles, float * __restrict__ ws, dfx_epi epi, int n_full) {
 #pragma clang fp contract(off)
     constexpr int BM = 32 * TM, BN = 128 * TN, WSZ = 2048 * TN;   // WSZ: nibble bytes per wave and step
     constexpr int NA = 2 * TM;                                     // A operand copies per wave and step
@@ -860,7 +861,30 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
     };
 
     const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
-    const int z = blockIdx.x / per_pass, L = blockIdx.x - z * per_pass, xcd = L & 7, j = L >> 3;
+    // Tile L (numbered as the grid without split).  With ws and no tile counters every tile's
+    // K range is split at chunk borders (z = chunk).  With counters (two chunks): workgroups
+    // 0 .. n_full-1 take whole tiles, the others half tiles, the two halves of tile L being
+    // workgroups n_full + 16q + e and n_full + 16q + 8 + e (L = n_full + 8q + e): both on
+    // XCD L mod 8, so the halves meet in one L2.
+    int z, L, cpart = 0;
+    bool half = false;
+    int32_t * const cnt = epi.tile_cnt;
+    if (cnt) {
+        const int B = blockIdx.x;
+        if (B < n_full) {
+            L = B;
+        } else {
+            const int u = B - n_full;
+            L = n_full + 8 * (u >> 4) + (u & 7);
+            cpart = (u >> 3) & 1;
+            half = true;
+        }
+        z = 0;
+    } else {
+        z = blockIdx.x / per_pass;
+        L = blockIdx.x - z * per_pass;
+    }
+    const int xcd = L & 7, j = L >> 3;
     const int ty = j % m_tiles, tx = 8 * (j / m_tiles) + xcd;
     if (tx >= n_tiles) return;
 
@@ -869,8 +893,9 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
     const int n0 = tx * BN, m0 = ty * BM;
     constexpr int SB_CHUNK = DFX_DOT_CHUNK / 256;
     const int n_sb_all = K >> 8;
-    const int sb_first = ws ? z * SB_CHUNK : 0;
-    const int n_sb = ws ? min(SB_CHUNK, n_sb_all - sb_first) : n_sb_all;
+    const bool split = cnt ? half : ws != nullptr;
+    const int sb_first = split ? (cnt ? cpart : z) * SB_CHUNK : 0;
+    const int n_sb = split ? min(SB_CHUNK, n_sb_all - sb_first) : n_sb_all;
     const int n_kt = 2 * n_sb;
     const uint32_t row_bytes = (uint32_t)n_sb_all * SB_Q4_K;
     const act_layout Lay = act_layout_of(CONV_Q8_K_P4, M, K);
@@ -1093,12 +1118,47 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
     // them finish before the workgroup (and its LDS) can end
     __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm(0, 0));
 
+    if (half) {
+        // half tile: chunk total T = 0 + S_c to ws[c]; the later of the tile's two halves reads
+        // the other's and forms (0 + S_0) + (0 + S_1), which equals the whole tile's
+        // (0 + S_0) + S_1 (0 + x is never -0), then applies the epilogue.  Its stores complete
+        // in the XCD's L2 before the counter's atomic there; the partner's loads of lines it
+        // never touched miss its own vector L1.  No workgroup waits for another.
+        __shared__ int first;
+#pragma unroll
+        for (int t = 0; t < TN; t++)
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                epilogue_tile(T[i][t], m0 + i * 32, n0 + (wv * TN + t) * 32 + l32, M, N, nullptr, nullptr, nullptr, 0,
+                              nullptr, ws, cpart, lane, epi);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm(0, 15));
+        __syncthreads();
+        if (tid == 0) first = __hip_atomic_fetch_add(cnt + 32 * L, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0;
+        __syncthreads();
+        if (first) return;
+        const float * other = ws + (int64_t)(1 - cpart) * M * N;
+#pragma unroll
+        for (int t = 0; t < TN; t++)
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const int n = n0 + (wv * TN + t) * 32 + l32;
+                float o[16];
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int m = m0 + i * 32 + tile_row(r, lane);
+                    o[r] = (m < M && n < N) ? other[(int64_t)m * N + n] : 0.0f;
+                }
+#pragma unroll
+                for (int r = 0; r < 16; r++) T[i][t][r] = cpart == 0 ? T[i][t][r] + o[r] : o[r] + T[i][t][r];
+            }
+        if (tid == 0) cnt[32 * L] = 0;   // ready for the next call
+    }
 #pragma unroll
     for (int t = 0; t < TN; t++)
 #pragma unroll
         for (int i = 0; i < TM; i++)
-            epilogue_tile(T[i][t], m0 + i * 32, n0 + (wv * TN + t) * 32 + l32, M, N, bias, res, Y, ldy, ymap, ws, z,
-                          lane, epi);
+            epilogue_tile(T[i][t], m0 + i * 32, n0 + (wv * TN + t) * 32 + l32, M, N, bias, res, Y, ldy, ymap,
+                          cnt ? nullptr : ws, z, lane, epi);
 }
 
 // ---------------------------------------------------------------------------
@@ -1568,7 +1628,7 @@ __global__ void k_gemm_reduce(const float * __restrict__ ws, int S, int64_t MN, 
 struct tile_force {
     bool on = false;
     int got = 0, tm = 0, tn = 0, d = 0;
-    bool split = false, nosplit = false, w = false, w1 = false, w3 = false;
+    bool split = false, nosplit = false, w = false, w1 = false, w3 = false, halves = false;
 };
 static std::mutex g_force_mu;
 static tile_force g_force[2];   // [0] Q4_K, [1] Q6_K
@@ -1584,6 +1644,7 @@ static tile_force parse_force(const char * f) {
     t.w = strchr(f, 'w') != nullptr;
     t.w1 = strstr(f, "w1") != nullptr;
     t.w3 = strstr(f, "w3") != nullptr;
+    t.halves = strchr(f, 'f') != nullptr;
     return t;
 }
 
@@ -1705,9 +1766,11 @@ static int launch_q4k(const void * w, int N, int K, const void * act, int M, con
 }
 
 template <int TM, int TN, int DEPTH>
+// n_full >= 0 (with epi.tile_cnt, two chunks, ws of 2 M N floats): tiles n_full.. are split
+// into halves combined inside the launch; otherwise epi.tile_cnt is ignored.
 static int launch_q4k_w(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                         float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st, int * defer,
-                      dfx_epi epi) {
+                      dfx_epi epi, int n_full = -1) {
     const int n_tiles = (N + 128 * TN - 1) / (128 * TN), m_tiles = (M + 32 * TM - 1) / (32 * TM);
     const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
     const int chunks = dot_chunks(K), passes = ws ? chunks : 1;
@@ -1716,11 +1779,44 @@ static int launch_q4k_w(const void * w, int N, int K, const void * act, int M, c
         dfx_set_error("dfx_gemm q4_k: K=%d does not fit the pipeline depth %d", K, DEPTH);
         return DFX_ERR_ARG;
     }
-    hipLaunchKernelGGL((k_q4k_w<TM, TN, DEPTH>), dim3((unsigned)(per_pass * passes)), dim3(256), 0, st, (const uint8_t *)w, N,
-                       K, (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles, ws, epi);
+    const bool halves = n_full >= 0 && epi.tile_cnt && ws && chunks == 2 && n_full % 8 == 0 && n_full <= per_pass;
+    if (!halves) epi.tile_cnt = nullptr;
+    const int grid = halves ? 2 * per_pass - n_full : per_pass * passes;
+    hipLaunchKernelGGL((k_q4k_w<TM, TN, DEPTH>), dim3((unsigned)grid), dim3(256), 0, st, (const uint8_t *)w, N, K,
+                       (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles, ws, epi, halves ? n_full : 0);
     DFX_CHECK_LAUNCH("dfx_gemm q4_k");
-    if (ws) return reduce_or_defer(ws, chunks, M, N, bias, res, y, ldy, ymap, st, defer, epi);
+    if (ws && !halves) return reduce_or_defer(ws, chunks, M, N, bias, res, y, ldy, ymap, st, defer, epi);
     return DFX_OK;
+}
+
+// Compute units of the current device (cached per device).
+static int device_cu_count() {
+    static std::atomic<int> cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int v = cached[dev].load(std::memory_order_relaxed);
+    if (!v) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cached[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
+// Whole tiles for the first n_full workgroups, half tiles after them, so that the workgroup
+// slots (two per CU) carry about the same number of K steps: T = q S + r tiles over S slots
+// leave r tiles to a last round; n_full = q S + max(0, 2r - S) whole tiles and the rest as
+// halves fill that round with halves instead (r <= S/2: every tile of it split; r > S/2:
+// 2 (S - r) halves beside 2r - S whole tiles).  Returns -1 where no split is taken: the measured wins (MI355X, LLaDA-8B shapes, every result the same bits) are
+// 256 < T <= 512 tiles (Q|K|V at 129-320 rows 6-15 % faster, gate|up at 65-128 rows 16 %)
+// and a last round of at least 3/4 of the slots (gate|up at 288 rows, 5 %); a last round of
+// half the slots (gate|up at 193-256 rows) is 6 % slower split, and at most 256 tiles
+// (one per CU or fewer) gain nothing.
+static int split_tile_count(int per_pass, bool force) {
+    const int S = 2 * device_cu_count();
+    const int q = per_pass / S, r = per_pass - q * S;
+    if (!force && !(per_pass > S / 2 && per_pass <= S) && !(per_pass > S && 4 * r >= 3 * S)) return -1;
+    const int n_full = q * S + std::max(0, 2 * r - S);
+    return std::min(per_pass, (n_full + 7) / 8 * 8);
 }
 
 template <int TM, int TN, int D>
@@ -1839,10 +1935,23 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
     if (f.on && f.w) {
         // "w": 64 x 64 per wave; "w1": 64 x 32 per wave, two workgroups per CU
         float * wsw = split ? (float *)ws : nullptr;
-        if (f.w1) return launch_q4k_w<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer, epi);
+        if (f.w1) {
+            if (f.halves && epi.tile_cnt && chunks == 2 && N % 128 == 0 && ws &&
+                ws_bytes >= (size_t)2 * M * N * sizeof(float))
+                return launch_q4k_w<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, (float *)ws, st, defer, epi,
+                                             split_tile_count(8 * ((n_col + 7) / 8) * ((M + 63) / 64), true));
+            return launch_q4k_w<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer, epi);
+        }
         if (f.w3) return launch_q4k_w<3, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer, epi);
         if (sb_last % 2) return launch_q4k_w<2, 2, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer, epi);
         return launch_q4k_w<2, 2, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer, epi);
+    }
+    // whole and half tiles in one launch where that evens out the workgroups per CU
+    if (dma && epi.tile_cnt && chunks == 2 && N % 128 == 0 && ws && ws_bytes >= (size_t)2 * M * N * sizeof(float) &&
+        (!f.on || f.got < 2)) {
+        const int nf = split_tile_count(8 * ((n_col + 7) / 8) * ((M + 63) / 64), f.on && f.halves);
+        if (nf >= 0)
+            return launch_q4k_w<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, (float *)ws, st, defer, epi, nf);
     }
     // 96-row tiles (k_q4k_w<3, 1, 2>): each dequantised weight feeds three MFMAs instead of
     // two, but a workgroup takes 1.5x longer, so they only pay when the chosen kernel's grid
@@ -2192,6 +2301,20 @@ extern "C" int dfx_gemm(int wtype, const void * w, int64_t N, int64_t K, const v
                         const float * bias, const float * residual, float * y, void * ws, void * stream) {
     return dfx_gemm_ex(wtype, w, N, K, act, M, bias, residual, y, N, nullptr, ws,
                        ws ? dfx_gemm_ws_bytes(M, N, K) : 0, stream, nullptr, nullptr);
+}
+
+extern "C" size_t dfx_gemm_tile_cnt_bytes(int64_t M, int64_t N) {
+    if (M <= 0 || N <= 0) return 0;
+    return (size_t)(8 * ((((N + 127) / 128) + 7) / 8) * ((M + 63) / 64)) * 32 * sizeof(int32_t);
+}
+
+extern "C" int dfx_gemm_counted(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
+                                const float * bias, const float * residual, float * y, void * ws, int32_t * tile_cnt,
+                                void * stream) {
+    dfx_epi e{};
+    e.tile_cnt = tile_cnt;
+    return dfx_gemm_ex(wtype, w, N, K, act, M, bias, residual, y, N, nullptr, ws,
+                       ws ? dfx_gemm_ws_bytes(M, N, K) : 0, stream, nullptr, &e);
 }
 
 extern "C" int dfx_gemm_swiglu(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,

@@ -130,6 +130,8 @@ def _declare(L):
         "dfx_gemm_ws_bytes": (S, [I64, I64, I64]),
         "dfx_gemm": (I32, [I32, P, I64, I64, P, I64, P, P, P, P, P]),
         "dfx_gemm_noalloc": (I32, [I32, P, I64, I64, P, I64, P, P, P, P]),
+        "dfx_gemm_counted": (I32, [I32, P, I64, I64, P, I64, P, P, P, P, P, P]),
+        "dfx_gemm_tile_cnt_bytes": (S, [I64, I64]),
         "dfx_gemm_swiglu": (I32, [I32, P, I64, I64, P, I64, P, I64, P, P]),
         "dfx_gemm_rope": (I32, [I32, P, I64, I64, P, I64, P, I32, P, I32, I32, I32, P, P, P, P, I64, P, P]),
         "dfx_gemm_force_tile": (I32, [I32, C.c_char_p]),

@@ -53,7 +53,7 @@ void free_buffers(diffuse_context * c) {
     drop_graphs(c);
     void * bufs[] = {c->x, c->act, c->qkv, c->qr, c->att, c->gu, c->logits, c->kc, c->vc, c->rope_tab,
                      c->d_ints, c->ws, c->d_stats, c->d_out, c->x_prev, c->d_imp, c->d_ar, c->d_state,
-                     c->d_counts, c->d_hist};
+                     c->d_counts, c->d_hist, c->tile_cnt};
     for (void * p : bufs)
         if (p) (void)hipFree(p);
     if (c->h_pin) (void)hipHostFree(c->h_pin);
@@ -72,6 +72,7 @@ void free_buffers(diffuse_context * c) {
     c->act = nullptr;
     c->d_ints = c->d_tok = c->d_pos = c->d_hrows = c->d_hmap = c->d_srows = c->d_spos = c->d_order = c->d_nun = nullptr;
     c->ws = c->d_out = c->h_out = nullptr;
+    c->tile_cnt = nullptr;
     c->out_bytes = 0;
     c->d_stats = nullptr;
     c->d_cand = nullptr;
@@ -126,11 +127,14 @@ int ensure_capacity(diffuse_context * c, int N) {
     c->d_hmap = c->d_ints + 3 * n;
     c->d_srows = c->d_ints + 4 * n;
     c->d_spos = c->d_ints + 5 * n;
-    // split-K workspace for the GEMMs with few output tiles (Q|K|V, O, down); gate|up
-    // (N = 2F) always has enough tiles and gets whatever fits
-    c->ws_bytes = std::max(std::max(dfx_gemm_ws_bytes(n, D.nqkv, D.d), dfx_gemm_ws_bytes(n, D.d, D.d)),
-                           dfx_gemm_ws_bytes(n, D.d, D.F));
+    // split-K workspace for the GEMMs with few output tiles (Q|K|V, O, down) and the chunk
+    // totals of half tiles (Q|K|V, gate|up); their completion counters start (and stay) zero
+    c->ws_bytes = std::max({dfx_gemm_ws_bytes(n, D.nqkv, D.d), dfx_gemm_ws_bytes(n, D.d, D.d),
+                            dfx_gemm_ws_bytes(n, D.d, D.F), dfx_gemm_ws_bytes(n, 2 * D.F, D.d)});
     TRY(A(&c->ws, c->ws_bytes));
+    const size_t cnt_bytes = std::max(dfx_gemm_tile_cnt_bytes(n, D.nqkv), dfx_gemm_tile_cnt_bytes(n, 2 * D.F));
+    TRY(A((void **)&c->tile_cnt, cnt_bytes));
+    TRY(hip_ok(hipMemsetAsync(c->tile_cnt, 0, cnt_bytes, c->stream), "counter clear"));
     TRY(A((void **)&c->d_stats, n * sizeof(dfx_row_stat)));
     TRY(A((void **)&c->d_state, 5 * n * 4));
     c->out_bytes = n * sizeof(dfx_candidate) + n * 4 + 16;
@@ -234,6 +238,7 @@ int run_group(diffuse_context * c, const proj_group & g, const float * norm, int
         TRY(norm_convert(g.all.type));
         dfx_epi e{};
         e.kind = DFX_EPI_SWIGLU;
+        e.tile_cnt = c->tile_cnt;
         return gemm(c, g.all, g.n_out, K, M, nullptr, nullptr, out, g.n_out / 2, nullptr, true, nullptr, &e);
     }
     if (rope) {       // Q|K|V rotated and stored by the GEMM's epilogue (rows permuted at load)
@@ -287,6 +292,7 @@ int forward_layers(diffuse_context * c, int M, int n_keys, const pass_opts & o, 
             e.kc = kc;
             e.vt = vc;
             e.v_ld = c->cap;
+            e.tile_cnt = c->tile_cnt;
             TRY(run_group(c, L.qkv, L.attn_norm, M, D.d, nullptr, pending, &e));
         } else {
             TRY(run_group(c, L.qkv, L.attn_norm, M, D.d, c->qkv, pending));

@@ -104,8 +104,9 @@ struct diffuse_context {
     int32_t *    d_hmap = nullptr;   // slot 3: logits row of each of them
     int32_t *    d_srows = nullptr;  // slot 4: logits rows scanned by the sampler
     int32_t *    d_spos = nullptr;   // slot 5: masked position of each scanned row
-    void *       ws = nullptr;       // split-K workspace
+    void *       ws = nullptr;       // split-K workspace (also the half tiles' chunk totals)
     size_t       ws_bytes = 0;
+    int32_t *    tile_cnt = nullptr; // completion counters of half-tile GEMM launches (kept zero)
     dfx_row_stat *  d_stats = nullptr;
     // Sampler results, one allocation d_out = [cand: cap][order: cap][n_unmask], read back
     // with one copy into the pinned h_out.

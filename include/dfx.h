@@ -126,6 +126,19 @@ size_t dfx_gemm_ws_bytes(int64_t M, int64_t N, int64_t K);
 int dfx_gemm(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
              const float * bias, const float * residual, float * y, void * ws, void * stream);
 
+/* dfx_gemm on Q4_K weights whose column tiles may each split their K range (two 2048-element
+ * chunks) over two workgroups of one launch, the later of which adds the two chunk totals in
+ * chunk order and applies the epilogue: the same bits as dfx_gemm, with the workgroups spread
+ * more evenly over the CUs where a whole-tile grid would leave some with one workgroup and
+ * others with two (a scheduling form of the same mul_mat; no counterpart in the reference).
+ * Other weight types, shapes and row counts run as dfx_gemm.  ws: dfx_gemm_ws_bytes(M, N, K)
+ * bytes (2*M*N floats used).  tile_cnt: dfx_gemm_tile_cnt_bytes(M, N) bytes, all zero before
+ * the first call; every call leaves them zero.  Calls sharing tile_cnt or ws must not overlap. */
+size_t dfx_gemm_tile_cnt_bytes(int64_t M, int64_t N);
+int dfx_gemm_counted(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
+                     const float * bias, const float * residual, float * y, void * ws, int32_t * tile_cnt,
+                     void * stream);
+
 /* GEMM of a fused gate|up matrix with the SwiGLU of the FFN (src/diffuse-graph.cpp:136-139:
  * silu(gate) * up of two ggml_mul_mat results) applied to the accumulators before they are
  * stored.  W: device-layout [N][K] whose rows are gate and up interleaved in blocks of 16

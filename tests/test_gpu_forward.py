@@ -247,8 +247,8 @@ class Replay:
     on the oracle, but unmasking what the GPU unmasked (teacher forcing).  At every step
     the GPU's choice must be the oracle's, except across near-ties of the ordering key."""
 
-    def __init__(self, om, prompt, n_gen, p):
-        self.om, self.p = om, p
+    def __init__(self, om, prompt, n_gen, p, n_threads=8):
+        self.om, self.p, self.n_threads = om, p, n_threads
         self.P, self.N = len(prompt), len(prompt) + n_gen
         self.V = om.dims["V"]
         self.mask = int(om.m.mask_token_id)
@@ -280,11 +280,12 @@ class Replay:
             if len(act) >= self.N or not act:
                 full = True
         if full:
-            self.logits[:] = self._full_kv() if p["use_cache"] else self.om.forward_full(self.seq)
+            self.logits[:] = self._full_kv() if p["use_cache"] else self.om.forward_full(self.seq,
+                                                                                           n_threads=self.n_threads)
             self.rows.append(self.N)
         else:
             act = np.array(act, np.int32)
-            self.logits[act] = self.om.forward_cached(self.kv, self.seq[act], act, self.N)
+            self.logits[act] = self.om.forward_cached(self.kv, self.seq[act], act, self.N, n_threads=self.n_threads)
             self.rows.append(len(act))
         if p["use_cache"]:
             self.prev = self.seq.copy()
@@ -298,7 +299,7 @@ class Replay:
         return cand
 
     def _full_kv(self):
-        logits, kv = self.om.forward_full(self.seq, kv_tokens=self.N)
+        logits, kv = self.om.forward_full(self.seq, kv_tokens=self.N, n_threads=self.n_threads)
         self.kv = kv
         return logits
 

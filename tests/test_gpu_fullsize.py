@@ -11,7 +11,9 @@ against the oracle: the first (full) denoising step and one cached step of
 Bar: rel-L2 <= 1e-2 and >= 99% argmax agreement on the rows the sampler reads; the
 quantised models are expected (and asserted) to give the oracle's floats exactly.
 Weights are random-init N(0, 0.02) (seed 0 for LLaDA, as the benchmark; 2 Dream; 5 the
-batched unit), norms 1.0; files are generated once per machine (about 30 s each)."""
+batched unit), norms 1.0; files are generated once per machine (about 30 s each).
+Progress lines (model ready, oracle pass done, step replayed) go straight to the terminal
+(`say`, output capture bypassed), so a run that takes minutes of host time is never silent."""
 import numpy as np
 import pytest
 
@@ -24,18 +26,26 @@ pytestmark = pytest.mark.gpu
 THREADS = 16
 
 
-def _report(tag, got, ref, rows):
+@pytest.fixture
+def say(capfd):
+    def _say(msg):
+        with capfd.disabled():
+            print(f"[fullsize] {msg}", flush=True)
+    return _say
+
+
+def _report(say, tag, got, ref, rows):
     err = rel_l2(got, ref)
     agree = float(np.mean(got[rows].argmax(1) == ref[rows].argmax(1)))
     same = float(np.mean(got == ref))
-    print(f"[fullsize] {tag}: rel-L2 {err:.3e}, argmax agreement {agree:.4f} on {len(rows)} rows, "
-          f"identical floats {same:.6f}", flush=True)
+    say(f"{tag}: rel-L2 {err:.3e}, argmax agreement {agree:.4f} on {len(rows)} rows, identical floats {same:.6f}")
     assert err <= 1e-2, (tag, err)
     assert agree >= 0.99, (tag, agree)
     return same
 
 
-def _step0_and_cached(path, P, B, prompt_seed, vocab_hi, n_unmask, exact):
+def _step0_and_cached(say, path, P, B, prompt_seed, vocab_hi, n_unmask, exact):
+    say(f"model ready: {path}")
     om = O.OracleModel(path)
     V, mask = om.dims["V"], int(om.m.mask_token_id)
     shift = bool(om.m.is_dream)
@@ -47,9 +57,10 @@ def _step0_and_cached(path, P, B, prompt_seed, vocab_hi, n_unmask, exact):
     try:
         # step 0: full forward over every position
         ref, kv = om.forward_full(seq, kv_tokens=N, n_threads=THREADS)
+        say(f"oracle step 0 done (M={N})")
         got = ctx.forward(seq)
         read = np.array([max(i - 1, 0) if shift else i for i in range(P, N)])   # rows the sampler reads
-        same = _report(f"step 0 (M={N})", got, ref, read)
+        same = _report(say, f"step 0 (M={N})", got, ref, read)
         if exact:
             assert same == 1.0
         # unmask the n_unmask most confident masked positions (low_confidence), as step 0 would
@@ -59,10 +70,11 @@ def _step0_and_cached(path, P, B, prompt_seed, vocab_hi, n_unmask, exact):
         # step 1: cached forward over the still-masked and the just-changed positions
         act = np.arange(P, N, dtype=np.int32)
         ref1 = om.forward_cached(kv, seq[act], act, N, n_threads=THREADS)
+        say(f"oracle cached step done (M={len(act)})")
         got1 = ctx.forward_cached(seq[act], act, N)
         masked = np.setdiff1d(act, pick)
         rows1 = np.searchsorted(act, np.array([max(i - 1, P) if shift else i for i in masked]))
-        same = _report(f"cached step (M={len(act)} of {N})", got1, ref1, rows1)
+        same = _report(say, f"cached step (M={len(act)} of {N})", got1, ref1, rows1)
         if exact:
             assert same == 1.0
     finally:
@@ -70,31 +82,36 @@ def _step0_and_cached(path, P, B, prompt_seed, vocab_hi, n_unmask, exact):
         model.close()
 
 
-def test_llada8b_q4km_step0_and_cached_step(gpu):
+def test_llada8b_q4km_step0_and_cached_step(gpu, say):
+    say("model llada8b q4_k_m seed 0 (generated on first use)")
     path = big_model("llada8b", dfx.LLADA_8B, "q4_k_m", 0)
-    _step0_and_cached(path, 32, 256, 1, 126000, 1, exact=True)
+    _step0_and_cached(say, path, 32, 256, 1, 126000, 1, exact=True)
 
 
-def test_dream7b_q4km_step0_and_cached_step(gpu):
+def test_dream7b_q4km_step0_and_cached_step(gpu, say):
+    say("model dream7b q4_k_m seed 2 (generated on first use)")
     path = big_model("dream7b", dfx.DREAM_7B, "q4_k_m", 2)
-    _step0_and_cached(path, 64, 64, 3, 151643, 1, exact=True)
+    _step0_and_cached(say, path, 64, 64, 3, 151643, 1, exact=True)
 
 
-def test_llada8b_q8_0_long_context_unit(gpu):
+def test_llada8b_q8_0_long_context_unit(gpu, say):
+    say("model llada8b q8_0 seed 5 (generated on first use)")
     path = big_model("llada8b", dfx.LLADA_8B, "q8_0", 5)
-    _step0_and_cached(path, 512, 256, 5, 126000, 1, exact=True)
+    _step0_and_cached(say, path, 512, 256, 5, 126000, 1, exact=True)
 
 
-def test_llada8b_width_f16_long_context_unit(gpu):
+def test_llada8b_width_f16_long_context_unit(gpu, say):
     arch = dict(dfx.LLADA_8B, n_layer=2)
+    say("model llada8b-2l f16 seed 5 (generated on first use)")
     path = big_model("llada8b-2l", arch, "f16", 5)
-    _step0_and_cached(path, 512, 256, 5, 126000, 1, exact=False)
+    _step0_and_cached(say, path, 512, 256, 5, 126000, 1, exact=False)
 
 
-def test_dream7b_q4km_autoregressive_prefill_and_decode(gpu):
+def test_dream7b_q4km_autoregressive_prefill_and_decode(gpu, say):
     """The autoregressive path at Dream-7B size (GQA 28/4, Q/K/V bias, V = 152064): a
     32-token causal prefill, then greedy ar_generate of 4 tokens against the oracle's
     ar_generate (the same floats, so the same tokens)."""
+    say("model dream7b q4_k_m seed 2 (generated on first use)")
     path = big_model("dream7b", dfx.DREAM_7B, "q4_k_m", 2)
     om = O.OracleModel(path)
     prompt = np.random.default_rng(3).integers(0, 151643, 32).astype(np.int32)
@@ -104,18 +121,18 @@ def test_dream7b_q4km_autoregressive_prefill_and_decode(gpu):
         cache = O.OracleArCache(om, 64)
         ref = om.ar_forward(cache, prompt, last_only=True, n_threads=THREADS)
         got = ctx.ar_forward(prompt, reset=True)[-1:]
-        same = _report("ar prefill (M=32, last row)", got, ref, np.arange(1))
+        same = _report(say, "ar prefill (M=32, last row)", got, ref, np.arange(1))
         assert same == 1.0
         ref_toks, _ = om.ar_generate(prompt, 4, O.OrcArParams.make(), n_threads=THREADS)
         got_toks = ctx.ar_generate(prompt, 4, dfx.ArParams.make())
-        print(f"[fullsize] ar_generate greedy: {list(got_toks)} vs oracle {list(ref_toks)}", flush=True)
+        say(f"ar_generate greedy: {list(got_toks)} vs oracle {list(ref_toks)}")
         assert list(got_toks) == list(ref_toks)
     finally:
         ctx.close()
         model.close()
 
 
-def test_llada8b_q4km_benchmark_generation_replays_through_oracle(gpu):
+def test_llada8b_q4km_benchmark_generation_replays_through_oracle(gpu, say):
     """The benchmark's own generation end to end: LLaDA-8B Q4_K_M (the bench's model file and
     prompt), 32 + 256 masks, 16 steps, entropy_exit with the inter-step cache, through the
     default device-resident loop with graph replays, replayed step by step through the
@@ -127,6 +144,7 @@ def test_llada8b_q4km_benchmark_generation_replays_through_oracle(gpu):
     sequential float sums and the GPU's double sums (more accurate) part; the step-0 entropies
     are compared directly (relative difference below 1e-4)."""
     from test_gpu_forward import Replay, key_of
+    say("model llada8b q4_k_m seed 0 (generated on first use)")
     path = big_model("llada8b", dfx.LLADA_8B, "q4_k_m", 0)
     om = O.OracleModel(path)
     P, B, S = 32, 256, 16
@@ -149,11 +167,11 @@ def test_llada8b_q4km_benchmark_generation_replays_through_oracle(gpu):
         ent_ref = np.array([O.entropy(r) for r in lg], np.float32)
         rel = float(np.max(np.abs(ent_gpu - ent_ref) / np.abs(ent_ref)))
         spread = float(np.max(ent_ref) - np.min(ent_ref))
-        print(f"[fullsize] step-0 entropy: max rel diff GPU vs reference formula {rel:.2e}, "
-              f"rows span {np.min(ent_ref):.6f}..{np.max(ent_ref):.6f}", flush=True)
+        say(f"step-0 entropy: max rel diff GPU vs reference formula {rel:.2e}, "
+            f"rows span {np.min(ent_ref):.6f}..{np.max(ent_ref):.6f}")
         assert rel < 1e-4
         pd = dict(use_cache=True, cache_refresh=0, cache_keep_active=0, remasking=dfx.ENTROPY_EXIT)
-        rep = Replay(om, prompt, B, pd)
+        rep = Replay(om, prompt, B, pd, n_threads=THREADS)
         n_masked, n_cut_diff = B, 0
         for s in range(S):
             if n_masked == 0:
@@ -178,10 +196,10 @@ def test_llada8b_q4km_benchmark_generation_replays_through_oracle(gpu):
                 rep.seq[i] = toks[i - P]
                 rep.masked[i] = False
             n_masked -= len(gpu_set)
-            print(f"[fullsize] replayed step {s}: {rep.rows[-1]} rows, {len(gpu_set)} unmasked", flush=True)
+            say(f"replayed step {s}: {rep.rows[-1]} rows, {len(gpu_set)} unmasked")
         assert n_masked == 0
-        print(f"[fullsize] benchmark generation replayed: {st.actual_steps} steps, positions chosen across "
-              f"entropy near-ties at the cut: {n_cut_diff}", flush=True)
+        say(f"benchmark generation replayed: {st.actual_steps} steps, positions chosen across "
+            f"entropy near-ties at the cut: {n_cut_diff}")
     finally:
         ctx.close()
         model.close()

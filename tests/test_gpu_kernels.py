@@ -673,3 +673,51 @@ def test_gemm_f32_matches_oracle(gpu, N, K, M):
     assert rel_l2(got, ref) < 1e-5, rel_l2(got, ref)
     f64 = X.astype(np.float64) @ W.astype(np.float64).T
     assert rel_l2(got, f64) < 1e-5
+
+
+# (N, K, M, forced tile): Q|K|V at 256 and 288 rows and gate|up at 288 rows (the default rule
+# splits tiles: 384 / 480 / 960 tiles over 512 workgroup slots), Dream-7B's K = 3584 (a short
+# second chunk), every tile split (forced, 64 and 1 tile rows), ragged M; N off a multiple of
+# 128 and one-chunk K run as dfx_gemm
+COUNTED_CASES = [(12288, 4096, 256, None), (12288, 4096, 288, None), (24576, 4096, 288, None),
+                 (4608, 3584, 200, "w1f"), (4096, 4096, 77, "w1f"), (2048, 4096, 33, "w1f"), (1024, 4096, 300, "w1f"),
+                 (1000, 4096, 100, "w1f"), (512, 2048, 70, "w1f")]
+
+
+@pytest.mark.parametrize("N,K,M,tile", COUNTED_CASES)
+def test_gemm_counted_equals_dfx_gemm(gpu, N, K, M, tile):
+    """dfx_gemm_counted (column tiles split over two workgroups of one launch, the later adding
+    the chunk totals) gives dfx_gemm's bits, with bias and an in-place residual, on two calls in
+    a row; the tile counters are zero again after each call."""
+    typ = dfx.TYPE_Q4_K
+    raw = quant(typ, N, K)
+    w = to_device_weights(typ, raw, N, K)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    r0 = rng.standard_normal((M, N)).astype(np.float32)
+    xb, ab = dfx.Buf.of(X), dfx.Buf(L().dfx_act_bytes(typ, M, K))
+    dfx.check(L().dfx_act_convert(typ, xb.ptr, M, K, ab.ptr, None), "convert")
+    bb = dfx.Buf.of(bias)
+    ref_b, got_b = dfx.Buf.of(r0), dfx.Buf.of(r0)
+    dfx.check(L().dfx_gemm(typ, w.ptr, N, K, ab.ptr, M, bb.ptr, ref_b.ptr, ref_b.ptr, None, None), "gemm")
+    ref = ref_b.download(np.float32, shape=(M, N))
+    ws = dfx.Buf(L().dfx_gemm_ws_bytes(M, N, K))
+    cnt = dfx.Buf(L().dfx_gemm_tile_cnt_bytes(M, N))
+    cnt.zero()
+    with forced_tile(typ, tile) if tile else contextlib.nullcontext():
+        for call in range(2):
+            got_b.upload(r0)
+            dfx.check(L().dfx_gemm_counted(typ, w.ptr, N, K, ab.ptr, M, bb.ptr, got_b.ptr, got_b.ptr, ws.ptr, cnt.ptr,
+                                           None), "gemm_counted")
+            got = got_b.download(np.float32, shape=(M, N))
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (call, rel_l2(got, ref))
+            assert not cnt.download(np.int32).any()
+    if (N, K, M) == (4096, 4096, 77):
+        plain = dfx.Buf(M * N * 4)
+        cnt.zero()
+        with forced_tile(typ, tile):
+            dfx.check(L().dfx_gemm_counted(typ, w.ptr, N, K, ab.ptr, M, None, None, plain.ptr, ws.ptr, cnt.ptr, None),
+                      "gemm_counted")
+        got = plain.download(np.float32, shape=(M, N))
+        oracle = O.mul_mat(typ, raw, N, K, X)
+        assert np.array_equal(got.view(np.uint32), oracle.view(np.uint32))
