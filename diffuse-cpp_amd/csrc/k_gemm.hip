@@ -1802,21 +1802,24 @@ static int device_cu_count() {
     return v;
 }
 
-// Whole tiles for the first n_full workgroups, half tiles after them, so that the workgroup
-// slots (two per CU) carry about the same number of K steps: T = q S + r tiles over S slots
-// leave r tiles to a last round; n_full = q S + max(0, 2r - S) whole tiles and the rest as
-// halves fill that round with halves instead (r <= S/2: every tile of it split; r > S/2:
-// 2 (S - r) halves beside 2r - S whole tiles).  Returns -1 where no split is taken: the measured wins (MI355X, LLaDA-8B shapes, every result the same bits) are
-// 256 < T <= 512 tiles (Q|K|V at 129-320 rows 6-15 % faster, gate|up at 65-128 rows 16 %)
-// and a last round of at least 3/4 of the slots (gate|up at 288 rows, 5 %); a last round of
-// half the slots (gate|up at 193-256 rows) is 6 % slower split, and at most 256 tiles
-// (one per CU or fewer) gain nothing.
+// Whole tiles for the first n_full workgroups, half tiles after them.  Taken where a grid of
+// whole tiles fills more than half but not all of the workgroup slots (two per CU): S/2 < T
+// <= S tiles, where some CUs would carry two whole tiles and others one.  n_full from a sweep
+// on MI355X at the LLaDA-8B shapes (Q|K|V and gate|up, every result the same bits):
+//   T = 384: 2T - S = 256 whole tiles and 256 halves, one of each per CU (10-16 % faster
+//            than whole tiles; 192 or 288 whole tiles are slower);
+//   T = 288: 3T/4 = 216 whole tiles (15 % faster; 2T - S = 64 gives 8 %);
+//   T = 480: 2T - S = 448 (3 %).
+// Not taken for T <= S/2 (no CU holds two whole tiles; splitting gains nothing) nor above S
+// (a last part-filled round: 0-6 % slower split).  `force` (tests) splits the second half of
+// the tiles of any grid.
 static int split_tile_count(int per_pass, bool force) {
     const int S = 2 * device_cu_count();
-    const int q = per_pass / S, r = per_pass - q * S;
-    if (!force && !(per_pass > S / 2 && per_pass <= S) && !(per_pass > S && 4 * r >= 3 * S)) return -1;
-    const int n_full = q * S + std::max(0, 2 * r - S);
-    return std::min(per_pass, (n_full + 7) / 8 * 8);
+    const int T = per_pass;
+    if (force) return T / 2 / 8 * 8;
+    if (2 * T <= S || T > S) return -1;
+    const int n_full = std::max(2 * T - S, 4 * T <= 5 * S / 2 ? 3 * T / 4 : 0);
+    return std::min(T, (n_full + 7) / 8 * 8);
 }
 
 template <int TM, int TN, int D>

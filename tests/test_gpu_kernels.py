@@ -675,11 +675,11 @@ def test_gemm_f32_matches_oracle(gpu, N, K, M):
     assert rel_l2(got, f64) < 1e-5
 
 
-# (N, K, M, forced tile): Q|K|V at 256 and 288 rows and gate|up at 288 rows (the default rule
-# splits tiles: 384 / 480 / 960 tiles over 512 workgroup slots), Dream-7B's K = 3584 (a short
-# second chunk), every tile split (forced, 64 and 1 tile rows), ragged M; N off a multiple of
-# 128 and one-chunk K run as dfx_gemm
-COUNTED_CASES = [(12288, 4096, 256, None), (12288, 4096, 288, None), (24576, 4096, 288, None),
+# (N, K, M, forced tile): Q|K|V at 181, 256 and 288 rows (the default rule splits some of the
+# 288 / 384 / 480 tiles over 512 workgroup slots) and gate|up at 288 rows (960 tiles: not
+# split); forced (half the tiles split): Dream-7B's K = 3584 (a short second chunk), one and
+# several tile rows, ragged M; N off a multiple of 128 and one-chunk K run as dfx_gemm
+COUNTED_CASES = [(12288, 4096, 256, None), (12288, 4096, 288, None), (12288, 4096, 181, None), (24576, 4096, 288, None),
                  (4608, 3584, 200, "w1f"), (4096, 4096, 77, "w1f"), (2048, 4096, 33, "w1f"), (1024, 4096, 300, "w1f"),
                  (1000, 4096, 100, "w1f"), (512, 2048, 70, "w1f")]
 
