@@ -1935,23 +1935,30 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
     }
     // a 4-deep ring needs a multiple of 4 K steps in every workgroup
     const int sb = K / 256, sb_last = sb - (chunks - 1) * (DFX_DOT_CHUNK / 256);
+    // whole and half tiles in one launch (k_q4k_w): two chunks, tile counters, and room in ws
+    // for both halves' chunk totals
+    const bool halves_ok = epi.tile_cnt && chunks == 2 && N % 128 == 0 && ws &&
+                           ws_bytes >= (size_t)2 * M * N * sizeof(float);
     if (f.on && f.w) {
         // "w": 64 x 64 per wave; "w1": 64 x 32 per wave, two workgroups per CU
         float * wsw = split ? (float *)ws : nullptr;
         if (f.w1) {
-            if (f.halves && epi.tile_cnt && chunks == 2 && N % 128 == 0 && ws &&
-                ws_bytes >= (size_t)2 * M * N * sizeof(float))
+            if (f.halves && halves_ok)
                 return launch_q4k_w<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, (float *)ws, st, defer, epi,
                                              split_tile_count(8 * ((n_col + 7) / 8) * ((M + 63) / 64), true));
             return launch_q4k_w<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer, epi);
         }
-        if (f.w3) return launch_q4k_w<3, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer, epi);
+        if (f.w3) {
+            if (f.halves && halves_ok)
+                return launch_q4k_w<3, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, (float *)ws, st, defer, epi,
+                                             split_tile_count(8 * ((n_col + 7) / 8) * ((M + 95) / 96), true));
+            return launch_q4k_w<3, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer, epi);
+        }
         if (sb_last % 2) return launch_q4k_w<2, 2, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer, epi);
         return launch_q4k_w<2, 2, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsw, st, defer, epi);
     }
     // whole and half tiles in one launch where that evens out the workgroups per CU
-    if (dma && epi.tile_cnt && chunks == 2 && N % 128 == 0 && ws && ws_bytes >= (size_t)2 * M * N * sizeof(float) &&
-        (!f.on || f.got < 2)) {
+    if (dma && halves_ok && (!f.on || f.got < 2)) {
         const int nf = split_tile_count(8 * ((n_col + 7) / 8) * ((M + 63) / 64), f.on && f.halves);
         if (nf >= 0)
             return launch_q4k_w<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, (float *)ws, st, defer, epi, nf);
@@ -1966,9 +1973,13 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
         const int64_t t3 = (int64_t)n_col * ((M + 95) / 96);
         const bool split3 = can_split && (chunks > 2 || t3 < 160);
         const int64_t t_def = (int64_t)n_col * (dma ? (M + 63) / 64 : (M + 31) / 32);
-        if (rounds(t3 * (split3 ? chunks : 1)) < rounds(t_def * (split ? chunks : 1)))
+        if (rounds(t3 * (split3 ? chunks : 1)) < rounds(t_def * (split ? chunks : 1))) {
+            const int n3 = halves_ok ? split_tile_count(8 * ((n_col + 7) / 8) * ((M + 95) / 96), false) : -1;
+            if (n3 >= 0)
+                return launch_q4k_w<3, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, (float *)ws, st, defer, epi, n3);
             return launch_q4k_w<3, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, split3 ? (float *)ws : nullptr, st,
                                          defer, epi);
+        }
     }
     if (dma) return launch_q4k_w<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, split ? (float *)ws : nullptr, st, defer, epi);
     if (cands[pick].d == 4 && (sb_last % 2))

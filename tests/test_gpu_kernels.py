@@ -677,11 +677,12 @@ def test_gemm_f32_matches_oracle(gpu, N, K, M):
 
 # (N, K, M, forced tile): Q|K|V at 181, 256 and 288 rows (the default rule splits some of the
 # 288 / 384 / 480 tiles over 512 workgroup slots) and gate|up at 288 rows (960 tiles: not
-# split); forced (half the tiles split): Dream-7B's K = 3584 (a short second chunk), one and
-# several tile rows, ragged M; N off a multiple of 128 and one-chunk K run as dfx_gemm
+# split), gate|up at 181 rows (96-row tiles, 384 of them: split); forced (half the tiles split):
+# Dream-7B's K = 3584 (a short second chunk), one and several tile rows, ragged M, the 96-row
+# tile; N off a multiple of 128 and one-chunk K run as dfx_gemm
 COUNTED_CASES = [(12288, 4096, 256, None), (12288, 4096, 288, None), (12288, 4096, 181, None), (24576, 4096, 288, None),
                  (4608, 3584, 200, "w1f"), (4096, 4096, 77, "w1f"), (2048, 4096, 33, "w1f"), (1024, 4096, 300, "w1f"),
-                 (1000, 4096, 100, "w1f"), (512, 2048, 70, "w1f")]
+                 (1000, 4096, 100, "w1f"), (512, 2048, 70, "w1f"), (24576, 4096, 181, None), (4096, 4096, 130, "w3f")]
 
 
 @pytest.mark.parametrize("N,K,M,tile", COUNTED_CASES)
