@@ -236,7 +236,7 @@ def test_gemm_bias_and_residual_epilogue(gpu):
 
 
 GEMV_CASES = [(t, N, K, M) for t in (dfx.TYPE_Q4_K, dfx.TYPE_Q6_K)
-              for (N, K) in ((64, 2304), (4608, 3584), (4096, 12288), (1024, 18944)) for M in (1, 2, 3, 4)]
+              for (N, K) in ((64, 2304), (4608, 3584), (96, 8192), (4096, 12288), (1024, 18944)) for M in (1, 2, 3, 4)]
 GEMV_CASES += [(dfx.TYPE_Q6_K, 152064, 3584, 1), (dfx.TYPE_Q4_K, 37888, 3584, 1)]
 
 
@@ -244,7 +244,9 @@ GEMV_CASES += [(dfx.TYPE_Q6_K, 152064, 3584, 1), (dfx.TYPE_Q4_K, 37888, 3584, 1)
 def test_gemv_bit_exact(gpu, typ, N, K, M):
     """At most four rows the matrix-vector kernels run (integer dot products on the int8
     plane, the exact float order over super-blocks and chunks, a short last chunk at
-    K = 2304 / 3584 / 18944): the oracle's values bit for bit, and the same bits as the
+    K = 2304 / 3584 / 18944; one, two and four waves per column pair at 1, 2 and 3-5
+    passes of 4096 elements): the oracle's
+    values bit for bit, and the same bits as the
     matrix-core kernel forced by a tile override."""
     raw = quant(typ, N, K)
     X = rng.standard_normal((M, K)).astype(np.float32)
