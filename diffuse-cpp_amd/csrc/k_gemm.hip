@@ -2037,6 +2037,19 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
+// v + (v of lane ^ 1), then + (lane ^ 2): the four lanes of a quad end with their sum
+// (DPP quad permutes, no LDS traffic)
+__device__ __forceinline__ int quad_sum(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1, 0, 3, 2]
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm [2, 3, 0, 1]
+    return v;
+}
+
+// the value of a lane known at compile time, as a wave-uniform value
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
 // One output of the matrix-vector kernels through the epilogue: v = row m at column n,
 // w = row m at the paired column n ^ 16 (the SwiGLU up value, or the other dim of the RoPE
 // pair).  Float expressions as in epilogue_tile / rope_tile / k_gemm_reduce.
@@ -2189,12 +2202,9 @@ __global__ void __launch_bounds__(256) k_gemv(const uint8_t * __restrict__ W, in
             // the super-block's four lanes (consecutive) hold its four groups
 #pragma unroll
             for (int m = 0; m < MR; m++) {
-                int is = isum[m], ms = msum[m];
-                is += __shfl_xor(is, 1, WAVE);
-                is += __shfl_xor(is, 2, WAVE);
+                const int is = quad_sum(isum[m]);
                 if constexpr (Q4) {
-                    ms += __shfl_xor(ms, 1, WAVE);
-                    ms += __shfl_xor(ms, 2, WAVE);
+                    const int ms = quad_sum(msum[m]);
                     x[c][m] = fmaf(-dmw, (float)ms, dw * (float)is);
                 } else {
                     x[c][m] = dw * (float)is;
@@ -2217,7 +2227,7 @@ __global__ void __launch_bounds__(256) k_gemv(const uint8_t * __restrict__ W, in
                 for (int m = 0; m < MR; m++) {
                     const float da = ad[(int64_t)(first + i) * Lay.mq + min(m, M - 1)];
 #pragma unroll
-                    for (int c = 0; c < 2; c++) S[c][m] = fmaf(da, __shfl(x[c][m], 32 * h + 4 * i, WAVE), S[c][m]);
+                    for (int c = 0; c < 2; c++) S[c][m] = fmaf(da, lane_value(x[c][m], 32 * h + 4 * i), S[c][m]);
                 }
             }
             if constexpr (WS == 1) {
