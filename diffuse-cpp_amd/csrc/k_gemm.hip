@@ -2212,6 +2212,10 @@ __global__ void __launch_bounds__(256) k_gemv(const uint8_t * __restrict__ W, in
                 if (!live) x[c][m] = 0.0f;
             }
         }
+        // each lane's super-block scale of the activation rows, loaded together for the pass
+        float dam[MR];
+#pragma unroll
+        for (int m = 0; m < MR; m++) dam[m] = ad[(int64_t)sbc * Lay.mq + min(m, M - 1)];
         // the pass's two chunks of 8 super-blocks: S = fma(d_a, x, S) in order, T = T + S
 #pragma unroll
         for (int h = 0; h < 2; h++) {
@@ -2225,7 +2229,7 @@ __global__ void __launch_bounds__(256) k_gemv(const uint8_t * __restrict__ W, in
             for (int i = 0; i < 8 && first + i < nsb; i++) {
 #pragma unroll
                 for (int m = 0; m < MR; m++) {
-                    const float da = ad[(int64_t)(first + i) * Lay.mq + min(m, M - 1)];
+                    const float da = lane_value(dam[m], 32 * h + 4 * i);
 #pragma unroll
                     for (int c = 0; c < 2; c++) S[c][m] = fmaf(da, lane_value(x[c][m], 32 * h + 4 * i), S[c][m]);
                 }
