@@ -2021,16 +2021,17 @@ static int dispatch_mmq(const void * w, int N, int K, const void * act, int M, c
 // One wave per pair of output columns (n, n + 16) and pass set, n = 32 (p / 16) + p % 16 for
 // pair p: the pairs the SwiGLU and RoPE epilogues combine.  A pass is 16 super-blocks (two
 // chunks of 2048); lane l takes the 64-element group l % 4 of super-block l / 4 of each
-// pass, for both columns and all rows.  With WS > 1 the workgroup's four waves hold 4 / WS
-// pairs and the WS waves of a pair take every WS-th pass, so long rows (the FFN down
-// projection) keep WS times as many weight loads in flight.  Integer dot products come from
-// v_dot4_i32_i8 on the natural-order int8 activation plane (nibbles and 6-bit quants are
-// non-negative bytes), exactly, in int32; the four lanes of a super-block add them (xor
-// shuffles), and every lane then runs the exact float order over the super-blocks of each
-// chunk (shuffled from the lanes that hold them): x = d_w*isum (Q4_K: x = fma(-dmin_w,
-// msum, x)); S = fma(d_a, x, S).  The chunk sums are added in chunk order, T = T + S, in the
-// wave (WS = 1) or, after a barrier, from LDS by the pair's first wave.  No MFMA: at these
-// row counts the weights' HBM stream sets the time.
+// pass, for both columns and all rows.  Rows of one pass: four pairs per workgroup, a wave
+// each.  Longer rows (SPLIT, e.g. the FFN down projection): a workgroup per pair with one
+// wave per pass (up to 16, each taking every ws-th pass beyond that), so every pass's weight
+// loads are in flight at once.  Integer dot products come from v_dot4_i32_i8 on the
+// natural-order int8 activation plane (nibbles and 6-bit quants are non-negative bytes),
+// exactly, in int32; the four lanes of a super-block add them (DPP quad permutes), and every
+// lane then runs the exact float order over the super-blocks of each chunk (x and d_a read
+// from the lanes that hold them): x = d_w*isum (Q4_K: x = fma(-dmin_w, msum, x));
+// S = fma(d_a, x, S).  The chunk sums are added in chunk order, T = T + S, in the wave or,
+// after a barrier, from LDS by the pair's first wave.  No MFMA: at these row counts the
+// weights' HBM stream sets the time.
 constexpr int GEMV_MAX_CHUNKS = 64;     // K <= 131072 for the pass-split form
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
@@ -2087,8 +2088,8 @@ __device__ __forceinline__ void gemv_store(float v, float w, int m, int n, int N
     Y[o] = v;
 }
 
-template <int WT, int MR, int WS>
-__global__ void __launch_bounds__(256) k_gemv(const uint8_t * __restrict__ W, int N, int K,
+template <int WT, int MR, bool SPLIT>
+__global__ void __launch_bounds__(1024) k_gemv(const uint8_t * __restrict__ W, int N, int K,
                                               const uint8_t * __restrict__ act, int M, const float * __restrict__ bias,
                                               const float * res, float * Y, int64_t ldy,
                                               const int32_t * __restrict__ ymap, dfx_epi epi) {
@@ -2096,9 +2097,10 @@ __global__ void __launch_bounds__(256) k_gemv(const uint8_t * __restrict__ W, in
     constexpr bool Q4 = WT == DFX_TYPE_Q4_K;
     constexpr int SB = Q4 ? SB_Q4_K : SB_Q6_K;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int p = blockIdx.x * (4 / WS) + wv / WS, part = wv % WS;
+    const int ws = SPLIT ? (int)(blockDim.x >> 6) : 1;   // waves per pair
+    const int p = SPLIT ? (int)blockIdx.x : (int)blockIdx.x * 4 + wv, part = SPLIT ? wv : 0;
     const bool pair_live = p < N / 2;                    // the whole wave
-    if (WS == 1 && !pair_live) return;
+    if (!SPLIT && !pair_live) return;
     const int ncol[2] = {32 * (p >> 4) + (p & 15), 32 * (p >> 4) + (p & 15) + 16};
     const int nsb = K >> 8, g = lane & 3, sbl = lane >> 2;
     const act_layout Lay = act_layout_of(Q4 ? CONV_Q8_K_P4 : CONV_Q8_K_P6, M, K);
@@ -2106,14 +2108,14 @@ __global__ void __launch_bounds__(256) k_gemv(const uint8_t * __restrict__ W, in
     const float * ad = (const float *)(act + Lay.d);     // [nsb][mq]
     const uint16_t * abs = (const uint16_t *)(act + Lay.bs);   // [M][K/16], exact small integers
     const int64_t rb = (int64_t)nsb * SB;
-    [[maybe_unused]] __shared__ float sS[WS > 1 ? 4 / WS * GEMV_MAX_CHUNKS * 2 * MR : 1];
+    [[maybe_unused]] __shared__ float sS[SPLIT ? GEMV_MAX_CHUNKS * 2 * MR : 1];
     float T[2][MR];
 #pragma unroll
     for (int c = 0; c < 2; c++)
 #pragma unroll
         for (int m = 0; m < MR; m++) T[c][m] = 0.0f;
 
-    for (int sb0 = 16 * part; pair_live && sb0 < nsb; sb0 += 16 * WS) {
+    for (int sb0 = 16 * part; pair_live && sb0 < nsb; sb0 += 16 * ws) {
         const int sbc = min(sb0 + sbl, nsb - 1);          // clamped: lanes past the end add nothing
         const bool live = sb0 + sbl < nsb;
         float x[2][MR];
@@ -2234,13 +2236,13 @@ __global__ void __launch_bounds__(256) k_gemv(const uint8_t * __restrict__ W, in
                     for (int c = 0; c < 2; c++) S[c][m] = fmaf(da, lane_value(x[c][m], 32 * h + 4 * i), S[c][m]);
                 }
             }
-            if constexpr (WS == 1) {
+            if constexpr (!SPLIT) {
 #pragma unroll
                 for (int c = 0; c < 2; c++)
 #pragma unroll
                     for (int m = 0; m < MR; m++) T[c][m] = T[c][m] + S[c][m];
             } else if (lane == 0) {
-                float * d = sS + ((wv / WS) * GEMV_MAX_CHUNKS + (first >> 3)) * 2 * MR;
+                float * d = sS + (first >> 3) * 2 * MR;
 #pragma unroll
                 for (int c = 0; c < 2; c++)
 #pragma unroll
@@ -2248,10 +2250,10 @@ __global__ void __launch_bounds__(256) k_gemv(const uint8_t * __restrict__ W, in
             }
         }
     }
-    if constexpr (WS > 1) {
+    if constexpr (SPLIT) {
         __syncthreads();
         if (part != 0 || !pair_live) return;
-        const float * d = sS + (wv / WS) * GEMV_MAX_CHUNKS * 2 * MR;
+        const float * d = sS;
         for (int ch = 0; ch < (nsb + 7) >> 3; ch++)
 #pragma unroll
             for (int c = 0; c < 2; c++)
@@ -2269,14 +2271,16 @@ __global__ void __launch_bounds__(256) k_gemv(const uint8_t * __restrict__ W, in
 template <int WT>
 static int launch_gemv(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                        float * y, int64_t ldy, const int32_t * ymap, hipStream_t st, dfx_epi epi) {
-    // waves per pair: the passes, up to four (powers of two)
+    // waves per pair: one per pass of 16 super-blocks, up to 16 (a workgroup per pair); one
+    // pass: four pairs per workgroup, one wave each
     const int passes = (K / 256 + 15) / 16;
-    const int ws = K / 2048 + 1 > GEMV_MAX_CHUNKS || passes == 1 ? 1 : passes == 2 ? 2 : 4;
-    const dim3 grid((unsigned)((N / 2 + 4 / ws - 1) / (4 / ws)));
+    const bool split = passes > 1 && (K / 256 + 7) / 8 <= GEMV_MAX_CHUNKS;
+    const int ws = split ? std::min(passes, 16) : 1;
+    const dim3 grid((unsigned)(split ? N / 2 : (N / 2 + 3) / 4)), block((unsigned)(split ? 64 * ws : 256));
     const uint8_t * W = (const uint8_t *)w;
     const uint8_t * A = (const uint8_t *)act;
-#define GEMV_CASE(mr, wsv) hipLaunchKernelGGL((k_gemv<WT, mr, wsv>), grid, dim3(256), 0, st, W, N, K, A, M, bias, res, y, ldy, ymap, epi)
-#define GEMV_WS(mr) if (ws == 1) GEMV_CASE(mr, 1); else if (ws == 2) GEMV_CASE(mr, 2); else GEMV_CASE(mr, 4)
+#define GEMV_CASE(mr, sp) hipLaunchKernelGGL((k_gemv<WT, mr, sp>), grid, block, 0, st, W, N, K, A, M, bias, res, y, ldy, ymap, epi)
+#define GEMV_WS(mr) if (split) GEMV_CASE(mr, true); else GEMV_CASE(mr, false)
     switch (M) {
         case 1: GEMV_WS(1); break;
         case 2: GEMV_WS(2); break;
