@@ -1133,7 +1133,18 @@ k_q4k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
                               nullptr, ws, cpart, lane, epi);
         __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm(0, 15));
         __syncthreads();
-        if (tid == 0) first = __hip_atomic_fetch_add(cnt + 32 * L, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0;
+        if (tid == 0) {
+            // The handover relies on both halves sharing one L2, i.e. on workgroup L being
+            // dispatched to XCD L mod 8.  Each half adds 1 + 16 * (its XCC id) to the counter;
+            // the later half compares the earlier one's id with its own and, if they differ
+            // (the totals it is about to read may be stale), raises the sticky flag cnt[1],
+            // which the host checks after the pass.
+            const int xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20) & 15;   // HW_REG_XCC_ID[3:0]
+            const int old = __hip_atomic_fetch_add(cnt + 32 * L, 1 + 16 * xcc, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+            first = old == 0;
+            if (!first && (old >> 4) != xcc) cnt[1] = 1;
+        }
         __syncthreads();
         if (first) return;
         const float * other = ws + (int64_t)(1 - cpart) * M * N;
@@ -1696,6 +1707,20 @@ static int reduce_or_defer(const void * ws, int S, int M, int N, const float * b
     return DFX_OK;
 }
 
+// K slices of an F16 GEMM with TM row tiles per workgroup: K is split while the grid is
+// smaller than the CU count, ws_bytes holds the partials and every slice keeps at least 4
+// K steps.  (f32 sums: the slice count decides the summation order, hence the bits.)
+static int f16_splits(int TM, int64_t M, int64_t N, int64_t K, size_t ws_bytes) {
+    const int64_t tiles = ((N + 127) / 128) * ((M + 32 * TM - 1) / (32 * TM));
+    const int n_kt = (int)(K / BK);
+    int S = 1;
+    while (S < MAX_SPLIT && tiles * S < 256 && n_kt / (S * 2) >= 4 &&
+           (size_t)(S * 2) * M * N * sizeof(float) <= ws_bytes)
+        S *= 2;
+    const int per = (n_kt + S - 1) / S;
+    return (n_kt + per - 1) / per;
+}
+
 template <int TM>
 static int launch_f16(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                       float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer,
@@ -1703,17 +1728,8 @@ static int launch_f16(const void * w, int N, int K, const void * act, int M, con
     constexpr int BM = TM * 32, BN = 128;
     const int gx = (N + BN - 1) / BN, gy = (M + BM - 1) / BM;
     const int n_kt = K / BK;
-    int S = 1;
-    if (ws) {
-        // split K while the grid is smaller than the CU count, the workspace holds the
-        // partials and every split keeps at least 4 K steps
-        const int tiles = gx * gy;
-        while (S < MAX_SPLIT && tiles * S < 256 && n_kt / (S * 2) >= 4 &&
-               (size_t)(S * 2) * M * N * sizeof(float) <= ws_bytes)
-            S *= 2;
-    }
+    const int S = f16_splits(TM, M, N, K, ws ? ws_bytes : 0);
     const int per = (n_kt + S - 1) / S;
-    S = (n_kt + per - 1) / per;
     hipLaunchKernelGGL((k_gemm_f16<TM>), dim3(gx, gy, S), dim3(256), 0, st, (const uint8_t *)w, N, K,
                        (const half_t *)act, M, bias, res, y, ldy, ymap, (float *)ws, per, epi);
     DFX_CHECK_LAUNCH("dfx_gemm f16");
@@ -1876,10 +1892,11 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
                         float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer,
                         dfx_epi epi) {
     struct cand { int tm, tn, d; };
-    // (a 96-row tile, TM = 3, spills its sums at two workgroups per CU and is not built)
-    static const cand cands[] = {{2, 2, 2}, {4, 1, 2}, {2, 1, 2}, {1, 2, 2}, {1, 1, 4}, {1, 1, 2}, {2, 1, 4}, {2, 2, 4}};
-    constexpr int n_cand = 8;
-    enum { C_2x1x2 = 2, C_1x1x4 = 4, C_1x1x2 = 5 };
+    // (a 96-row tile, TM = 3, spills its sums at two workgroups per CU and is not built; nor is
+    // 32 x 64 per wave, TM = 1, TN = 2, whose two-deep ring spills 68 registers)
+    static const cand cands[] = {{2, 2, 2}, {4, 1, 2}, {2, 1, 2}, {1, 1, 4}, {1, 1, 2}, {2, 1, 4}, {2, 2, 4}};
+    constexpr int n_cand = 7;
+    enum { C_2x1x2 = 2, C_1x1x4 = 3, C_1x1x2 = 4 };
     // Kernel and split choice, from a warmed-up sweep of every variant on MI355X over
     // the LLaDA-8B shapes (N 4096 / 12288 / 24576, K 4096 / 12288) and the row counts
     // of a 16-step, 256-mask generation (M 50..288), kept where the whole generation
@@ -1989,8 +2006,8 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
 #define Q4K_CASE(c, TM_, TN_, D_) \
     case c: return launch_q4k<TM_, TN_, D_>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi);
     switch (pick) {
-        Q4K_CASE(0, 2, 2, 2) Q4K_CASE(1, 4, 1, 2) Q4K_CASE(2, 2, 1, 2) Q4K_CASE(3, 1, 2, 2) Q4K_CASE(4, 1, 1, 4)
-        Q4K_CASE(6, 2, 1, 4) Q4K_CASE(7, 2, 2, 4)
+        Q4K_CASE(0, 2, 2, 2) Q4K_CASE(1, 4, 1, 2) Q4K_CASE(2, 2, 1, 2) Q4K_CASE(3, 1, 1, 4)
+        Q4K_CASE(5, 2, 1, 4) Q4K_CASE(6, 2, 2, 4)
         default: return launch_q4k<1, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi);
     }
 #undef Q4K_CASE
@@ -2436,25 +2453,37 @@ extern "C" int dfx_gemm_noalloc(int wtype, const void * w, int64_t N, int64_t K,
         return DFX_ERR_HIP;
     }
     std::call_once(scratch_once[dev], [dev] {
+        // The first call on a device may come while the caller captures a stream: the
+        // lookup is not a stream operation, so this thread's capture mode is relaxed around
+        // it (and restored) rather than letting a global-mode capture reject it.
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        const bool exchanged = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
         void * p = nullptr;
         scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         scratch_ptr[dev] = scratch_err[dev] == hipSuccess ? p : nullptr;
+        if (exchanged) (void)hipThreadExchangeStreamCaptureMode(&mode);
     });
     if (!scratch_ptr[dev]) {
         dfx_set_error("dfx_gemm_noalloc: device %d scratch address: %s", dev, hipGetErrorString(scratch_err[dev]));
         return DFX_ERR_HIP;
     }
-    // the split-K partial slices (one per K chunk, every element written by its chunk's
-    // workgroups before the reduction reads it) must fit the scratch array
-    const size_t need = (size_t)std::max<int64_t>(M, 0) * (size_t)std::max<int64_t>(N, 0) *
-                        (size_t)dot_chunks(std::max<int64_t>(K, 1)) * sizeof(float);
-    if (need > DFX_GEMM_SCRATCH_BYTES) {
-        dfx_set_error("dfx_gemm_noalloc: M*N*chunks*4 = %zu bytes exceeds the %u-byte scratch (M=%lld N=%lld K=%lld)",
-                      need, DFX_GEMM_SCRATCH_BYTES, (long long)M, (long long)N, (long long)K);
-        return DFX_ERR_ARG;
+    // Quantised weights: the chunk sums are added in chunk order whether K is split or not,
+    // so a workspace too small for the split dfx_gemm would choose only makes the dispatch
+    // keep K whole, with the same bits.  F16: the slice count decides the f32 summation
+    // order, so the split dfx_gemm would choose must fit the array.  F32 and Q8_0 use no
+    // workspace.
+    const size_t full = M > 0 && N > 0 && K > 0 ? dfx_gemm_ws_bytes(M, N, K) : 0;
+    if (wtype == DFX_TYPE_F16 && M > 0 && N > 0 && K > 0 && K % 256 == 0) {
+        const int S = f16_splits(pick_tm((int)std::min<int64_t>(M, INT32_MAX), 4), M, N, K, full);
+        const size_t need = S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
+        if (need > DFX_GEMM_SCRATCH_BYTES) {
+            dfx_set_error("dfx_gemm_noalloc: the F16 split's partial sums (%d slices, %zu bytes) exceed the %u-byte "
+                          "scratch (M=%lld N=%lld K=%lld)", S, need, DFX_GEMM_SCRATCH_BYTES, (long long)M,
+                          (long long)N, (long long)K);
+            return DFX_ERR_ARG;
+        }
     }
-    // the same workspace size as dfx_gemm's (when it fits), so the same split is chosen
-    const size_t ws_bytes = std::min<size_t>(dfx_gemm_ws_bytes(M, N, K), DFX_GEMM_SCRATCH_BYTES);
+    const size_t ws_bytes = std::min<size_t>(full, DFX_GEMM_SCRATCH_BYTES);
     return dfx_gemm_ex(wtype, w, N, K, act, M, bias, residual, y, N, nullptr, scratch_ptr[dev], ws_bytes, stream,
                        nullptr, nullptr);
 }

@@ -189,7 +189,9 @@ __global__ void k_act_convert(int mode, const float * x, int64_t M, int64_t K, u
 
 // RMSNorm + weight + conversion; one workgroup of up to 16 waves per row.  Wave wv
 // owns the BPW consecutive 256-element blocks from wv*BPW; x and w are loaded once,
-// before the row reduction, and kept in registers for the scaling pass.
+// before the row reduction, and kept in registers for the scaling pass (with 8 blocks per
+// wave, rows above 16384, w is read in the scaling pass instead: 16 waves of 1024 threads
+// leave 128 registers per lane, which x and w of 8 blocks together would overflow).
 // GGML ggml_compute_forward_rms_norm_f32: sum += (double)(x*x); mean = (float)(sum/K);
 // scale = 1.0f/sqrtf(mean + eps); y = x*scale; then ggml_mul by w.
 // Output row m normalises input row r = xmap[m] (or m).  With n_part > 0 the row is first
@@ -207,12 +209,13 @@ __global__ void __launch_bounds__(1024) k_rmsnorm_convert(int mode, float * x, c
     const int nb = (int)(K >> 8);
     const int64_t r = xmap ? xmap[m] : m;
     float * xr = x + r * K;
-    float4 t[BPW], g[BPW];
+    constexpr bool KEEP_W = BPW < 8;
+    float4 t[BPW], g[KEEP_W ? BPW : 1];
 #pragma unroll
     for (int j = 0; j < BPW; j++) {
         const int b = min(wv * BPW + j, nb - 1);   // clamped: the duplicate is not summed or stored
         t[j] = *(const float4 *)(xr + (int64_t)b * 256 + 4 * lane);
-        g[j] = *(const float4 *)(w + (int64_t)b * 256 + 4 * lane);
+        if constexpr (KEEP_W) g[j] = *(const float4 *)(w + (int64_t)b * 256 + 4 * lane);
     }
     if (n_part > 0) {
         const float * pr = part + r * K + 4 * lane;
@@ -266,8 +269,9 @@ __global__ void __launch_bounds__(1024) k_rmsnorm_convert(int mode, float * x, c
     for (int j = 0; j < BPW; j++) {
         const int b = wv * BPW + j;
         if (b < nb) {
-            const float v[4] = {(t[j].x * scale) * g[j].x, (t[j].y * scale) * g[j].y, (t[j].z * scale) * g[j].z,
-                                (t[j].w * scale) * g[j].w};
+            const float4 gw = KEEP_W ? g[KEEP_W ? j : 0] : *(const float4 *)(w + (int64_t)b * 256 + 4 * lane);
+            const float v[4] = {(t[j].x * scale) * gw.x, (t[j].y * scale) * gw.y, (t[j].z * scale) * gw.z,
+                                (t[j].w * scale) * gw.w};
             convert_block256(v, lane, mode, act, Lay, m, K, b);
         }
     }

@@ -216,6 +216,7 @@ int engine_ar_forward(diffuse_context * c, const int32_t * tokens, int n_new, bo
         TRY(engine_hip_ok(hipMemcpyAsync(logits_out, c->logits, (size_t)n_new * V * 4, hipMemcpyDeviceToHost,
                                          c->stream), "D2H"));
     TRY(engine_hip_ok(hipStreamSynchronize(c->stream), "ar_forward"));
+    TRY(engine_check_tiles(c));
     engine_prof_collect(c);
     return DFX_OK;
 }
@@ -242,6 +243,7 @@ int engine_ar_profile(diffuse_context * c, const int32_t * tokens, int n, int wi
         TRY(engine_hip_ok(hipMemcpyAsync(logits_out, c->logits, (size_t)n * V * 4, hipMemcpyDeviceToHost, c->stream),
                           "D2H"));
     TRY(engine_hip_ok(hipStreamSynchronize(c->stream), "ar_profile_layers"));
+    TRY(engine_check_tiles(c));
     if (impact_out) memcpy(impact_out, impact.data(), (size_t)L * 4);
     if (skip_out) memcpy(skip_out, skip.data(), (size_t)L);
     engine_prof_collect(c);
@@ -289,6 +291,7 @@ int engine_ar_generate(diffuse_context * c, const int32_t * prompt, int n_prompt
         TRY(ar_pass(c, prompt, n_prompt, p.sliding_window, false, false, nullptr));
     }
     TRY(engine_hip_ok(hipStreamSynchronize(c->stream), "ar_generate prefill"));
+    TRY(engine_check_tiles(c));
     const double prefill_ms = std::chrono::duration<double, std::milli>(clk::now() - gen_start).count();
     DIFFUSE_LOG("  prefill: %d tokens in %.1f ms (%.1f tok/s)", n_prompt, prefill_ms, 1000.0 * n_prompt / prefill_ms);
 

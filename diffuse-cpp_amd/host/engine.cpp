@@ -174,6 +174,22 @@ static int d2h_sync(diffuse_context * c, void * dst, const void * src, size_t by
     return hip_ok(hipStreamSynchronize(c->stream), "D2H");
 }
 
+// The half-tile GEMMs raise tile_cnt[1] when the two halves of a tile ran on different XCDs
+// (their chunk-total handover assumes one L2; see k_q4k_w): checked after every pass that
+// reads results back, so such a pass fails instead of returning possibly stale sums.
+int check_tiles(diffuse_context * c) {
+    if (!c->tile_cnt) return DFX_OK;
+    int32_t flag = 0;
+    TRY(d2h_sync(c, &flag, c->tile_cnt + 1, sizeof(flag)));
+    if (flag) {
+        TRY(hip_ok(hipMemsetAsync(c->tile_cnt + 1, 0, sizeof(int32_t), c->stream), "counter clear"));
+        dfx_set_error("GEMM half tiles ran on different XCDs (workgroup-to-XCD mapping not round-robin): "
+                      "results of this pass are invalid");
+        return DFX_ERR_HIP;
+    }
+    return DFX_OK;
+}
+
 // Every GEMM of the forward goes through here; with profiling on, a pair of events
 // brackets the launch on the context stream (read back by prof_collect).
 // With n_partials, a split-K GEMM may leave its chunk sums in c->ws (see dfx_gemm_ex)
@@ -534,6 +550,7 @@ int generate_device(diffuse_context * c, const int32_t * prompt, int n_prompt, i
         }
     }
     TRY(hip_ok(hipStreamSynchronize(c->stream), "generate"));
+    TRY(check_tiles(c));
     for (int t = 0; t < actual_steps; t++) TRY(step_unmasked(t));
     const double gen_ms = std::chrono::duration<double, std::milli>(clk::now() - gen_start).count();
     // the device's own row counts must be the ones the host launched with
@@ -666,6 +683,7 @@ int engine_forward(diffuse_context * c, const int32_t * tokens, int n, float * l
     TRY(forward_pass(c, n, n, n));
     TRY(hip_ok(hipMemcpyAsync(logits_out, c->logits, (size_t)n * D.V * 4, hipMemcpyDeviceToHost, c->stream), "D2H"));
     TRY(hip_ok(hipStreamSynchronize(c->stream), "forward"));
+    TRY(check_tiles(c));
     c->kv_valid = n;   // the K/V of positions 0..n-1 are in the cache
     prof_collect(c);
     return DFX_OK;
@@ -707,6 +725,7 @@ int engine_forward_cached(diffuse_context * c, const int32_t * active_tokens, co
     TRY(hip_ok(hipMemcpyAsync(logits_out, c->logits, (size_t)n_active * D.V * 4, hipMemcpyDeviceToHost, c->stream),
                "D2H"));
     TRY(hip_ok(hipStreamSynchronize(c->stream), "forward"));
+    TRY(check_tiles(c));
     prof_collect(c);
     return DFX_OK;
 }
@@ -965,11 +984,13 @@ int engine_generate(diffuse_context * c, const int32_t * prompt, int n_prompt, i
         stats->forward_ms = total_fwd;
         stats->sample_ms = total_sample + total_sort + total_unmask;
     }
+    TRY(check_tiles(c));
     memcpy(out, seq.data() + n_prompt, (size_t)n_generate * 4);
     return DFX_OK;
 }
 
 int engine_hip_ok(hipError_t e, const char * what) { return hip_ok(e, what); }
+int engine_check_tiles(diffuse_context * c) { return check_tiles(c); }
 int engine_reserve(diffuse_context * c, int N) { return ensure_capacity(c, N); }
 int engine_pass(diffuse_context * c, int M, int n_keys, int n_head, const pass_opts & o) {
     return forward_pass(c, M, n_keys, n_head, o);

@@ -177,6 +177,7 @@ struct pass_opts {
 int  engine_hip_ok(hipError_t e, const char * what);
 int  engine_reserve(diffuse_context * c, int N);
 int  engine_pass(diffuse_context * c, int M, int n_keys, int n_head, const pass_opts & o);
+int  engine_check_tiles(diffuse_context * c);   // after a synchronised pass: half-tile XCD check
 void engine_prof_collect(diffuse_context * c);
 
 // ar.cpp (src/ar-graph.cpp, src/ar-sampler.cpp)

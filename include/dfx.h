@@ -133,7 +133,11 @@ int dfx_gemm(int wtype, const void * w, int64_t N, int64_t K, const void * act, 
  * others with two (a scheduling form of the same mul_mat; no counterpart in the reference).
  * Other weight types, shapes and row counts run as dfx_gemm.  ws: dfx_gemm_ws_bytes(M, N, K)
  * bytes (2*M*N floats used).  tile_cnt: dfx_gemm_tile_cnt_bytes(M, N) bytes, all zero before
- * the first call; every call leaves them zero.  Calls sharing tile_cnt or ws must not overlap. */
+ * the first call; every call leaves them zero except tile_cnt[1], which a call sets to 1 when
+ * the two halves of a tile ran on different XCDs (the handover of their chunk totals assumes
+ * one L2, i.e. the round-robin workgroup-to-XCD dispatch): the results of such a call are
+ * invalid.  Callers check tile_cnt[1] after the call and clear it.  Calls sharing tile_cnt or
+ * ws must not overlap. */
 size_t dfx_gemm_tile_cnt_bytes(int64_t M, int64_t N);
 int dfx_gemm_counted(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
                      const float * bias, const float * residual, float * y, void * ws, int32_t * tile_cnt,
@@ -175,8 +179,11 @@ int dfx_gemm_force_tile(int wtype, const char * spec);
 
 /* dfx_gemm without a workspace argument and without any allocation: the split-K partial
  * sums go to a library-held device array of 32 MiB per GPU (held from the library's load to
- * process end), so M * N * ceil(K / 2048) * 4 bytes must not exceed 32 MiB (DFX_ERR_ARG
- * otherwise).  Same kernels and the same bits as dfx_gemm with a workspace.  Calls on one GPU
+ * process end).  Quantised weights whose split would need more (M * N * ceil(K / 2048) * 4
+ * bytes) keep K whole, which gives the same bits; an F16 split that would not fit is refused
+ * with DFX_ERR_ARG (the split rule needs at most 16 MiB).  Same kernels and the same bits as
+ * dfx_gemm with a workspace.  The first call on a device may be made under stream capture
+ * (it looks the array's address up with the thread's capture mode relaxed).  Calls on one GPU
  * share that array: calls that overlap in time on one GPU (several streams or host threads)
  * race; serialise them.  No counterpart in the reference: for callers that cannot allocate
  * device memory (code under stream capture, serving loops that forbid hipMalloc). */
