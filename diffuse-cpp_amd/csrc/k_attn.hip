@@ -733,6 +733,73 @@ __global__ void __launch_bounds__(256) k_attn_long(const float * __restrict__ q,
     }
 }
 
+// Few query rows (autoregressive decoding: one row per token): one workgroup per (row, head),
+// in the oracle's own order: each score is one thread's sequential f64 dot product over the
+// head's dimensions (f32 x f32 products are exact in f64), rounded to float and scaled; the
+// exponentials are computed in parallel and summed in double by one thread in key order; each
+// output dimension is one thread's sequential f64 sum over the keys in key order.  Keys are
+// the cache positions in order, so a pass whose keys are its positions 0..n-1 (decoding)
+// repeats the oracle's sums exactly.  At most ROWS_MAX_KEYS visible keys per row.
+#define ROWS_MAX_KEYS 1024
+template <int HD>
+__global__ void __launch_bounds__(256) k_attn_rows(const float * __restrict__ q, const float * __restrict__ kc,
+                                                   const float * __restrict__ vt, int64_t v_ld, int M, int n_keys,
+                                                   int H, int Hkv, int q_pos0, int window, float * __restrict__ out) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) float qs[HD];
+    __shared__ float sc[ROWS_MAX_KEYS];
+    __shared__ float red[4];
+    __shared__ float inv_s;
+    const int h = blockIdx.x % H, row = blockIdx.x / H;
+    const int kvh = h / (H / Hkv);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const key_range kr = row_keys(row, M, n_keys, q_pos0, window);
+    const int nk = kr.hi - kr.lo + 1;
+    const float scale = 1.0f / sqrtf((float)HD);
+    if (tid < HD) qs[tid] = q[((int64_t)row * H + h) * HD + tid];
+    __syncthreads();
+    const int64_t kvstride = (int64_t)Hkv * HD;
+    float mx = -INFINITY;
+    for (int j = tid; j < nk; j += 256) {
+        const float * kr4 = kc + (int64_t)(kr.lo + j) * kvstride + (int64_t)kvh * HD;
+        double acc = 0.0;
+#pragma unroll 8
+        for (int i = 0; i < HD; i += 4) {
+            const float4 k4 = *(const float4 *)(kr4 + i);
+            const float4 q4 = *(const float4 *)(qs + i);
+            acc = acc + (double)k4.x * (double)q4.x;
+            acc = acc + (double)k4.y * (double)q4.y;
+            acc = acc + (double)k4.z * (double)q4.z;
+            acc = acc + (double)k4.w * (double)q4.w;
+        }
+        const float sv = (float)acc * scale;
+        sc[j] = sv;
+        mx = fmaxf(mx, sv);
+    }
+    mx = wave_max(mx);
+    if (lane == 0) red[wv] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int j = tid; j < nk; j += 256) sc[j] = (float)exp((double)(sc[j] - mx));
+    __syncthreads();
+    if (tid == 0) {
+        double sum = 0.0;
+        for (int j = 0; j < nk; j++) sum += (double)sc[j];
+        inv_s = (float)(1.0 / sum);
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    for (int j = tid; j < nk; j += 256) sc[j] = sc[j] * inv;
+    __syncthreads();
+    if (tid < HD) {
+        const float * vr = vt + ((int64_t)kvh * HD + tid) * v_ld + kr.lo;
+        double acc = 0.0;
+#pragma unroll 8
+        for (int j = 0; j < nk; j++) acc = acc + (double)vr[j] * (double)sc[j];
+        out[(int64_t)row * H * HD + (int64_t)h * HD + tid] = (float)acc;
+    }
+}
+
 extern "C" int dfx_rope_store(const float * qkv, const int32_t * pos, int64_t M, int H, int Hkv, int hd,
                               const float * tab, float * q_out, float * kc, float * vt, int64_t v_ld, void * stream) {
     if (M < 0 || H <= 0 || Hkv <= 0 || H % Hkv || hd <= 0 || (hd & 1) || v_ld <= 0) {
@@ -792,6 +859,18 @@ static inline int attn_split_sstride(int64_t n_keys) { return (int)(((n_keys + 3
 // else recomputed in three passes.  q_pos0 / window: the causal mask (q_pos0 < 0: none).
 static int attn_exact(const float * q, const float * kc, const float * vt, int64_t v_ld, int M, int n_keys, int H,
                       int Hkv, int hd, int q_pos0, int window, float * out, hipStream_t st) {
+    if (M <= 4 && n_keys <= ROWS_MAX_KEYS) {
+        // decoding: one workgroup per (row, head) instead of a 16-row tile per head
+        const dim3 grid((unsigned)(M * H));
+        if (hd == 128)
+            hipLaunchKernelGGL((k_attn_rows<128>), grid, dim3(256), 0, st, q, kc, vt, v_ld, M, n_keys, H, Hkv, q_pos0,
+                               window, out);
+        else
+            hipLaunchKernelGGL((k_attn_rows<64>), grid, dim3(256), 0, st, q, kc, vt, v_ld, M, n_keys, H, Hkv, q_pos0,
+                               window, out);
+        DFX_CHECK_LAUNCH("dfx_attention (few rows)");
+        return DFX_OK;
+    }
     const int sstride = attn_sstride(n_keys);
     const size_t lds = (size_t)16 * sstride * sizeof(float);
     const int q_tiles = (M + 15) / 16;

@@ -1,15 +1,17 @@
 // k_sampler.hip — per-row vocab statistics and remask selection.
 //
 // Row statistics restate the reference's per-masked-position scan
-// (src/diffuse-sampler.cpp:34-57 compute_entropy, 241-252 top-1/top-2) as
-// workgroup reductions over a logits row, in two reads of the row:
-//   pass 1  argmax (strict >, lowest index on ties), top-2, and sum = sum of exp(x - max),
-//           each thread keeping its sum relative to its own running maximum (rescaled when
-//           that maximum grows) until the row maximum is known
-//   pass 2  entropy = -sum p*log_p over p = exp((x - max) - log(sum)) > 1e-10
-// The top-2 values are exact.  exp is the transcendental unit's 2^(x log2 e) (about 1 ulp);
-// per-thread partial sums are float, the sums across threads double.  The reference adds
-// 126464 floats one after another, so its own sum carries a larger rounding error.
+// (src/diffuse-sampler.cpp:34-57 compute_entropy, 241-252 top-1/top-2) as one
+// workgroup reduction over a logits row, in a single read of the row:
+//   argmax (strict >, lowest index on ties), top-2 (exact), and
+//   S = sum of e = exp(x - max) and T = sum of e * (x - max), each thread keeping its sums
+//   relative to its own running maximum m (when m grows to m', S and T are rescaled by
+//   r = exp(m - m'): S' = r S, T' = r (T + (m - m') S)) until the row maximum is known;
+//   entropy = -sum p log p = log S - T / S  (p = e / S, log p = (x - max) - log S).
+// The reference drops terms with p <= 1e-10 (at most V * 2.3e-9 in all, far less for any
+// real row) and adds 126464 float terms one after another, whose rounding walk is ~1e-5
+// relative; here exp is the transcendental unit's 2^(x log2 e) (about 1 ulp), per-thread
+// sums are float and the sums across threads double.
 #include "dfx_device.h"
 
 #include <algorithm>
@@ -50,15 +52,36 @@ __global__ void __launch_bounds__(RS_THREADS) k_row_stats(const float * __restri
                                                           dfx_row_stat * __restrict__ out) {
 #pragma clang fp contract(off)
     __shared__ top2_t red_t[RS_THREADS / 64];
-    __shared__ double red_d[RS_THREADS / 64];
+    __shared__ double red_d[RS_THREADS / 64], red_d2[RS_THREADS / 64];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int nw = RS_THREADS / 64;
     const float * x = logits + (int64_t)rows[blockIdx.x] * ld;
     const bool vec = ((V & 3) == 0) && ((((uintptr_t)x) & 15) == 0);
 
-    // pass 1: top-2 and the exp sum relative to this thread's running maximum m
+    // top-2, and S / T relative to this thread's running maximum m
     top2_t t = {-INFINITY, 0x7fffffff, -INFINITY};
-    float m = -INFINITY, s = 0.0f;
+    float m = -INFINITY, s = 0.0f, tm = 0.0f;
+    // one element e (at most the running m) into S and T; d is clamped where exp(d) is
+    // already 0 in float, so that a -inf logit adds 0 * (-256), not 0 * -inf
+    auto add = [&](float e) __attribute__((always_inline)) {
+        const float d = fmaxf(e - m, -256.0f);
+        const float p = exp_fast(d);
+        s = s + p;
+        tm = tm + p * d;
+    };
+    // raise the running maximum to m4 >= m, rescaling S and T
+    auto raise = [&](float m4) __attribute__((always_inline)) {
+        if (m == -INFINITY) {
+            s = 0.0f;
+            tm = 0.0f;
+        } else {
+            const float d = m - m4;
+            const float r = exp_fast(d);
+            tm = r * (tm + d * s);
+            s = r * s;
+        }
+        m = m4;
+    };
     if (vec) {
         // RS_UNROLL float4 loads in flight per thread, from clamped addresses; elements past
         // the row end read as -inf (no effect on top-2, exp(-inf) = 0)
@@ -69,7 +92,7 @@ __global__ void __launch_bounds__(RS_THREADS) k_row_stats(const float * __restri
 #pragma unroll
             for (int u = 0; u < RS_UNROLL; u++) {
                 const int i = i0 + 4 * u * RS_THREADS;
-                if (i >= V) v[u] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+                if (i >= V) continue;
                 const float g = fmaxf(fmaxf(v[u].x, v[u].y), fmaxf(v[u].z, v[u].w));
                 // elements <= the running second change neither the best nor the second
                 if (g > t.second) {
@@ -78,16 +101,12 @@ __global__ void __launch_bounds__(RS_THREADS) k_row_stats(const float * __restri
                     top2_push(t, v[u].z, i + 2);
                     top2_push(t, v[u].w, i + 3);
                 }
-                const float m4 = fmaxf(g, m);
-                if (m4 > m) {
-                    s = m == -INFINITY ? 0.0f : s * exp_fast(m - m4);
-                    m = m4;
-                }
+                if (g > m) raise(g);
                 if (m != -INFINITY) {
-                    s = s + exp_fast(v[u].x - m);
-                    s = s + exp_fast(v[u].y - m);
-                    s = s + exp_fast(v[u].z - m);
-                    s = s + exp_fast(v[u].w - m);
+                    add(v[u].x);
+                    add(v[u].y);
+                    add(v[u].z);
+                    add(v[u].w);
                 }
             }
         }
@@ -95,11 +114,8 @@ __global__ void __launch_bounds__(RS_THREADS) k_row_stats(const float * __restri
         for (int i = tid; i < V; i += RS_THREADS) {
             const float e = x[i];
             top2_push(t, e, i);
-            if (e > m) {
-                s = m == -INFINITY ? 0.0f : s * exp_fast(m - e);
-                m = e;
-            }
-            s = s + exp_fast(e - m);
+            if (e > m) raise(e);
+            if (m != -INFINITY) add(e);
         }
     }
     for (int off = 32; off > 0; off >>= 1) t = top2_merge(t, top2_shfl(t, off));
@@ -115,52 +131,31 @@ __global__ void __launch_bounds__(RS_THREADS) k_row_stats(const float * __restri
     float second = t.second;
     if (t.idx == 0) second = fmaxf(second, -1e30f);
 
-    double sd = m == -INFINITY ? 0.0 : (double)(s * exp_fast(m - mx));
-    sd = wave_sum_d(sd);
-    if (lane == 0) red_d[wv] = sd;
-    __syncthreads();
-    double tot = 0.0;
-    for (int w = 0; w < nw; w++) tot += red_d[w];
-    const float log_sum = logf((float)tot);
-    __syncthreads();
-
-    // pass 2: entropy
-    float ent = 0.0f;
-    if (vec) {
-        for (int i0 = 4 * tid; i0 < V; i0 += 4 * RS_UNROLL * RS_THREADS) {
-            float4 v[RS_UNROLL];
-#pragma unroll
-            for (int u = 0; u < RS_UNROLL; u++) v[u] = *(const float4 *)(x + min(i0 + 4 * u * RS_THREADS, V - 4));
-#pragma unroll
-            for (int u = 0; u < RS_UNROLL; u++) {
-                if (i0 + 4 * u * RS_THREADS >= V) continue;
-                const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float lp = (e[j] - mx) - log_sum;
-                    const float p = exp_fast(lp);
-                    if (p > 1e-10f) ent = ent - p * lp;
-                }
-            }
-        }
-    } else {
-        for (int i = tid; i < V; i += RS_THREADS) {
-            const float lp = (x[i] - mx) - log_sum;
-            const float p = exp_fast(lp);
-            if (p > 1e-10f) ent = ent - p * lp;
-        }
+    // this thread's S and T relative to the row maximum, summed over the row in double
+    double sd = 0.0, td = 0.0;
+    if (m != -INFINITY) {
+        const double d = (double)m - (double)mx, r = (double)exp_fast(m - mx);
+        sd = r * (double)s;
+        td = r * ((double)tm + d * (double)s);
     }
-    double ed = wave_sum_d((double)ent);
-    if (lane == 0) red_d[wv] = ed;
+    sd = wave_sum_d(sd);
+    td = wave_sum_d(td);
+    if (lane == 0) {
+        red_d[wv] = sd;
+        red_d2[wv] = td;
+    }
     __syncthreads();
     if (tid == 0) {
-        double e = 0.0;
-        for (int w = 0; w < nw; w++) e += red_d[w];
+        double S = 0.0, T = 0.0;
+        for (int w = 0; w < nw; w++) {
+            S += red_d[w];
+            T += red_d2[w];
+        }
         dfx_row_stat r;
         r.token = t.idx;
         r.best = mx;
         r.second = second;
-        r.entropy = (float)e;
+        r.entropy = S > 0.0 ? (float)(log(S) - T / S) : 0.0f;
         out[blockIdx.x] = r;
     }
 }

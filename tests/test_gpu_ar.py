@@ -69,6 +69,34 @@ def test_attention_causal_matches_oracle(gpu, M, n_keys, q_pos0, window, H, Hkv,
     assert ulps.max() <= 1 and (ulps > 0).mean() <= 1e-5, (int(ulps.max()), int((ulps > 0).sum()))
 
 
+@pytest.mark.parametrize("M,n_keys,q_pos0,window,H,Hkv,hd", [
+    (1, 192, 191, 0, 28, 4, 128),      # Dream-7B decode: one row, GQA 28 / 4
+    (1, 1024, 1023, 0, 8, 2, 64),      # the most keys of the few-row kernel
+    (4, 700, 696, 100, 4, 1, 128),     # four rows with a window
+    (2, 65, -1, 0, 4, 4, 128)])        # bidirectional (no mask)
+def test_attention_few_rows_equals_oracle_exactly(gpu, M, n_keys, q_pos0, window, H, Hkv, hd):
+    """At most 4 query rows and 1024 keys (decoding): one workgroup per row and head, summing
+    in the oracle's order (sequential f64 dot per score, double exp-sum and P.V sums in key
+    order), so the result is the oracle's floats."""
+    rng = np.random.default_rng(M * 7 + n_keys)
+    q = rng.standard_normal((M, H, hd)).astype(np.float32)
+    k = rng.standard_normal((n_keys, Hkv, hd)).astype(np.float32)
+    v = rng.standard_normal((n_keys, Hkv, hd)).astype(np.float32)
+    v_ld = (n_keys + 15) // 16 * 16 + 16
+    vt = np.full((Hkv, hd, v_ld), np.nan, np.float32)
+    vt[:, :, :n_keys] = v.transpose(1, 2, 0)
+    qb, kb, vb, ob = dfx.Buf.of(q), dfx.Buf.of(k), dfx.Buf.of(vt), dfx.Buf(M * H * hd * 4)
+    if q_pos0 >= 0:
+        dfx.check(L().dfx_attention_causal(qb.ptr, kb.ptr, vb.ptr, v_ld, M, n_keys, H, Hkv, hd, q_pos0, window,
+                                           ob.ptr, None), "attention_causal")
+        ref = O.attention_causal(q, k, v, np.arange(q_pos0, q_pos0 + M), np.arange(n_keys), window)
+    else:
+        dfx.check(L().dfx_attention(qb.ptr, kb.ptr, vb.ptr, v_ld, M, n_keys, H, Hkv, hd, ob.ptr, None), "attention")
+        ref = O.attention(q, k, v)
+    got = ob.download(np.float32, shape=(M, H, hd))
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), float(np.mean(got != ref))
+
+
 def test_attention_causal_rejects_queries_past_the_keys(gpu):
     b = dfx.Buf(1 << 16)
     rc = L().dfx_attention_causal(b.ptr, b.ptr, b.ptr, 32, 4, 20, 2, 2, 128, 17, 0, b.ptr, None)

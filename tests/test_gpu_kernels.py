@@ -164,7 +164,7 @@ def test_gemm_quantized_bit_exact(gpu, typ, N, K, M):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
 
 
-@pytest.mark.parametrize("tile", ["2x2x2", "4x1x2", "2x1x2", "1x2x2", "1x1x4", "1x1x2", "2x1x4", "2x2x4", "w", "w1", "w3"])
+@pytest.mark.parametrize("tile", ["2x2x2", "4x1x2", "2x1x2", "1x1x4", "1x1x2", "2x1x4", "2x2x4", "w", "w1", "w3"])
 @pytest.mark.parametrize("N,K,M", [(1000, 2048, 77), (4096, 4096, 288)])
 def test_gemm_q4k_every_tile_bit_exact(gpu, tile, N, K, M):
     """Every register tile of the Q4_K kernel (forced with dfx_gemm_force_tile), with ragged
@@ -177,7 +177,7 @@ def test_gemm_q4k_every_tile_bit_exact(gpu, tile, N, K, M):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
 
 
-@pytest.mark.parametrize("tile", ["1x1x4s", "2x1x2s", "1x2x2s", "2x1x4s", "ws", "w1s", "w3s"])
+@pytest.mark.parametrize("tile", ["1x1x4s", "2x1x2s", "2x1x4s", "ws", "w1s", "w3s"])
 @pytest.mark.parametrize("N,K,M", [(512, 12288, 70), (1000, 3584, 33), (640, 2304, 40), (4096, 4096, 256)])
 def test_gemm_q4k_split_k_bit_exact(gpu, tile, N, K, M):
     """Split K (one workgroup per 2048-element chunk, chunk sums added in order by the
@@ -590,7 +590,11 @@ def test_attention_split_bf16_is_more_than_one_bf16_pass(gpu):
 @pytest.mark.parametrize("sigma", [0.5, 2.0, 8.0])
 def test_row_stats_matches_oracle(gpu, sigma):
     """Sampler microbench shape: [256 x 126464] N(0, sigma) logits.  argmax / top-1 / top-2
-    exact; entropy within the reference's own float-accumulation error (2e-3 relative)."""
+    exact; entropy within 1e-4 relative + 2e-5 absolute.  The reference adds 126464 float terms
+    one after another (the GPU sums in double): the rounding walk of its exp-sum, ~1e-5 of the
+    sum, moves log(sum) and so the entropy by ~1e-5 absolute whatever the entropy's size, which
+    dominates on peaked rows (entropy ~0.01 at sigma 8); measured against an f64 evaluation of
+    these rows the reference formula stays within 0.37 of this bound."""
     R, V = 256, 126464
     x = (np.random.default_rng(4).standard_normal((R, V)) * sigma).astype(np.float32)
     x[0, [5, 77]] = x[0].max() + 1.0           # tie on the max: lowest index
@@ -603,7 +607,7 @@ def test_row_stats_matches_oracle(gpu, sigma):
         b, bv, sv = O.top2(x[r])
         assert (st["token"][i], st["best"][i], st["second"][i]) == (b, np.float32(bv), np.float32(sv)), r
         e_ref = O.entropy(x[r])
-        assert abs(st["entropy"][i] - e_ref) <= 2e-3 * abs(e_ref) + 1e-5, r
+        assert abs(st["entropy"][i] - e_ref) <= 1e-4 * abs(e_ref) + 2e-5, (r, st["entropy"][i], e_ref)
 
 
 @pytest.mark.parametrize("remasking", [0, 2, 3, 4])
