@@ -69,65 +69,121 @@ def time_generations(ctx, prompt, n_gen, params, reps, warmup):
     return (time.perf_counter() - t0) / reps, stats
 
 
-def cpu_baseline(path, row_plan, n_threads):
-    """The CPU oracle (a restatement of the reference's GGML CPU path, run here as the
-    reference cannot be built) timed on this host's cores, on a bounded sample:
-      * a whole 16-step generation (entropy_exit + cache, 32 + 256) of a two-layer model of
-        the LLaDA-8B width (vocab head, embedding and sampler at full size), timed end to end;
-      * the 32-layer and the 1-layer forward over the 288-row step-0 sequence, whose
-        difference gives the cost of one layer per row;
-    the full-depth generation = the two-layer one + 30 layers' cost at the rows of every
-    step.  Its GEMM rate per core is reported beside the reference's published rate."""
+def host_cpu():
+    """The host's CPU as lscpu reports it, and the threads this process may use: its affinity
+    set, the cgroup's CPU quota and OMP_NUM_THREADS (the GPU box grants one GPU's share of the
+    host, 16 threads, whatever the host's core count)."""
+    info = {}
+    try:
+        import subprocess
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=30).stdout
+        kv = {k.strip(): v.strip() for k, v in (l.split(":", 1) for l in txt.splitlines() if ":" in l)}
+        sockets, cores, tpc = int(kv.get("Socket(s)", 1)), int(kv.get("Core(s) per socket", 0)), \
+            int(kv.get("Thread(s) per core", 1))
+        info = {"model": kv.get("Model name"), "sockets": sockets, "physical_cores": sockets * cores,
+                "threads_per_core": tpc, "smt": tpc > 1, "logical_cpus": int(kv.get("CPU(s)", 0)),
+                "avx512": "avx512f" in kv.get("Flags", "")}
+    except Exception as e:   # noqa: BLE001 - informational only
+        info = {"lscpu_error": str(e)}
+    limits = {"affinity": len(os.sched_getaffinity(0))}
+    try:
+        q, per = open("/sys/fs/cgroup/cpu.max").read().split()
+        if q != "max":
+            limits["cgroup_quota"] = max(1, int(int(q) / int(per)))
+    except (OSError, ValueError):
+        pass
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        limits["omp_num_threads"] = int(os.environ["OMP_NUM_THREADS"])
+    info["limits"] = limits
+    info["threads_granted"] = min(limits.values())
+    return info
+
+
+def cpu_baseline(path, row_plan, n_threads, host):
+    """The CPU oracle (a restatement of the reference's GGML CPU path: GGML's own sources are
+    not in the reference, so it cannot be built) timed on this host, on a bounded sample of
+    the headline workload with every layer of the model run:
+      * the full-depth (32-layer) forward of step 0 over the 288 rows, and a full-depth cached
+        step over 50 active rows against the 288-position cache (the smallest step);
+      * the same two passes and a whole 16-step generation (entropy_exit + cache, 32 + 256) of
+        the model with its layers removed (embedding, final norm, vocab head and the sampler
+        at every step), which times the head, the sampler and the loop as they run;
+    generation = the layerless generation + the layers' cost at each step's rows, linear in the
+    rows between the two measured passes.  Its GEMM rate per core is reported beside the
+    reference's published rate (1586 ms per 96-row Q4_K_M step on a 12-core EPYC 4465P), and
+    the value scaled to that rate is the headline comparison."""
     sys.path.insert(0, os.path.join(REPO, "tests"))
     import oracle_py as O
-    spent = 0.0
-    # two-layer generate, timed
-    arch2 = dict(dfx.LLADA_8B, n_layer=2)
-    p2 = ensure_model("llada8b-2l", arch2, "q4_k_m", 0)
-    om2 = O.OracleModel(p2)
-    prompt = np.random.default_rng(1).integers(0, 126000, PROMPT).astype(np.int32)
-    t = time.perf_counter()
-    _, st = om2.generate(prompt, B, n_steps=STEPS, remasking=dfx.ENTROPY_EXIT, use_cache=True, seed=42,
-                         n_threads=n_threads)
-    t_gen2 = time.perf_counter() - t
-    spent += t_gen2
-    rows2 = [st.rows_per_step[i] for i in range(st.actual_steps)]
-    # per-layer-row cost from a 1-layer and the full-depth forward (better of two runs)
     om = O.OracleModel(path)
     L = om.m.n_layer
-    M = PROMPT + B
-    toks = np.random.default_rng(1).integers(0, 126000, M).astype(np.int32)
-    times = {}
-    for nl in (1, L):
-        om.m.n_layer = nl
-        best = float("inf")
-        for _ in range(2):
-            t = time.perf_counter()
-            om.forward_full(toks, n_threads=n_threads)
-            dt = time.perf_counter() - t
-            spent += dt
-            best = min(best, dt)
-        times[nl] = best
+    M0, Ms = PROMPT + B, min(row_plan) if row_plan else 50
+    rng = np.random.default_rng(1)
+    prompt = rng.integers(0, 126000, PROMPT).astype(np.int32)
+    seq = np.concatenate([prompt, np.full(B, dfx.LLADA_8B["mask_token_id"], np.int32)])
+    act = np.arange(M0 - Ms, M0, dtype=np.int32)
+    spent = 0.0
+
+    def passes(n_layer):
+        nonlocal spent
+        om.m.n_layer = n_layer
+        t = time.perf_counter()
+        _, kv = om.forward_full(seq, kv_tokens=M0, n_threads=n_threads)
+        t_full = time.perf_counter() - t
+        t = time.perf_counter()
+        om.forward_cached(kv, seq[act], act, M0, n_threads=n_threads)
+        t_cached = time.perf_counter() - t
+        spent += t_full + t_cached
+        return t_full, t_cached
+    full_L, cached_L = passes(L)
+    full_0, cached_0 = passes(0)
+    om.m.n_layer = 0
+    t = time.perf_counter()
+    _, st = om.generate(prompt, B, n_steps=STEPS, remasking=dfx.ENTROPY_EXIT, use_cache=True, seed=42,
+                        n_threads=n_threads)
+    t_gen0 = time.perf_counter() - t
+    spent += t_gen0
     om.m.n_layer = L
-    t_layer_row = max(times[L] - times[1], 1e-9) / ((L - 1) * M)
-    total = t_gen2 + (L - 2) * t_layer_row * sum(rows2)
-    gflop_layer = 2.0 * (4 * 4096 * 4096 + 3 * 4096 * 12288) * M / 1e9
-    gflops_core = gflop_layer / max(t_layer_row * M, 1e-9) / n_threads
+    rows = [st.rows_per_step[i] for i in range(st.actual_steps)]
+    lay_hi, lay_lo = full_L - full_0, cached_L - cached_0     # the layers' cost at M0 and at Ms rows
+    per_row = (lay_hi - lay_lo) / max(M0 - Ms, 1)
+    layers_total = sum(lay_lo + per_row * (m - Ms) for m in rows)
+    total = t_gen0 + layers_total
+    gflop_layers = 2.0 * (4 * 4096 * 4096 + 3 * 4096 * 12288) * M0 * L / 1e9
+    gflops_core = gflop_layers / max(lay_hi, 1e-9) / n_threads
     value = B / total
     return {
         "value": round(value, 4), "unit": "tok/s", "cores": n_threads, "kind": "port",
-        "sample": (f"oracle (GGML-semantics C++ restatement, {n_threads} threads, AVX2 integer block dots): "
-                   f"a whole 16-step generate (entropy_exit + cache, 32 + 256) of a 2-layer LLaDA-8B-width "
-                   f"model timed end to end ({t_gen2:.1f}s, rows {rows2}), plus 30 layers at those rows from "
-                   f"the 32- and 1-layer 288-row forwards (better of 2 each); {spent:.1f}s of CPU time in all"),
-        "two_layer_generate_s": round(t_gen2, 2),
-        "step0_forward_s": round(times[L], 3),
+        "sample": (f"oracle (GGML-semantics C++ restatement, {n_threads} threads, AVX2 integer block dots) on "
+                   f"{host.get('model')}: the full-depth ({L}-layer) step-0 forward over {M0} rows ({full_L:.1f}s) "
+                   f"and a full-depth cached step over {Ms} active rows ({cached_L:.1f}s), the same passes without "
+                   f"layers, and a whole 16-step generate (entropy_exit + cache, 32 + 256) without layers "
+                   f"({t_gen0:.1f}s: head, sampler, loop); generation = that + the layers' cost at each step's "
+                   f"rows {rows}, linear in rows between the two measured passes; {spent:.1f}s of CPU time in all"),
+        "host": host,
+        "step0_forward_s": round(full_L, 3),
+        "cached_step_forward_s": round(cached_L, 3),
+        "layerless_generate_s": round(t_gen0, 2),
         "ms_per_denoise_step": round(1000 * total / STEPS, 1),
         "layer_gflops_per_core": round(gflops_core, 2),
         "reference_published_gflops_per_core": round(GGML_GFLOPS_PER_CORE, 2),
         # the same generation at the reference's published per-core GEMM rate on these cores
-        "value_at_reference_rate": round(value * GGML_GFLOPS_PER_CORE / gflops_core, 4),
+        "value_at_reference_rate": round(B / (t_gen0 + layers_total * gflops_core / GGML_GFLOPS_PER_CORE), 4),
     }
+
+
+def cpu_full_generate(path, n_threads, host):
+    """One whole 16-step generation of the headline workload at full depth on the CPU oracle,
+    timed end to end (minutes of host time: run on its own, not in the default bench)."""
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import oracle_py as O
+    om = O.OracleModel(path)
+    prompt = np.random.default_rng(1).integers(0, 126000, PROMPT).astype(np.int32)
+    t = time.perf_counter()
+    out, st = om.generate(prompt, B, n_steps=STEPS, remasking=dfx.ENTROPY_EXIT, use_cache=True, seed=42,
+                          n_threads=n_threads)
+    sec = time.perf_counter() - t
+    return {"cpu_full_generate_s": round(sec, 2), "tok_s": round(B / sec, 4), "threads": n_threads, "host": host,
+            "rows_per_step": [st.rows_per_step[i] for i in range(st.actual_steps)]}
 
 
 def config_llada_b64(model):
@@ -194,15 +250,15 @@ def config_ar(reps=3):
             "decode_weight_gbs": round(gbs, 1), "decode_frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4)}
 
 
-def config_batched():
+def config_batched(scheme="q8_0"):
     """The batched long-context workload: 8 independent sequences of a 512-token prompt + B=256
-    masks on LLaDA-8B Q8_0 (seed 5), 16 steps, low_confidence with the inter-step cache (the
-    header's default policy).  The sequences run at the same time, one context each (own
-    stream) on one shared model, from 8 host threads; tok/s = 8 x 256 / the wall time of the
-    whole batch.  One warm-up batch, then one timed batch; a single sequence alone is timed
-    beside it."""
+    masks on LLaDA-8B (Q8_0 or F16 weights, seed 5), 16 steps, low_confidence with the
+    inter-step cache (the header's default policy).  The sequences run at the same time, one
+    context each (own stream) on one shared model, from 8 host threads; tok/s = 8 x 256 / the
+    wall time of the whole batch.  One warm-up batch, then one timed batch; a single sequence
+    alone is timed beside it."""
     import threading
-    path = ensure_model("llada8b", dfx.LLADA_8B, "q8_0", 5)
+    path = ensure_model("llada8b", dfx.LLADA_8B, scheme, 5)
     model = dfx.Model(path)
     S, P, Bm = 8, 512, 256
     prompts = [np.random.default_rng(50 + i).integers(0, 126000, P).astype(np.int32) for i in range(S)]
@@ -235,8 +291,8 @@ def config_batched():
     for c in ctxs:
         c.close()
     model.close()
-    return {"workload": "8 x (512 + 256) LLaDA-8B Q8_0, 16 steps, low_confidence + inter-step KV cache, "
-                        "8 contexts generating concurrently",
+    return {"workload": f"8 x (512 + 256) LLaDA-8B {scheme.upper()}, 16 steps, low_confidence + inter-step KV "
+                        "cache, 8 contexts generating concurrently",
             "tok_s": round(S * Bm / sec, 2), "ms_per_batch": round(1000 * sec, 1),
             "single_sequence_ms": round(1000 * one, 1),
             "single_ms_per_denoise_step_full": round(st1.step_ms[0], 3),
@@ -280,6 +336,139 @@ def config_sampler():
             "results": out}
 
 
+LLADA_Q4K_SHAPES = (("q|k|v", 12288, 4096), ("o", 4096, 4096), ("gate|up", 24576, 4096), ("down", 4096, 12288))
+
+
+def ceiling(rows=(288, 256, 97, 74, 50), reps=20):
+    """Evidence for the GEMM ceiling at the headline's shapes (LLaDA-8B, M = 288 / 256):
+      * mfma-rate: back-to-back independent f16 MFMAs on one CU and on every SIMD (the
+        dense rate the chip sustains under full matrix-core load);
+      * hipBLASLt's plain f16 GEMM (torch.matmul, no dequantisation, no exact order) at the
+        same M, N, K;
+      * this library's exact Q4_K GEMM (dfx_gemm_counted: split-K workspace and half-tile
+        counters, as the engine calls it) at the same shapes on random N(0, 0.02) weights.
+    Times from HIP events over `reps` back-to-back calls after 3 warm-up calls."""
+    import subprocess
+    import torch
+    out = {}
+    exe = os.path.join(REPO, "diffuse-cpp_amd", "bin", "mfma-rate")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    if r.returncode != 0:
+        raise RuntimeError(f"mfma-rate failed: {r.stderr[-500:]}")
+    out["mfma_rate"] = json.loads(r.stdout.strip().splitlines()[-1])
+    L = dfx.lib
+    rng = np.random.default_rng(7)
+    res = []
+    for name, N, K in LLADA_Q4K_SHAPES:
+        raw = dfx.quantize_rows(dfx.TYPE_Q4_K, rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+        w = dfx.Buf.of(dfx.repack(dfx.TYPE_Q4_K, raw, N, K))
+        del raw
+        for M in rows:
+            flop = 2.0 * M * N * K
+            a = torch.randn(M, K, dtype=torch.float16, device="cuda")
+            b = torch.randn(K, N, dtype=torch.float16, device="cuda") * 0.02
+            for _ in range(3):
+                torch.matmul(a, b)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                torch.matmul(a, b)
+            e1.record()
+            torch.cuda.synchronize()
+            blas_us = 1000.0 * e0.elapsed_time(e1) / reps
+            del a, b
+            xb = dfx.Buf.of(rng.standard_normal((M, K), dtype=np.float32))
+            ab = dfx.Buf(L().dfx_act_bytes(dfx.TYPE_Q4_K, M, K))
+            dfx.check(L().dfx_act_convert(dfx.TYPE_Q4_K, xb.ptr, M, K, ab.ptr, None), "convert")
+            yb, ws = dfx.Buf(M * N * 4), dfx.Buf(L().dfx_gemm_ws_bytes(M, N, K))
+            cnt = dfx.Buf(L().dfx_gemm_tile_cnt_bytes(M, N))
+            cnt.zero()
+
+            def call():
+                dfx.check(L().dfx_gemm_counted(dfx.TYPE_Q4_K, w.ptr, N, K, ab.ptr, M, None, None, yb.ptr, ws.ptr,
+                                               cnt.ptr, None), "gemm_counted")
+            for _ in range(3):
+                call()
+            tm, ms = C.c_void_p(), C.c_float()
+            dfx.check(L().dfx_timer_start(C.byref(tm), None), "timer")
+            for _ in range(reps):
+                call()
+            dfx.check(L().dfx_timer_stop(tm, None, C.byref(ms)), "timer")
+            ours_us = 1000.0 * ms.value / reps
+            res.append({"gemm": name, "M": M, "N": N, "K": K,
+                        "hipblaslt_f16_us": round(blas_us, 2),
+                        "hipblaslt_f16_frac": round(flop / (blas_us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                        "exact_q4k_us": round(ours_us, 2),
+                        "exact_q4k_frac": round(flop / (ours_us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                        "exact_q4k_weight_gbs": round(N * K * 144 / 256 / (ours_us * 1e-6) / 1e9, 1)})
+            log(f"ceiling {name} M={M}: hipBLASLt f16 {blas_us:.1f} us, exact Q4_K {ours_us:.1f} us")
+    out["gemms"] = res
+    return out
+
+
+def stack_ab(reps=5):
+    """The batched long-context unit's GEMMs, stacked or not: for each LLaDA-8B projection
+    (Q8_0 and F16 weights, random N(0, 0.02)), one GEMM over 6144 rows (the 8 sequences'
+    step-0 rows stacked) against 8 GEMMs over 768 rows, run one after another on one stream
+    and concurrently on 8 streams.  HIP events around `reps` repetitions after 2 warm-ups."""
+    L = dfx.lib
+    rng = np.random.default_rng(9)
+    S, R = 8, 768
+    streams = []
+    for _ in range(S):
+        h = C.c_void_p()
+        dfx.check(L().dfx_stream_create(C.byref(h)), "stream")
+        streams.append(h)
+    out = []
+    for scheme, typ in (("q8_0", dfx.TYPE_Q8_0), ("f16", dfx.TYPE_F16)):
+        for name, N, K in LLADA_Q4K_SHAPES:
+            raw = dfx.quantize_rows(typ, rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+            w = dfx.Buf.of(dfx.repack(typ, raw, N, K))
+            del raw
+            xb = dfx.Buf.of(rng.standard_normal((S * R, K), dtype=np.float32))
+            ab = dfx.Buf(L().dfx_act_bytes(typ, S * R, K))
+            dfx.check(L().dfx_act_convert(typ, xb.ptr, S * R, K, ab.ptr, None), "convert")
+            abs_ = [dfx.Buf(L().dfx_act_bytes(typ, R, K)) for _ in range(S)]
+            for i in range(S):
+                dfx.check(L().dfx_act_convert(typ, C.c_void_p(xb.ptr.value + i * R * K * 4), R, K, abs_[i].ptr, None),
+                          "convert")
+            yb = dfx.Buf(S * R * N * 4)
+            wsb = [dfx.Buf(L().dfx_gemm_ws_bytes(R, N, K)) for _ in range(S)]
+            ws_big = dfx.Buf(L().dfx_gemm_ws_bytes(S * R, N, K))
+
+            def stacked():
+                dfx.check(L().dfx_gemm(typ, w.ptr, N, K, ab.ptr, S * R, None, None, yb.ptr, ws_big.ptr, None), "gemm")
+
+            def each(concurrent):
+                for i in range(S):
+                    st = streams[i] if concurrent else None
+                    dfx.check(L().dfx_gemm(typ, w.ptr, N, K, abs_[i].ptr, R, None, None,
+                                           C.c_void_p(yb.ptr.value + i * R * N * 4), wsb[i].ptr, st), "gemm")
+                if concurrent:
+                    for st in streams:
+                        dfx.check(L().dfx_stream_sync(st), "sync")
+
+            def timed(fn):
+                for _ in range(2):
+                    fn()
+                dfx.sync()
+                t0 = time.perf_counter()
+                for _ in range(reps):
+                    fn()
+                dfx.sync()
+                return 1e6 * (time.perf_counter() - t0) / reps
+            us_st, us_seq, us_conc = timed(stacked), timed(lambda: each(False)), timed(lambda: each(True))
+            flop = 2.0 * S * R * N * K
+            out.append({"weights": scheme, "gemm": name, "N": N, "K": K, "stacked_6144_us": round(us_st, 1),
+                        "eight_768_one_stream_us": round(us_seq, 1), "eight_768_eight_streams_us": round(us_conc, 1),
+                        "stacked_tflops": round(flop / us_st / 1e6, 1)})
+            log(f"stack A/B {scheme} {name}: stacked {us_st:.0f} us, 8 x 768 {us_seq:.0f} us (one stream), "
+                f"{us_conc:.0f} us (8 streams)")
+    for st in streams:
+        dfx.check(L().dfx_stream_destroy(st), "stream")
+    return out
+
+
 def committed_traffic():
     """HBM bytes per Q4_K GEMM launch of this workload, from the committed rocprofv3
     counter summary (FETCH_SIZE / WRITE_SIZE scaled by a plain copy's readings), or
@@ -308,7 +497,26 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 3 device-to-device copies of 512 MiB (reference kernel for the "
                          "FETCH_SIZE / WRITE_SIZE counter scale) and exit")
+    ap.add_argument("--stack-ab", action="store_true",
+                    help="only time the batched unit's GEMMs stacked (6144 rows) against 8 x 768 rows, print one "
+                         "JSON line and exit")
+    ap.add_argument("--cpu-full", action="store_true",
+                    help="only time one whole full-depth generation of the headline workload on the CPU oracle "
+                         "(minutes of host time), print one JSON line and exit")
+    ap.add_argument("--ceiling", action="store_true",
+                    help="only measure the GEMM ceiling evidence (sustained MFMA rate, hipBLASLt f16 and the exact "
+                         "Q4_K GEMM at the headline's shapes), print one JSON line and exit")
     args = ap.parse_args()
+    if args.ceiling:
+        print(json.dumps(ceiling()))
+        return
+    if args.stack_ab:
+        print(json.dumps({"stack_ab": stack_ab()}))
+        return
+    if args.cpu_full:
+        host = host_cpu()
+        print(json.dumps(cpu_full_generate(ensure_model(), args.cpu_threads or host["threads_granted"], host)))
+        return
     if args.copy_calibration:
         n = 512 << 20
         a, b = dfx.Buf(n), dfx.Buf(n)
@@ -390,14 +598,18 @@ def main():
         configs["ar_dream7b_q4km_decode"] = config_ar()
         log(f"AR workload took {time.time() - t:.1f}s")
         t = time.time()
-        configs["batched_8x768_llada8b_q8_0"] = config_batched()
-        log(f"batched long-context workload took {time.time() - t:.1f}s")
+        configs["batched_8x768_llada8b_q8_0"] = config_batched("q8_0")
+        log(f"batched long-context workload (Q8_0) took {time.time() - t:.1f}s")
+        t = time.time()
+        configs["batched_8x768_llada8b_f16"] = config_batched("f16")
+        log(f"batched long-context workload (F16) took {time.time() - t:.1f}s")
 
     cpu = None
     if not args.no_cpu:
-        n_thr = args.cpu_threads or min(os.cpu_count() or 1, 16)
+        host = host_cpu()
+        n_thr = args.cpu_threads or host["threads_granted"]
         t = time.time()
-        cpu = cpu_baseline(path, rows, n_thr)
+        cpu = cpu_baseline(path, rows, n_thr, host)
         log(f"cpu baseline leg took {time.time() - t:.1f}s")
 
     out = {
@@ -445,8 +657,10 @@ def main():
         "other_workloads": configs,
     }
     if cpu:
-        out["vs_cpu"] = round(out["value"] / cpu["value"], 1)
-        out["vs_cpu_at_reference_rate"] = round(out["value"] / cpu["value_at_reference_rate"], 1)
+        # against the CPU path at the reference's published per-core rate (the oracle's own AVX2
+        # rate is lower, which would inflate the ratio), and against the oracle as timed
+        out["vs_cpu"] = round(out["value"] / cpu["value_at_reference_rate"], 1)
+        out["vs_cpu_oracle_as_timed"] = round(out["value"] / cpu["value"], 1)
     print(json.dumps(out))
 
 

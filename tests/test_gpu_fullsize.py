@@ -5,8 +5,8 @@ against the oracle: the first (full) denoising step and one cached step of
     benchmark's model file and prompt;
   * Dream-7B Q4_K_M, 64 prompt + 64 masks (GQA 28/4, Q/K/V bias, V = 152064);
   * the batched long-context unit: one 512 + 256 sequence (M = 768) on LLaDA-8B Q8_0
-    weights, and on F16 weights with two layers of the same width (the F16 oracle sums in
-    double and a 32-layer pass over 768 rows would take minutes of host time).
+    weights and on LLaDA-8B F16 weights (32 layers; the F16 oracle sums in double, a minute
+    or two of host time per pass).
 
 Bar: rel-L2 <= 1e-2 and >= 99% argmax agreement on the rows the sampler reads; the
 quantised models are expected (and asserted) to give the oracle's floats exactly.
@@ -100,10 +100,12 @@ def test_llada8b_q8_0_long_context_unit(gpu, say):
     _step0_and_cached(say, path, 512, 256, 5, 126000, 1, exact=True)
 
 
-def test_llada8b_width_f16_long_context_unit(gpu, say):
-    arch = dict(dfx.LLADA_8B, n_layer=2)
-    say("model llada8b-2l f16 seed 5 (generated on first use)")
-    path = big_model("llada8b-2l", arch, "f16", 5)
+def test_llada8b_f16_long_context_unit(gpu, say):
+    """The batched unit on F16 weights at full depth (32 layers, 768 rows): F16 GEMMs add their
+    exact f16 x f16 products in f32 in another order than the oracle's double sums, so this is
+    held to the bar, not to equality.  The oracle's pass takes a minute or two of host time."""
+    say("model llada8b f16 seed 5 (generated on first use)")
+    path = big_model("llada8b", dfx.LLADA_8B, "f16", 5)
     _step0_and_cached(say, path, 512, 256, 5, 126000, 1, exact=False)
 
 
