@@ -733,69 +733,152 @@ __global__ void __launch_bounds__(256) k_attn_long(const float * __restrict__ q,
     }
 }
 
-// Few query rows (autoregressive decoding: one row per token): one workgroup per (row, head),
-// in the oracle's own order: each score is one thread's sequential f64 dot product over the
-// head's dimensions (f32 x f32 products are exact in f64), rounded to float and scaled; the
-// exponentials are computed in parallel and summed in double by one thread in key order; each
-// output dimension is one thread's sequential f64 sum over the keys in key order.  Keys are
-// the cache positions in order, so a pass whose keys are its positions 0..n-1 (decoding)
-// repeats the oracle's sums exactly.  At most ROWS_MAX_KEYS visible keys per row.
+// Few query rows (autoregressive decoding: one row per token): one workgroup of 4 waves per
+// (row, head) instead of a 16-row tile per head.  Scores: 16 lanes per key, each adding the
+// products of its HD/16 dimensions in f64 (f32 x f32 products are exact there), the 16 partial
+// sums added by an xor butterfly, rounded to float and scaled; 16 keys per round.  Softmax as the
+// oracle: max, e = (float)exp((double)(s - max)), sum in double, p = e * (float)(1 / sum).
+// Output: HD dimensions x 256/HD key ranges per workgroup, each range summed in f64 in key order
+// (16-byte loads of the transposed value cache), the ranges' f64 sums added in order, rounded to
+// float once.  Only the f64 summation order differs from the oracle's (as in the matrix-core
+// kernels): a float result differs where two orders straddle a rounding boundary.
+// At most ROWS_MAX_KEYS visible keys per row.
 #define ROWS_MAX_KEYS 1024
 template <int HD>
 __global__ void __launch_bounds__(256) k_attn_rows(const float * __restrict__ q, const float * __restrict__ kc,
                                                    const float * __restrict__ vt, int64_t v_ld, int M, int n_keys,
                                                    int H, int Hkv, int q_pos0, int window, float * __restrict__ out) {
 #pragma clang fp contract(off)
-    __shared__ __attribute__((aligned(16))) float qs[HD];
+    constexpr int DPL = HD / 16;            // dimensions per lane of a key's group
+    constexpr int PARTS = 256 / HD;         // key ranges of the output sums
     __shared__ float sc[ROWS_MAX_KEYS];
     __shared__ float red[4];
-    __shared__ float inv_s;
+    __shared__ double red_d[4];
+    __shared__ double part[PARTS][HD];
     const int h = blockIdx.x % H, row = blockIdx.x / H;
     const int kvh = h / (H / Hkv);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const key_range kr = row_keys(row, M, n_keys, q_pos0, window);
     const int nk = kr.hi - kr.lo + 1;
     const float scale = 1.0f / sqrtf((float)HD);
-    if (tid < HD) qs[tid] = q[((int64_t)row * H + h) * HD + tid];
-    __syncthreads();
+    const int sub = lane & 15, grp = (tid >> 4);            // grp: key slot 0..15 of a round
+    float qd[DPL];
+    {
+        const float * qr = q + ((int64_t)row * H + h) * HD + DPL * sub;
+#pragma unroll
+        for (int i = 0; i < DPL; i += 4) {
+            const float4 v = *(const float4 *)(qr + i);
+            qd[i] = v.x; qd[i + 1] = v.y; qd[i + 2] = v.z; qd[i + 3] = v.w;
+        }
+    }
+    // output work of this thread (used after the softmax): dimension d, key range pt of PARTS
+    // (range borders on multiples of 4 keys); the range's first PV x 4 values are requested now,
+    // so that their latency passes during the scores and the softmax
+    constexpr int PV = 8;
+    const int d = tid % HD, pt = tid / HD;
+    const int per = ((nk + PARTS - 1) / PARTS + 3) & ~3;
+    const int ra = kr.lo + pt * per, rb = min(kr.lo + (pt + 1) * per, kr.hi + 1);
+    const float * vr = vt + ((int64_t)kvh * HD + d) * v_ld;
+    const int pa = (ra + 3) & ~3;                 // first 16-byte aligned key of the range
+    float4 vpre[PV];
+#pragma unroll
+    for (int u = 0; u < PV; u++) vpre[u] = *(const float4 *)(vr + min(pa + 4 * u, (int)(v_ld - 4)));
     const int64_t kvstride = (int64_t)Hkv * HD;
     float mx = -INFINITY;
-    for (int j = tid; j < nk; j += 256) {
-        const float * kr4 = kc + (int64_t)(kr.lo + j) * kvstride + (int64_t)kvh * HD;
-        double acc = 0.0;
-#pragma unroll 8
-        for (int i = 0; i < HD; i += 4) {
-            const float4 k4 = *(const float4 *)(kr4 + i);
-            const float4 q4 = *(const float4 *)(qs + i);
-            acc = acc + (double)k4.x * (double)q4.x;
-            acc = acc + (double)k4.y * (double)q4.y;
-            acc = acc + (double)k4.z * (double)q4.z;
-            acc = acc + (double)k4.w * (double)q4.w;
+    // RK keys per lane group and round, all their loads issued before any arithmetic (a round
+    // at a time would wait out one memory latency per 16 keys)
+    constexpr int RK = 8;
+    for (int j0 = 0; j0 < nk; j0 += 16 * RK) {
+        float4 kv[RK][DPL / 4];
+#pragma unroll
+        for (int u = 0; u < RK; u++) {
+            const int j = min(j0 + grp + 16 * u, nk - 1);
+            const float * kp = kc + (int64_t)(kr.lo + j) * kvstride + (int64_t)kvh * HD + DPL * sub;
+#pragma unroll
+            for (int i = 0; i < DPL / 4; i++) kv[u][i] = *(const float4 *)(kp + 4 * i);
         }
-        const float sv = (float)acc * scale;
-        sc[j] = sv;
-        mx = fmaxf(mx, sv);
+#pragma unroll
+        for (int u = 0; u < RK; u++) {
+            double acc = 0.0;
+#pragma unroll
+            for (int i = 0; i < DPL / 4; i++) {
+                acc = acc + (double)kv[u][i].x * (double)qd[4 * i];
+                acc = acc + (double)kv[u][i].y * (double)qd[4 * i + 1];
+                acc = acc + (double)kv[u][i].z * (double)qd[4 * i + 2];
+                acc = acc + (double)kv[u][i].w * (double)qd[4 * i + 3];
+            }
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o, WAVE);
+            const int j = j0 + grp + 16 * u;
+            if (sub == 0 && j < nk) {
+                const float sv = (float)acc * scale;
+                sc[j] = sv;
+                mx = fmaxf(mx, sv);
+            }
+        }
     }
     mx = wave_max(mx);
     if (lane == 0) red[wv] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int j = tid; j < nk; j += 256) sc[j] = (float)exp((double)(sc[j] - mx));
-    __syncthreads();
-    if (tid == 0) {
-        double sum = 0.0;
-        for (int j = 0; j < nk; j++) sum += (double)sc[j];
-        inv_s = (float)(1.0 / sum);
+    double sum = 0.0;
+    for (int j = tid; j < nk; j += 256) {
+        const float e = (float)exp((double)(sc[j] - mx));
+        sc[j] = e;
+        sum += (double)e;
     }
+    sum = wave_sum_d(sum);
+    if (lane == 0) red_d[wv] = sum;
     __syncthreads();
-    const float inv = inv_s;
+    const float inv = (float)(1.0 / (((red_d[0] + red_d[1]) + red_d[2]) + red_d[3]));
     for (int j = tid; j < nk; j += 256) sc[j] = sc[j] * inv;
     __syncthreads();
-    if (tid < HD) {
-        const float * vr = vt + ((int64_t)kvh * HD + tid) * v_ld + kr.lo;
+    {
         double acc = 0.0;
-#pragma unroll 8
-        for (int j = 0; j < nk; j++) acc = acc + (double)vr[j] * (double)sc[j];
+        int n = ra;
+        for (; n < rb && (n & 3); n++) acc = acc + (double)vr[n] * (double)sc[n - kr.lo];
+        // n == pa here (or the range is done): the prefetched 16-byte groups first
+#pragma unroll
+        for (int u = 0; u < PV; u++) {
+            if (n + 4 <= rb) {
+                const float * pp = sc + (n - kr.lo);
+                acc = acc + (double)vpre[u].x * (double)pp[0];
+                acc = acc + (double)vpre[u].y * (double)pp[1];
+                acc = acc + (double)vpre[u].z * (double)pp[2];
+                acc = acc + (double)vpre[u].w * (double)pp[3];
+                n += 4;
+            }
+        }
+        // 16 keys (four 16-byte loads) in flight per step
+        for (; n + 16 <= rb; n += 16) {
+            float4 v4[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) v4[u] = *(const float4 *)(vr + n + 4 * u);
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float * pp = sc + (n + 4 * u - kr.lo);
+                acc = acc + (double)v4[u].x * (double)pp[0];
+                acc = acc + (double)v4[u].y * (double)pp[1];
+                acc = acc + (double)v4[u].z * (double)pp[2];
+                acc = acc + (double)v4[u].w * (double)pp[3];
+            }
+        }
+        for (; n + 4 <= rb; n += 4) {
+            const float4 v4 = *(const float4 *)(vr + n);
+            const float * pp = sc + (n - kr.lo);
+            acc = acc + (double)v4.x * (double)pp[0];
+            acc = acc + (double)v4.y * (double)pp[1];
+            acc = acc + (double)v4.z * (double)pp[2];
+            acc = acc + (double)v4.w * (double)pp[3];
+        }
+        for (; n < rb; n++) acc = acc + (double)vr[n] * (double)sc[n - kr.lo];
+        part[pt][d] = acc;
+    }
+    __syncthreads();
+    if (tid < HD) {
+        double acc = part[0][tid];
+#pragma unroll
+        for (int pt = 1; pt < PARTS; pt++) acc += part[pt][tid];
         out[(int64_t)row * H * HD + (int64_t)h * HD + tid] = (float)acc;
     }
 }

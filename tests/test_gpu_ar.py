@@ -74,10 +74,10 @@ def test_attention_causal_matches_oracle(gpu, M, n_keys, q_pos0, window, H, Hkv,
     (1, 1024, 1023, 0, 8, 2, 64),      # the most keys of the few-row kernel
     (4, 700, 696, 100, 4, 1, 128),     # four rows with a window
     (2, 65, -1, 0, 4, 4, 128)])        # bidirectional (no mask)
-def test_attention_few_rows_equals_oracle_exactly(gpu, M, n_keys, q_pos0, window, H, Hkv, hd):
-    """At most 4 query rows and 1024 keys (decoding): one workgroup per row and head, summing
-    in the oracle's order (sequential f64 dot per score, double exp-sum and P.V sums in key
-    order), so the result is the oracle's floats."""
+def test_attention_few_rows_matches_oracle(gpu, M, n_keys, q_pos0, window, H, Hkv, hd):
+    """At most 4 query rows and 1024 keys (decoding): one workgroup per row and head.  The same
+    f64 sums of exact products as the oracle in another order: equal floats except where two
+    orders straddle an f32 rounding boundary (at most one ulp, rare)."""
     rng = np.random.default_rng(M * 7 + n_keys)
     q = rng.standard_normal((M, H, hd)).astype(np.float32)
     k = rng.standard_normal((n_keys, Hkv, hd)).astype(np.float32)
@@ -94,7 +94,8 @@ def test_attention_few_rows_equals_oracle_exactly(gpu, M, n_keys, q_pos0, window
         dfx.check(L().dfx_attention(qb.ptr, kb.ptr, vb.ptr, v_ld, M, n_keys, H, Hkv, hd, ob.ptr, None), "attention")
         ref = O.attention(q, k, v)
     got = ob.download(np.float32, shape=(M, H, hd))
-    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), float(np.mean(got != ref))
+    ulps = np.abs(got.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+    assert ulps.max() <= 1 and (ulps > 0).sum() <= 2, (int(ulps.max()), int((ulps > 0).sum()))
 
 
 def test_attention_causal_rejects_queries_past_the_keys(gpu):
