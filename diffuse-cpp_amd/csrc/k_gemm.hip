@@ -1913,16 +1913,29 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
     //   M <= 48 (outside the sweep, weight-bandwidth-bound): 32x128, 4-deep ring, split
     //     K while the grid leaves the SIMDs short of a wave each.
     // The choice only changes speed: every variant gives the same bits.
+    //   32 < M <= 48, wide (at least 160 column tiles) or over more than two chunks: the
+    //     64-row DMA tile (every weight dequantised once for all rows), K split only over
+    //     many chunks (Dream-7B gate|up and down at 34-48 rows: 15-18 % faster than 32-row
+    //     tiles);
+    //   64 < M <= 96, unless narrow over at most two chunks: one 96-row tile (k_q4k_w<3, 1, 2>),
+    //     K split over many chunks or on grids under 160 workgroups (LLaDA-8B Q|K|V, gate|up
+    //     and down at 74 and 96 rows: 2-15 % faster than 64-row tiles).
+    // "Narrow" is at most 40 column tiles (Dream-7B's Q|K|V, 36 tiles, runs best as the 32-tile
+    // O and down projections do).
     const int chunks = dot_chunks(K);
     const int n_col = (N + 127) / 128;
-    const bool narrow = n_col <= 32;
+    const bool narrow = n_col <= 40;
     const bool can_split = chunks > 1 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
     int pick = C_2x1x2;   // register-ring 64x128 (when the DMA kernel is not used)
-    bool dma = true, split = false;
+    bool dma = true, split = false, rows96 = false;
     if (M <= 48) {
-        dma = false;
-        pick = C_1x1x4;
-        split = can_split && (int64_t)n_col * ((M + 31) / 32) * 4 < 1024;
+        if (M > 32 && (n_col >= 160 || chunks > 2)) {
+            split = can_split && chunks > 2;
+        } else {
+            dma = false;
+            pick = C_1x1x4;
+            split = can_split && (int64_t)n_col * ((M + 31) / 32) * 4 < 1024;
+        }
     } else if (M > 128 && M < 150) {
         dma = false;
         pick = narrow && chunks > 2 ? C_1x1x2 : C_1x1x4;
@@ -1931,10 +1944,9 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
         dma = false;
         pick = C_1x1x2;
         split = can_split;
-    } else if (narrow && chunks > 2 && M > 64 && M <= 80) {
-        dma = false;
-        pick = C_1x1x2;
-        split = can_split;
+    } else if (M > 64 && M <= 96) {
+        rows96 = true;
+        split = can_split && (chunks > 2 || n_col < 160);
     } else {
         split = can_split && (chunks > 2 || (int64_t)n_col * ((M + 63) / 64) < 160);
     }
@@ -1998,6 +2010,9 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
                                          defer, epi);
         }
     }
+    if (rows96 && !f.on)
+        return launch_q4k_w<3, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, split ? (float *)ws : nullptr, st,
+                                     defer, epi);
     if (dma) return launch_q4k_w<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, split ? (float *)ws : nullptr, st, defer, epi);
     if (cands[pick].d == 4 && (sb_last % 2))
         for (int c = 0; c < n_cand; c++)
