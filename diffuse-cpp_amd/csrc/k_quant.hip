@@ -174,32 +174,17 @@ __device__ __forceinline__ void convert_block256(const float v[4], int lane, int
     }
 }
 
-// BPW (row, 256-block) units per wave, units wid * BPW .. (row-major over the blocks), all
-// loads issued before the first conversion: a unit's conversion is a chain of dependent steps
-// (loads, the wave-wide max, two divisions, stores), and two chains per wave halve the number
-// of waves and let one chain's latency hide the other's.
-template <int BPW>
+// One wave per (row, 256-block).
 __global__ void k_act_convert(int mode, const float * x, int64_t M, int64_t K, uint8_t * act) {
     const int lane = threadIdx.x & 63;
     const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    const int64_t nb = K >> 8, units = M * nb;
-    if (wid * BPW >= units) return;
+    const int64_t nb = K >> 8;
+    if (wid >= M * nb) return;
+    const int64_t m = wid / nb, b = wid - m * nb;
     const act_layout Lay = act_layout_of(mode, M, K);
-    float4 t[BPW];
-#pragma unroll
-    for (int j = 0; j < BPW; j++) {
-        const int64_t u = min(wid * BPW + j, units - 1);   // clamped: the duplicate is not converted
-        t[j] = *(const float4 *)(x + u * 256 + 4 * lane);  // unit u = row u / nb, block u % nb
-    }
-#pragma unroll
-    for (int j = 0; j < BPW; j++) {
-        const int64_t u = wid * BPW + j;
-        if (u < units) {
-            const int64_t m = u / nb, b = u - m * nb;
-            const float v[4] = {t[j].x, t[j].y, t[j].z, t[j].w};
-            convert_block256(v, lane, mode, act, Lay, m, K, b);
-        }
-    }
+    const float4 t = *(const float4 *)(x + m * K + b * 256 + 4 * lane);
+    const float v[4] = {t.x, t.y, t.z, t.w};
+    convert_block256(v, lane, mode, act, Lay, m, K, b);
 }
 
 // RMSNorm + weight + conversion; one workgroup of up to 16 waves per row.  Wave wv
@@ -238,17 +223,17 @@ __global__ void __launch_bounds__(1024) k_rmsnorm_convert(int mode, float * x, c
         for (int j = 0; j < BPW; j++) {
             const int b = min(wv * BPW + j, nb - 1);
             float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            // eight slices in flight at a time (the O and down projections leave two and six),
-            // added in slice order.  Loads past the last slice read the last slice again and
-            // add +0 instead: v starts at +0 and so is never -0, and v + 0 = v for every other v.
-            for (int s0 = 0; s0 < n_part; s0 += 8) {
-                float4v p[8];
+            // four slices in flight at a time, added in slice order.  Loads past the last
+            // slice read the last slice again and add +0 instead: v starts at +0 and so is
+            // never -0, and v + 0 = v for every other v.
+            for (int s0 = 0; s0 < n_part; s0 += 4) {
+                float4v p[4];
 #pragma unroll
-                for (int u = 0; u < 8; u++)
+                for (int u = 0; u < 4; u++)
                     p[u] = *(const float4v *)(pr + min(s0 + u, n_part - 1) * part_stride + (int64_t)b * 256);
                 const float4v z = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
+                for (int u = 0; u < 4; u++) {
                     const float4v q = s0 + u < n_part ? p[u] : z;
                     v.x = v.x + q.x;
                     v.y = v.y + q.y;
@@ -356,17 +341,9 @@ extern "C" int dfx_act_convert(int wtype, const float * x, int64_t M, int64_t K,
         return DFX_ERR_UNSUPPORTED;
     }
     if (M == 0) return DFX_OK;
-    // two units per wave once there are more units than the chip holds waves at one unit each
-    // (256 CUs x 32 waves)
-    const int64_t units = M * (K >> 8);
-    if (units > 8192) {
-        const int64_t waves = (units + 1) / 2;
-        hipLaunchKernelGGL(k_act_convert<2>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
-                           conv_mode(wtype), x, M, K, (uint8_t *)act);
-    } else {
-        hipLaunchKernelGGL(k_act_convert<1>, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
-                           conv_mode(wtype), x, M, K, (uint8_t *)act);
-    }
+    const int64_t waves = M * (K >> 8);
+    hipLaunchKernelGGL(k_act_convert, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
+                       conv_mode(wtype), x, M, K, (uint8_t *)act);
     DFX_CHECK_LAUNCH("dfx_act_convert");
     return DFX_OK;
 }
