@@ -299,7 +299,7 @@ k_mmq(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
     constexpr int BSTR = 24;                     // LDS halves per row of 16 block sums
     __shared__ __attribute__((aligned(16))) uint8_t Ws[BN * WSTR];
     __shared__ __attribute__((aligned(16))) half_t As[BM * ASTR];
-    __shared__ __attribute__((aligned(16))) float Ad[BM * 4];          // KQ: [BM]; Q8_0: [BM][4]
+    __shared__ __attribute__((aligned(16))) float Ad[BM * 4];          // KQ: [BM]; Q8_0: [4][BM]
     __shared__ __attribute__((aligned(16))) half_t Abs[KQ ? BM * BSTR : 8];
 
     const int tid = threadIdx.x, lane = tid & 63, wn = tid >> 6;
@@ -339,7 +339,11 @@ k_mmq(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
                 if (tid < 2 * BM) *(uint4 *)(Abs + (tid >> 1) * BSTR + (tid & 1) * 8) = bsreg;
             }
         } else if (tid < BM) {
-            *(float4 *)(Ad + tid * 4) = dreg4;
+            // [block][row]: a lane's four consecutive tile rows of one block are one 16-byte read
+            Ad[tid] = dreg4.x;
+            Ad[BM + tid] = dreg4.y;
+            Ad[2 * BM + tid] = dreg4.z;
+            Ad[3 * BM + tid] = dreg4.w;
         }
     };
 
@@ -393,15 +397,24 @@ k_mmq(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
                     u[j] = 8 * (sc * ((q6 >> 3) - 4));
                     u2[j] = sc * (q6 & 7);
                 }
-            } else {   // Q8_0
-                const uint2 q = *(const uint2 *)(wp + 16 + e);
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    u[j] = (int8_t)(q.x >> (8 * j));
-                    u[4 + j] = (int8_t)(q.y >> (8 * j));
-                }
             }
-            const half8 b = to_half8(u);
+            half8 b;
+            if (WT == DFX_TYPE_Q8_0) {
+                // int8 q as an exact f16 integer without conversions: q + 128 (the byte with its
+                // top bit flipped) becomes the mantissa of 0x6400 = 1024.0 (v_perm places two bytes
+                // beside 0x64 bytes), and one packed f16 add of -1152 leaves q
+                const uint2 qw = *(const uint2 *)(wp + 16 + e);
+                const uint32_t x0 = qw.x ^ 0x80808080u, x1 = qw.y ^ 0x80808080u;
+                const u32x4 pk = {__builtin_amdgcn_perm(x0, 0x64646464u, 0x00050004u),
+                                  __builtin_amdgcn_perm(x0, 0x64646464u, 0x00070006u),
+                                  __builtin_amdgcn_perm(x1, 0x64646464u, 0x00050004u),
+                                  __builtin_amdgcn_perm(x1, 0x64646464u, 0x00070006u)};
+                const half8 off = {(half_t)-1152.0f, (half_t)-1152.0f, (half_t)-1152.0f, (half_t)-1152.0f,
+                                   (half_t)-1152.0f, (half_t)-1152.0f, (half_t)-1152.0f, (half_t)-1152.0f};
+                b = __builtin_bit_cast(half8, pk) + off;
+            } else {
+                b = to_half8(u);
+            }
             half8 b2;
             if (WT == DFX_TYPE_Q6_K) b2 = to_half8(u2);
 #pragma unroll
@@ -416,9 +429,14 @@ k_mmq(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
                 const float dw = h2f(*(const uint16_t *)(wp + 2 * (4 * h + bl)));
 #pragma unroll
                 for (int i = 0; i < TM; i++) {
+                    // registers 4g..4g+3 hold rows 8g + 4(lane/32) + 0..3: one 16-byte read each
+                    // from the [block][row] layout of Ad
                     float dav[16];
 #pragma unroll
-                    for (int r = 0; r < 16; r++) dav[r] = Ad[(i * 32 + tile_row(r, lane)) * 4 + bl];
+                    for (int g = 0; g < 4; g++) {
+                        const float4 d4 = *(const float4 *)(Ad + bl * BM + i * 32 + 8 * g + 4 * hl);
+                        dav[4 * g] = d4.x; dav[4 * g + 1] = d4.y; dav[4 * g + 2] = d4.z; dav[4 * g + 3] = d4.w;
+                    }
                     flush_d(S1[i], P[i], dw, dav);
 #pragma unroll
                     for (int r = 0; r < 16; r++) P[i][r] = 0.0f;
