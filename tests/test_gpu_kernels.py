@@ -127,6 +127,8 @@ GEMM_CASES = [(dfx.TYPE_Q4_K, 4096, 4096, m) for m in (1, 5, 50, 96, 128, 255, 2
     (dfx.TYPE_Q8_0, 1024, 4096, 300),
     # batched long-context workload: one 512 + 256 sequence's step-0 rows on Q8_0 weights
     (dfx.TYPE_Q8_0, 4096, 4096, 768), (dfx.TYPE_Q8_0, 4096, 12288, 768),
+    # Q8_0 grids wide enough for 64-row tiles (Q|K|V at 768 rows; gate|up over a ragged 300)
+    (dfx.TYPE_Q8_0, 12288, 4096, 768), (dfx.TYPE_Q8_0, 24576, 4096, 300),
     # LLaDA-8B fused gate|up and vocab head at the benchmark's step 0
     (dfx.TYPE_Q4_K, 24576, 4096, 288), (dfx.TYPE_Q6_K, 126464, 4096, 288),
     # Dream-7B: fused Q|K|V, gate|up, down, vocab head (steps of 128 and 64 rows)
