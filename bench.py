@@ -497,6 +497,8 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 3 device-to-device copies of 512 MiB (reference kernel for the "
                          "FETCH_SIZE / WRITE_SIZE counter scale) and exit")
+    ap.add_argument("--only", choices=("llada_b64", "dream", "sampler", "ar", "batched_q8_0", "batched_f16"),
+                    help="only run one of the other workloads, print its JSON line and exit (for profiling)")
     ap.add_argument("--stack-ab", action="store_true",
                     help="only time the batched unit's GEMMs stacked (6144 rows) against 8 x 768 rows, print one "
                          "JSON line and exit")
@@ -509,6 +511,17 @@ def main():
     args = ap.parse_args()
     if args.ceiling:
         print(json.dumps(ceiling()))
+        return
+    if args.only:
+        runs = {"dream": config_dream, "sampler": config_sampler, "ar": config_ar,
+                "batched_q8_0": lambda: config_batched("q8_0"), "batched_f16": lambda: config_batched("f16")}
+        if args.only == "llada_b64":
+            model = dfx.Model(ensure_model())
+            res = config_llada_b64(model)
+            model.close()
+        else:
+            res = runs[args.only]()
+        print(json.dumps({args.only: res}))
         return
     if args.stack_ab:
         print(json.dumps({"stack_ab": stack_ab()}))
