@@ -301,8 +301,8 @@ def config_batched(scheme="q8_0"):
 
 def config_sampler():
     """The sampler over [256 x 126464] f32 logits N(0, sigma), sigma in {0.5, 2, 8} (seed 4):
-    row statistics (softmax max / sum, entropy, top-2), candidate records and the selection
-    of the 16 to unmask (256 / 16), on device.  HBM rate of the statistics pass: the logits
+    row statistics (softmax max / sum, entropy, top-2), then candidate records and the
+    selection of the 16 to unmask (256 / 16) in one launch, on device.  HBM rate of the statistics pass: the logits
     block read once (129.5 MB) over its time."""
     R, V, L = 256, 126464, dfx.lib
     rows = dfx.Buf.of(np.arange(R, dtype=np.int32))
@@ -312,10 +312,10 @@ def config_sampler():
     for sigma in (0.5, 2.0, 8.0):
         x = dfx.Buf.of(np.random.default_rng(4).standard_normal((R, V), dtype=np.float32) * np.float32(sigma))
 
-        def run():
+        def run():   # as the device loop runs a step's sampler: statistics, then candidates + selection
             dfx.check(L().dfx_row_stats(x.ptr, V, rows.ptr, R, V, st.ptr, None), "row_stats")
-            dfx.check(L().dfx_make_candidates(st.ptr, pos.ptr, R, 0, cand.ptr, None), "candidates")
-            dfx.check(L().dfx_select(cand.ptr, R, dfx.ENTROPY_EXIT, 1.5, R // 16, order.ptr, nun.ptr, None), "select")
+            dfx.check(L().dfx_select_from_stats(st.ptr, pos.ptr, R, dfx.ENTROPY_EXIT, 1.5, R // 16, cand.ptr,
+                                                order.ptr, nun.ptr, None), "select")
 
         def timed(fn, reps=20):
             for _ in range(3):

@@ -263,6 +263,48 @@ __global__ void __launch_bounds__(SEL_THREADS) k_select(const dfx_candidate * __
     }
 }
 
+// Candidates from the row statistics (as k_make_candidates) and their selection (as k_select)
+// in one workgroup, for at most SEL_FUSED_MAX candidates: candidate i goes to place
+// rank(i) = #{j : key j before key i} (sel_key below: the policy key, then the position), a
+// strict total order, so this is k_select's order; the candidates are also written out (the
+// unmask step reads them).
+#define SEL_FUSED_MAX 1024
+__device__ __forceinline__ uint64_t sel_key(const dfx_candidate & c, bool by_entropy);
+__global__ void __launch_bounds__(SEL_FUSED_MAX) k_select_stats(const dfx_row_stat * __restrict__ st,
+                                                                const int32_t * __restrict__ pos, int n, int margin,
+                                                                int by_entropy, float tau, int n_sched,
+                                                                dfx_candidate * __restrict__ cand,
+                                                                int32_t * __restrict__ order,
+                                                                int32_t * __restrict__ n_unmask) {
+#pragma clang fp contract(off)
+    __shared__ uint64_t key[SEL_FUSED_MAX];
+    __shared__ int n_easy;
+    const int tid = threadIdx.x;
+    if (tid == 0) n_easy = 0;
+    __syncthreads();
+    uint64_t me = 0;
+    if (tid < n) {
+        const dfx_row_stat s = st[tid];
+        dfx_candidate c;
+        c.pos = pos[tid];
+        c.token = s.token;
+        c.confidence = margin ? (s.best - s.second) : s.best;
+        c.entropy = s.entropy;
+        cand[tid] = c;
+        me = sel_key(c, by_entropy != 0);
+        key[tid] = me;
+        if (by_entropy && c.entropy < tau) atomicAdd(&n_easy, 1);
+    }
+    __syncthreads();
+    if (tid < n) {
+        int rank = 0;
+        // equal keys (only if a caller repeats a position) keep the input order
+        for (int j = 0; j < n; j++) rank += (key[j] < me || (key[j] == me && j < tid)) ? 1 : 0;
+        order[rank] = tid;
+    }
+    if (tid == 0) *n_unmask = min(by_entropy ? max(n_sched, n_easy) : n_sched, n);
+}
+
 // More candidates than one workgroup sorts: the key order (ties by position) is a strict
 // total order, so candidate i goes to place rank(i) = #{j : j before i}.  Each thread ranks
 // one candidate against all of them, read in 1024-candidate tiles through LDS.
@@ -307,6 +349,31 @@ __global__ void __launch_bounds__(1024) k_select_count(const dfx_candidate * __r
             if (!(cand[order[r]].entropy < tau)) atomicMin(&first_hard, r);
     __syncthreads();
     if (threadIdx.x == 0) *n_unmask = min(by_entropy ? max(n_sched, first_hard) : n_sched, n);
+}
+
+extern "C" int dfx_select_from_stats(const dfx_row_stat * stats, const int32_t * pos, int n, int remasking,
+                                     float tau, int n_sched, dfx_candidate * cand, int32_t * order,
+                                     int32_t * n_unmask, void * stream) {
+    if (n < 0 || remasking < 0 || remasking > 4 || remasking == 1 ||
+        (n > 0 && (!stats || !pos || !cand || !order || !n_unmask))) {
+        dfx_set_error("dfx_select_from_stats: unsupported n=%d or remasking=%d", n, remasking);
+        return DFX_ERR_ARG;
+    }
+    const int margin = remasking == 4 ? 1 : 0;
+    if (n > SEL_FUSED_MAX) {
+        const int rc = dfx_make_candidates(stats, pos, n, margin, cand, stream);
+        if (rc != DFX_OK) return rc;
+        return dfx_select(cand, n, remasking, tau, n_sched, order, n_unmask, stream);
+    }
+    if (n == 0) {
+        hipLaunchKernelGGL(k_select_stats, dim3(1), dim3(64), 0, (hipStream_t)stream, stats, pos, 0, margin,
+                           remasking == 2 ? 1 : 0, tau, n_sched, cand, order, n_unmask);
+    } else {
+        hipLaunchKernelGGL(k_select_stats, dim3(1), dim3((unsigned)((n + 63) / 64 * 64)), 0, (hipStream_t)stream,
+                           stats, pos, n, margin, remasking == 2 ? 1 : 0, tau, n_sched, cand, order, n_unmask);
+    }
+    DFX_CHECK_LAUNCH("dfx_select_from_stats");
+    return DFX_OK;
 }
 
 extern "C" int dfx_select(const dfx_candidate * cand, int n, int remasking, float tau, int n_sched, int32_t * order,

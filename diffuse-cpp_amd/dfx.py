@@ -140,6 +140,7 @@ def _declare(L):
         "dfx_attention_ex": (I32, [P, P, P, I64, I64, I64, I32, I32, I32, P, I32, P]),
         "dfx_row_stats": (I32, [P, I64, P, I64, I64, P, P]),
         "dfx_select": (I32, [P, I32, I32, F, I32, P, P, P]),
+        "dfx_select_from_stats": (I32, [P, P, I32, I32, F, I32, P, P, P, P]),
         "dfx_make_candidates": (I32, [P, P, I32, I32, P, P]),
         "dfx_quantize_rows": (I32, [I32, P, I64, I64, P]),
         "dfx_quantize_file": (I32, [C.c_char_p, C.c_char_p, C.c_char_p, I32]),

@@ -535,9 +535,8 @@ int generate_device(diffuse_context * c, const int32_t * prompt, int n_prompt, i
         TRY(forward_head(c, M, n_head, c->d_hrows, c->d_hmap, pending));
         const int n_sched = tokens_to_unmask(s, p.n_steps, n_masked, p.schedule);
         TRY(dfx_row_stats(c->logits, V, c->d_srows, n_masked, V, c->d_stats, c->stream));
-        TRY(dfx_make_candidates(c->d_stats, c->d_spos, n_masked, p.remasking == 4 ? 1 : 0, c->d_cand, c->stream));
-        TRY(dfx_select(c->d_cand, n_masked, p.remasking, p.entropy_threshold, n_sched, c->d_order, c->d_nun,
-                       c->stream));
+        TRY(dfx_select_from_stats(c->d_stats, c->d_spos, n_masked, p.remasking, p.entropy_threshold, n_sched,
+                                  c->d_cand, c->d_order, c->d_nun, c->stream));
         TRY(dfx_step_unmask(N, use_cache ? 1 : 0, s, d_seq, d_prev, d_msk, c->d_cand, c->d_order, c->d_nun, n_masked,
                             unmask_step ? d_ustep : nullptr, c->d_hist, c->stream));
         TRY(hip_ok(hipMemcpyAsync(c->h_hist + s, c->d_hist + s, 4, hipMemcpyDeviceToHost, c->stream), "D2H"));

@@ -259,6 +259,13 @@ int dfx_make_candidates(const dfx_row_stat * stats, const int32_t * pos, int n, 
 int dfx_select(const dfx_candidate * cand, int n, int remasking, float tau, int n_sched,
                int32_t * order, int32_t * n_unmask, void * stream);
 
+/* dfx_make_candidates (margin for TOPK_MARGIN) followed by dfx_select in one launch
+ * (src/diffuse-sampler.cpp:253-255 and 277-305 as one step): writes cand[0..n), order[0..n)
+ * and *n_unmask exactly as the two calls do.  Up to 1024 candidates in one workgroup that
+ * places each candidate by rank; more run as the two calls. */
+int dfx_select_from_stats(const dfx_row_stat * stats, const int32_t * pos, int n, int remasking, float tau,
+                          int n_sched, dfx_candidate * cand, int32_t * order, int32_t * n_unmask, void * stream);
+
 /* Device-resident step bookkeeping of the denoising loop.  The sequence state is device
  * int32 arrays of N: seq (ids), prev (seq right after the last forward), masked (0/1),
  * lastc (step of the last change seen, -1 never).

@@ -630,6 +630,36 @@ def test_select_bit_exact(gpu, remasking):
         assert int(nb.download(np.int32)[0]) == n_ref
 
 
+@pytest.mark.parametrize("remasking", [0, 2, 3, 4])
+@pytest.mark.parametrize("n", [1, 17, 256, 1000, 1024, 1025])
+def test_select_from_stats_equals_the_two_calls(gpu, remasking, n):
+    """dfx_select_from_stats (candidates and selection in one launch, by rank up to 1024
+    candidates) writes the candidates, the order and the unmask count of dfx_make_candidates
+    + dfx_select, with many equal keys (ties broken by position)."""
+    st = np.zeros(n, dfx.ROW_STAT)
+    st["token"] = rng.integers(0, 1000, n)
+    st["best"] = rng.integers(0, 20, n).astype(np.float32) * 0.25
+    st["second"] = st["best"] - rng.integers(0, 8, n).astype(np.float32) * 0.25
+    st["entropy"] = rng.integers(0, 12, n).astype(np.float32) * 0.25
+    st["best"][:2] = [0.0, -0.0][:n]               # -0 and +0 compare equal: position decides
+    pos = rng.permutation(4 * n)[:n].astype(np.int32)
+    n_sched = int(rng.integers(1, n + 1))
+    sb, pb = dfx.Buf.of(st), dfx.Buf.of(pos)
+    outs = []
+    for fused in (False, True):
+        cb, ob, nb = dfx.Buf(n * 16), dfx.Buf(n * 4), dfx.Buf(4)
+        if fused:
+            dfx.check(L().dfx_select_from_stats(sb.ptr, pb.ptr, n, remasking, 1.5, n_sched, cb.ptr, ob.ptr, nb.ptr,
+                                                None), "select_from_stats")
+        else:
+            dfx.check(L().dfx_make_candidates(sb.ptr, pb.ptr, n, 1 if remasking == 4 else 0, cb.ptr, None), "cand")
+            dfx.check(L().dfx_select(cb.ptr, n, remasking, 1.5, n_sched, ob.ptr, nb.ptr, None), "select")
+        outs.append((cb.download(np.uint8).tobytes(), ob.download(np.int32), int(nb.download(np.int32)[0])))
+    assert outs[0][0] == outs[1][0]
+    assert np.array_equal(outs[0][1], outs[1][1])
+    assert outs[0][2] == outs[1][2]
+
+
 @pytest.mark.parametrize("remasking", [0, 2, 4])
 @pytest.mark.parametrize("n", [2049, 5000, 9000])
 def test_select_beyond_one_workgroup_bit_exact(gpu, remasking, n):
