@@ -339,6 +339,22 @@ def config_sampler():
 LLADA_Q4K_SHAPES = (("q|k|v", 12288, 4096), ("o", 4096, 4096), ("gate|up", 24576, 4096), ("down", 4096, 12288))
 
 
+def sustained_mfma_rate():
+    """The dense f16 rate this chip sustains: `mfma-rate` (back-to-back independent
+    v_mfma_f32_32x32x16_f16 on one CU, then on every SIMD), run as a child process; None when
+    the probe is not built."""
+    import subprocess
+    exe = os.path.join(REPO, "diffuse-cpp_amd", "bin", "mfma-rate")
+    if not os.path.exists(exe):
+        return None
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    if r.returncode != 0:
+        raise RuntimeError(f"mfma-rate failed: {r.stderr[-500:]}")
+    d = json.loads(r.stdout.strip().splitlines()[-1])
+    return {"all_cus_tflops": d["all_cus_tflops"], "one_cu_scaled_to_chip_tflops": d["one_cu_scaled_to_chip_tflops"],
+            "unit": "TFLOP/s", "probe": "diffuse-cpp_amd/bin/mfma-rate"}
+
+
 def ceiling(rows=(288, 256, 97, 74, 50), reps=20):
     """Evidence for the GEMM ceiling at the headline's shapes (LLaDA-8B, M = 288 / 256):
       * mfma-rate: back-to-back independent f16 MFMAs on one CU and on every SIMD (the
@@ -581,6 +597,7 @@ def main():
     prof = {t: ctx.profile_read(t) for t in (dfx.TYPE_Q4_K, dfx.TYPE_Q6_K)}
     q4_big = ctx.profile_read(dfx.TYPE_Q4_K, 1)     # M > 96: MFMA-bound shapes (mostly k_q4k_w<2, 1, 2>)
     q4_small = ctx.profile_read(dfx.TYPE_Q4_K, 2)   # M <= 96: weight-bandwidth-bound shapes
+    q4_full = ctx.profile_read(dfx.TYPE_Q4_K, 3)    # M >= 288: the step-0 forward over every row
     ctx.profile(False)
     ctx.close()
 
@@ -592,6 +609,8 @@ def main():
     achieved = q4_big["flops"] / (q4_big["ms"] * 1e-3) / 1e12 if q4_big["ms"] > 0 else 0.0
     achieved_all = q4["flops"] / (q4["ms"] * 1e-3) / 1e12 if q4["ms"] > 0 else 0.0
     small_gbs = q4_small["bytes"] / (q4_small["ms"] * 1e-3) / 1e9 if q4_small["ms"] > 0 else 0.0
+    achieved_full = q4_full["flops"] / (q4_full["ms"] * 1e-3) / 1e12 if q4_full["ms"] > 0 else 0.0
+    sustained = sustained_mfma_rate()
 
     configs = None
     if not args.no_configs:
@@ -661,6 +680,13 @@ def main():
             "gemm_share_of_time": round((q4["ms"] + prof[dfx.TYPE_Q6_K]["ms"]) / (1000 * elapsed_prof), 4),
             "events_pass_tok_s": round(B * args.steps / elapsed_prof, 2),
             "all_q4k_calls_tflops": round(achieved_all, 2),
+            "at_m_ge_288": {"kernel": "Q4_K GEMM calls over at least 288 rows (the step-0 forward)",
+                            "achieved": round(achieved_full, 2), "frac": round(achieved_full / MFMA_F16_PEAK_TFLOPS, 4),
+                            "launches": q4_full["launches"],
+                            "avg_launch_us": round(1000 * q4_full["ms"] / max(q4_full["launches"], 1), 3),
+                            "frac_of_sustained": (round(achieved_full / sustained["all_cus_tflops"], 4)
+                                                  if sustained else None)},
+            "sustained_mfma_f16": sustained,
             "small_rows": {"kernel": "Q4_K GEMM calls over at most 96 rows", "bound": "hbm",
                            "achieved": round(small_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(small_gbs / HBM_PEAK_GBS, 4), "launches": q4_small["launches"],

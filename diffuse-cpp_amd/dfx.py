@@ -458,7 +458,7 @@ class Context:
 
     def profile_read(self, wtype, rows_class=0):
         """{launches, ms, flops, bytes} of the GEMMs on weights of type wtype since profiling began;
-        rows_class 1 = launches over more than 96 rows, 2 = at most 96, 0 = all."""
+        rows_class 1 = launches over more than 96 rows, 2 = at most 96, 3 = at least 288, 0 = all."""
         n, ms, fl, by = C.c_int64(), C.c_double(), C.c_double(), C.c_double()
         check(lib().dfx_context_profile_read_rows(self.h, wtype, rows_class, C.byref(n), C.byref(ms), C.byref(fl),
                                                   C.byref(by)), "dfx_context_profile_read_rows")

@@ -224,7 +224,8 @@ void prof_collect(diffuse_context * c) {
     for (auto & r : c->prof_pending) {
         float ms = 0.0f;
         if (hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess && r.type >= 0 && r.type < 32)
-            for (int cls : {0, r.M > 96 ? 1 : 2}) {
+            for (int cls : {0, r.M > 96 ? 1 : 2, r.M >= 288 ? 3 : -1}) {
+                if (cls < 0) continue;
                 auto & t = c->prof_tot[cls][r.type];
                 t.launches++;
                 t.ms += ms;
@@ -648,7 +649,7 @@ int engine_profile(diffuse_context * c, bool enable) {
 
 int engine_profile_read(diffuse_context * c, int wtype, int rows_class, int64_t * launches, double * ms,
                         double * flops, double * bytes) {
-    if (wtype < 0 || wtype >= 32 || rows_class < 0 || rows_class > 2) return DFX_ERR_ARG;
+    if (wtype < 0 || wtype >= 32 || rows_class < 0 || rows_class > 3) return DFX_ERR_ARG;
     TRY(hip_ok(hipStreamSynchronize(c->stream), "profile"));
     prof_collect(c);
     const auto & t = c->prof_tot[rows_class][wtype];

@@ -155,8 +155,8 @@ struct diffuse_context {
     std::vector<gemm_rec> prof_pending;      // launched, not yet read
     std::vector<hipEvent_t> prof_pool;       // reusable events
     struct prof_total { long launches = 0; double ms = 0, flops = 0, bytes = 0; };
-    // by row class (0 every launch, 1 M > 96, 2 M <= 96) and weight type id
-    prof_total            prof_tot[3][32];
+    // by row class (0 every launch, 1 M > 96, 2 M <= 96, 3 M >= 288) and weight type id
+    prof_total            prof_tot[4][32];
 };
 
 // Options of one forward pass (the autoregressive graph of src/ar-graph.cpp:27-260):

@@ -399,7 +399,8 @@ int  dfx_context_profile(dfx_context * c, int enable);
 int  dfx_context_profile_read(dfx_context * c, int wtype, int64_t * launches, double * ms, double * flops,
                               double * bytes);
 /* The same totals for one class of row counts: rows_class 1 = GEMMs over M > 96 rows (the
- * 64-row-tile Q4_K kernel's range), 2 = M <= 96, 0 = all (as dfx_context_profile_read).
+ * 64-row-tile Q4_K kernel's range), 2 = M <= 96, 3 = M >= 288 (a full forward of 288 or more
+ * rows), 0 = all (as dfx_context_profile_read).
  * Build-defined instrumentation; no counterpart in the reference. */
 int  dfx_context_profile_read_rows(dfx_context * c, int wtype, int rows_class, int64_t * launches, double * ms,
                                    double * flops, double * bytes);

@@ -400,6 +400,30 @@ def test_generate_cache_off_equals_full_forward_loop(gpu, tiny_models):
     model.close()
 
 
+def test_gemm_profile_row_classes(gpu, tiny_models):
+    """Per-GEMM timing by row class: a 300-row forward counts in classes 1 (> 96 rows) and 3
+    (>= 288 rows), a 50-row forward in class 2 only; class 0 holds every launch."""
+    model = dfx.Model(tiny_models[("llada", "q4_k_m")])
+    ctx = dfx.Context(model, 320)
+    ctx.profile(True)
+    ctx.forward(np.arange(300, dtype=np.int32) % 1400)
+    big = [ctx.profile_read(dfx.TYPE_Q4_K, c) for c in range(4)]
+    assert big[0]["launches"] > 0 and big[2]["launches"] == 0
+    assert big[0] == big[1] == big[3]
+    assert big[3]["ms"] > 0
+    ctx.forward(np.arange(50, dtype=np.int32))
+    after = [ctx.profile_read(dfx.TYPE_Q4_K, c) for c in range(4)]
+    assert after[1] == big[1] and after[3] == big[3]
+    assert after[2]["launches"] == big[0]["launches"]
+    assert after[0]["launches"] == 2 * big[0]["launches"]
+    assert after[2]["flops"] * 300 == pytest.approx(big[3]["flops"] * 50)
+    with pytest.raises(RuntimeError):
+        ctx.profile_read(dfx.TYPE_Q4_K, 4)
+    ctx.profile(False)
+    ctx.close()
+    model.close()
+
+
 def test_contexts_generate_concurrently(gpu, tiny_models):
     """Independent sequences (the batched long-context workload's unit): several contexts
     share one model (read-only after load, as in the reference, main-bench.cpp:153) and
