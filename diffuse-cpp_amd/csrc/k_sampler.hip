@@ -11,7 +11,7 @@
 // The reference drops terms with p <= 1e-10 (at most V * 2.3e-9 in all, far less for any
 // real row) and adds 126464 float terms one after another, whose rounding walk is ~1e-5
 // relative; here exp is the transcendental unit's 2^(x log2 e) (about 1 ulp), per-thread
-// sums are float and the sums across threads double.
+// sums are float (T in base-2 units, one fma per element) and the sums across threads double.
 #include "dfx_device.h"
 
 #include <algorithm>
@@ -39,7 +39,9 @@ __device__ __forceinline__ top2_t top2_shfl(top2_t v, int off) {
     return o;
 }
 
-__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+#define LOG2E_F 1.44269504088896341f
+#define LN2_D 0.69314718055994530942
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * LOG2E_F); }
 
 // running top-2 of one element (elements arrive in increasing index order per thread)
 __device__ __forceinline__ void top2_push(top2_t & t, float e, int i) {
@@ -60,27 +62,31 @@ __global__ void __launch_bounds__(RS_THREADS) k_row_stats(const float * __restri
 
     // top-2, and S / T relative to this thread's running maximum m
     top2_t t = {-INFINITY, 0x7fffffff, -INFINITY};
-    float m = -INFINITY, s = 0.0f, tm = 0.0f;
-    // one element e (at most the running m) into S and T; d is clamped where exp(d) is
-    // already 0 in float, so that a -inf logit adds 0 * (-256), not 0 * -inf
+    // T is kept in base-2 units while the row is scanned (tm = sum p * d2 with d2 = (x - m) log2 e
+    // formed by one fma), and converted to natural units once at the end.
+    float m = -INFINITY, m2 = -INFINITY, s = 0.0f, tm = 0.0f;   // m2 = m log2 e
+    // one element e (at most the running m) into S and T; d2 is clamped where exp2(d2) is
+    // already 0 in float, so that a -inf logit adds 0 * (-370), not 0 * -inf
     auto add = [&](float e) __attribute__((always_inline)) {
-        const float d = fmaxf(e - m, -256.0f);
-        const float p = exp_fast(d);
+        const float d2 = fmaxf(fmaf(e, LOG2E_F, -m2), -370.0f);
+        const float p = __builtin_amdgcn_exp2f(d2);
         s = s + p;
-        tm = tm + p * d;
+        tm = fmaf(p, d2, tm);
     };
     // raise the running maximum to m4 >= m, rescaling S and T
     auto raise = [&](float m4) __attribute__((always_inline)) {
+        const float m42 = m4 * LOG2E_F;
         if (m == -INFINITY) {
             s = 0.0f;
             tm = 0.0f;
         } else {
-            const float d = m - m4;
-            const float r = exp_fast(d);
-            tm = r * (tm + d * s);
+            const float d2 = m2 - m42;
+            const float r = __builtin_amdgcn_exp2f(d2);
+            tm = r * fmaf(d2, s, tm);
             s = r * s;
         }
         m = m4;
+        m2 = m42;
     };
     if (vec) {
         // RS_UNROLL float4 loads in flight per thread, from clamped addresses; elements past
@@ -136,7 +142,7 @@ __global__ void __launch_bounds__(RS_THREADS) k_row_stats(const float * __restri
     if (m != -INFINITY) {
         const double d = (double)m - (double)mx, r = (double)exp_fast(m - mx);
         sd = r * (double)s;
-        td = r * ((double)tm + d * (double)s);
+        td = r * ((double)tm * LN2_D + d * (double)s);   // tm back to natural units
     }
     sd = wave_sum_d(sd);
     td = wave_sum_d(td);
