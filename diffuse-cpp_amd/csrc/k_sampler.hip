@@ -17,7 +17,7 @@
 #include <algorithm>
 
 #define RS_THREADS 1024
-#define RS_UNROLL 4
+#define RS_UNROLL 2
 
 struct top2_t { float best; int idx; float second; };
 
@@ -89,12 +89,17 @@ __global__ void __launch_bounds__(RS_THREADS) k_row_stats(const float * __restri
         m2 = m42;
     };
     if (vec) {
-        // RS_UNROLL float4 loads in flight per thread, from clamped addresses; elements past
-        // the row end read as -inf (no effect on top-2, exp(-inf) = 0)
-        for (int i0 = 4 * tid; i0 < V; i0 += 4 * RS_UNROLL * RS_THREADS) {
-            float4 v[RS_UNROLL];
+        // RS_UNROLL float4 per thread and pass, the next pass's loads issued before this pass's
+        // elements are used; clamped addresses (loads past the row's end re-read its last
+        // float4, and such elements are skipped)
+        constexpr int STEP = 4 * RS_UNROLL * RS_THREADS;
+        float4 v[RS_UNROLL], nx[RS_UNROLL];
 #pragma unroll
-            for (int u = 0; u < RS_UNROLL; u++) v[u] = *(const float4 *)(x + min(i0 + 4 * u * RS_THREADS, V - 4));
+        for (int u = 0; u < RS_UNROLL; u++) v[u] = *(const float4 *)(x + min(4 * tid + 4 * u * RS_THREADS, V - 4));
+        for (int i0 = 4 * tid; i0 < V; i0 += STEP) {
+#pragma unroll
+            for (int u = 0; u < RS_UNROLL; u++)
+                nx[u] = *(const float4 *)(x + min(i0 + STEP + 4 * u * RS_THREADS, V - 4));
 #pragma unroll
             for (int u = 0; u < RS_UNROLL; u++) {
                 const int i = i0 + 4 * u * RS_THREADS;
@@ -115,6 +120,8 @@ __global__ void __launch_bounds__(RS_THREADS) k_row_stats(const float * __restri
                     add(v[u].w);
                 }
             }
+#pragma unroll
+            for (int u = 0; u < RS_UNROLL; u++) v[u] = nx[u];
         }
     } else {
         for (int i = tid; i < V; i += RS_THREADS) {
