@@ -1428,6 +1428,184 @@ k_q6k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
 }
 
 // ---------------------------------------------------------------------------
+// Q6_K, LDS-DMA fed: k_q6k's operands, sums and flush inside k_q4k_w's pipeline.  A 64 x 128
+// workgroup tile (TM = 2 row tiles of 32, four waves side by side, 32 weight rows each); one
+// K step (128 elements, half a super-block) is requested one step ahead, in this order:
+//   NA = 2 * TM copies global -> LDS of the step's fragment-ordered A (shared by the waves);
+//   even steps: the 16 scale bytes and the d word of the wave's rows (register loads);
+//   odd steps: the super-block's activation scales d_a of rows m0.. (one copy per wave into
+//     its own 1 KB of LDS, read only by that wave);
+//   three 16-byte register loads per lane of ql (quarters p and p + 2) and qh.
+// Loads complete in issue order: the top-of-step wait leaves only the step's own scale and
+// weight loads in flight (after the barrier the next step's loads are issued); before the
+// weights are used, only the next step's loads.
+template <int TM>
+__global__ void __launch_bounds__(256, 2)
+k_q6k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__ act, int M,
+        const float * __restrict__ bias, const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
+        int n_tiles, int m_tiles, float * __restrict__ ws, dfx_epi epi) {
+#pragma clang fp contract(off)
+    constexpr int BM = 32 * TM, NA = 2 * TM;
+    static_assert(TM == 2 && NA <= 4, "64-row tiles");
+    __shared__ __attribute__((aligned(1024))) half_t As0[BM * 128], As1[BM * 128];
+    __shared__ __attribute__((aligned(1024))) uint8_t Ds[4 * 1024];   // [wave][1 KB]: d_a of rows m0..
+    auto aslot = [&](auto stage) __attribute__((always_inline)) -> half_t * {
+        if constexpr (decltype(stage)::value == 0) return As0;
+        else return As1;
+    };
+
+    const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
+    const int z = blockIdx.x / per_pass, L = blockIdx.x - z * per_pass, xcd = L & 7, j = L >> 3;
+    const int ty = j % m_tiles, tx = 8 * (j / m_tiles) + xcd;
+    if (tx >= n_tiles) return;
+
+    const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n0 = tx * 128, m0 = ty * BM;
+    constexpr int SB_CHUNK = DFX_DOT_CHUNK / 256;
+    const int n_sb_all = K >> 8;
+    const int sb_first = ws ? z * SB_CHUNK : 0;
+    const int n_sb = ws ? min(SB_CHUNK, n_sb_all - sb_first) : n_sb_all;
+    const int n_kt = 2 * n_sb;
+    const uint32_t row_bytes = (uint32_t)n_sb_all * SB_Q6_K;
+    const act_layout Lay = act_layout_of(CONV_Q8_K_P6, M, K);
+    const int m_pad = (int)act_q_rows(CONV_Q8_K_P6, M);
+
+    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void *)W, 0, 0xFFFFFFFF, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc((void *)act, 0, (int)Lay.bytes, 0x00020000);
+
+    // (fixed size: this clang drops the host stub of a kernel template whose lambdas capture a
+    // local array sized by a template parameter)
+    uint32_t off_a[4];   // this wave copies A operands NA*wv.. of the step: row tile f/8, operand f%8
+#pragma unroll
+    for (int f = 0; f < NA; f++) {
+        const int ff = NA * wv + f, mt = min(m0 / 32 + (ff >> 3), m_pad / 32 - 1);
+        off_a[f] = (uint32_t)Lay.q + (uint32_t)mt * (uint32_t)(K / 128) * 8192u + (uint32_t)(ff & 7) * 1024u +
+                   (uint32_t)lane * 16u;
+    }
+    const uint32_t off_w = (uint32_t)min(n0 + wv * 32 + l32, N - 1) * row_bytes;
+    // d_a is [sb][m_pad]: 1 KB from row m0 (BM of its rows are used; lanes past the buffer's
+    // end read nothing, the buffer's extent is set)
+    const uint32_t off_d = (uint32_t)Lay.d + (uint32_t)m0 * 4u + (uint32_t)lane * 16u;
+
+    u32x4 l_st[2][2], qh_st[2], sc_st;
+    uint32_t dw_st;
+    auto issue = [&](auto stage, int kt_req) __attribute__((always_inline)) {
+        constexpr int h = decltype(stage)::value;   // DEPTH 2: the stage is the step's parity
+        const int kt = 2 * sb_first + min(kt_req, n_kt - 1);
+        const int sb = kt >> 1;
+#pragma unroll
+        for (int f = 0; f < NA; f++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_ptr)(aslot(stage) + (NA * wv + f) * 512), 16, off_a[f],
+                                                     kt * 8192, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (h == 0) {
+            sc_st = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rW, off_w + 192, sb * SB_Q6_K, 0));
+            dw_st = __builtin_amdgcn_raw_buffer_load_b32(rW, off_w + 208, sb * SB_Q6_K, 0);
+        } else {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_ptr)(Ds + 1024 * wv), 16, off_d, sb * m_pad * 4, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        l_st[h][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rW, off_w + 64 * h + 16 * hl,
+                                                                                        sb * SB_Q6_K, 0));
+        l_st[h][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rW, off_w + 64 * h + 32 + 16 * hl,
+                                                                                        sb * SB_Q6_K, 0));
+        qh_st[h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rW, off_w + 128 + 32 * h + 16 * hl,
+                                                                                     sb * SB_Q6_K, 0));
+    };
+    // loads per step after its A copies: even 2 + 3, odd 1 + 3; per step in all: NA + those
+    constexpr int AFTER_A_EVEN = 5, AFTER_A_ODD = 4;
+
+    float16v P[TM], S[TM], T[TM];
+    const float16v zero16 = {};
+#pragma unroll
+    for (int i = 0; i < TM; i++) { P[i] = zero16; S[i] = zero16; T[i] = zero16; }
+    u32x4 sc4;
+    uint32_t dwh = 0;
+    const uint32_t M78 = opaque(0x00780078u), MG58 = opaque(0x58005800u), M300 = opaque(0x03000300u),
+                   MG44 = opaque(0x44004400u);
+
+    auto step = [&](auto stage, int kt) __attribute__((always_inline)) {
+        constexpr int h = decltype(stage)::value;
+        // this step's A copies done (its scale and weight loads may still be in flight), and
+        // every LDS read of the previous step done before the barrier
+        constexpr int WAIT_TOP = waitcnt_vm_lgkm(h == 0 ? AFTER_A_EVEN : AFTER_A_ODD, 0);
+        // everything of this step done, the next step's loads (NA + its scale and weight
+        // loads) still in flight
+        constexpr int WAIT_W = waitcnt_vm_lgkm(NA + (h == 0 ? AFTER_A_ODD : AFTER_A_EVEN), 15);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(WAIT_TOP);
+        barrier_only();
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (h == 0) {
+            // the super-block's scales and d (loaded with this step) before the next step's loads
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm(3, 15));
+            sc4 = sc_st;
+            dwh = dw_st;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        issue(std::integral_constant<int, h ^ 1>{}, kt + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(WAIT_W);
+        __builtin_amdgcn_sched_barrier(0);
+        const half_t * As = aslot(stage);
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            // quarters p and p+2 of this half: sub-blocks 8h + 2q + g
+            const q6k_qc ka = q6k_quarter_consts(q6k_scale(sc4, 8 * h + 2 * p + hl));
+            const q6k_qc kb = q6k_quarter_consts(q6k_scale(sc4, 8 * h + 2 * (p + 2) + hl));
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int kk = i + 4 * p;
+                half8 blo, bhi;
+                q6k_word(p, l_st[h][p][i], qh_st[h][i], ka, kb, blo, bhi, M78, MG58, M300, MG44);
+#pragma unroll
+                for (int ii = 0; ii < TM; ii++) {
+                    const half8 a = *(const half8 *)(As + (8 * ii + kk) * 512 + 8 * lane);
+                    P[ii] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, blo, (h == 0 && kk == 0) ? zero16 : P[ii], 0, 0,
+                                                                   0);
+                    P[ii] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bhi, P[ii], 0, 0, 0);
+                }
+            }
+        }
+        if constexpr (h == 1) {
+            // super-block complete: x = d_w*isum; S = fma(d_a, x, S)
+            const float dw = h2f((uint16_t)(dwh & 0xFFFFu));
+            const float * Ad = (const float *)(Ds + 1024 * wv);
+#pragma unroll
+            for (int ii = 0; ii < TM; ii++) {
+                float dav[16];
+#pragma unroll
+                for (int q4 = 0; q4 < 4; q4++) {
+                    const float4 da = *(const float4 *)(Ad + ii * 32 + 8 * q4 + 4 * hl);
+                    dav[4 * q4] = da.x; dav[4 * q4 + 1] = da.y; dav[4 * q4 + 2] = da.z; dav[4 * q4 + 3] = da.w;
+                }
+                flush_d(S[ii], P[ii], dw, dav);
+            }
+        }
+    };
+
+    issue(std::integral_constant<int, 0>{}, 0);
+    for (int c0 = 0; c0 < n_kt; c0 += 2 * SB_CHUNK) {
+        const int c1 = min(c0 + 2 * SB_CHUNK, n_kt);
+        for (int kt0 = c0; kt0 < c1; kt0 += 2) {
+            step(std::integral_constant<int, 0>{}, kt0);
+            step(std::integral_constant<int, 1>{}, kt0 + 1);
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            T[i] = T[i] + S[i];
+            S[i] = zero16;
+        }
+    }
+    // the copies issued past the last step still land in this workgroup's LDS
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm(0, 0));
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+        epilogue_tile(T[i], m0 + i * 32, n0 + wv * 32 + l32, M, N, bias, res, Y, ldy, ymap, ws, z, lane, epi);
+}
+
+// ---------------------------------------------------------------------------
 // F16 weights
 // ---------------------------------------------------------------------------
 template <int TM>
@@ -1876,8 +2054,23 @@ static int launch_q6k(const void * w, int N, int K, const void * act, int M, con
     return DFX_OK;
 }
 
-// Q6_K: 64x128 workgroup tiles (2-deep weight ring), split K when the grid is small.
-// A forced tile "<TM>x<TN>[x<D>][s|n]" (dfx_gemm_force_tile) overrides the choice.
+template <int TM>
+static int launch_q6k_w(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
+                        float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st, int * defer,
+                        dfx_epi epi) {
+    const int n_tiles = (N + 127) / 128, m_tiles = (M + 32 * TM - 1) / (32 * TM);
+    const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
+    const int chunks = dot_chunks(K), passes = ws ? chunks : 1;
+    hipLaunchKernelGGL((k_q6k_w<TM>), dim3((unsigned)(per_pass * passes)), dim3(256), 0, st, (const uint8_t *)w, N, K,
+                       (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles, ws, epi);
+    DFX_CHECK_LAUNCH("dfx_gemm q6_k");
+    if (ws) return reduce_or_defer(ws, chunks, M, N, bias, res, y, ldy, ymap, st, defer, epi);
+    return DFX_OK;
+}
+
+// Q6_K: 64x128 workgroup tiles, the LDS-DMA kernel above 48 rows, the register-ring kernel
+// (32 rows, 2-deep weight ring) below; split K when the grid is small.  A forced tile
+// "<TM>x<TN>[x<D>][s|n]" (dfx_gemm_force_tile) picks a register-ring tile, "w" the DMA kernel.
 static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                         float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer,
                         dfx_epi epi) {
@@ -1886,9 +2079,11 @@ static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, c
     const int64_t tiles = (int64_t)((M + 32 * tm - 1) / (32 * tm)) * ((N + 128 * tn - 1) / (128 * tn));
     bool split = chunks > 1 && tiles * 4 < 1024 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
     int d = 2;
+    bool dma = tm == 2;
     if (const tile_force f = forced_tile(1); f.on) {
-        if (f.got >= 2 && ((f.tm == 1 || f.tm == 2) && f.tn == 1)) { tm = f.tm; tn = f.tn; }
+        if (f.got >= 2 && ((f.tm == 1 || f.tm == 2) && f.tn == 1)) { tm = f.tm; tn = f.tn; dma = false; }
         if (f.got == 3 && (f.d == 2 || f.d == 4)) d = f.d;
+        if (f.w) { tm = 2; dma = true; }
         if (f.split) split = chunks > 1 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
         if (f.nosplit) split = false;
     }
@@ -1896,6 +2091,7 @@ static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, c
     const int sb = K / 256, sb_last = sb - (chunks - 1) * (DFX_DOT_CHUNK / 256);
     if (sb_last % 2) d = 2;
     float * wsf = split ? (float *)ws : nullptr;
+    if (dma) return launch_q6k_w<2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi);
     if (tm == 2)
         return d == 4 ? launch_q6k<2, 1, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi)
                       : launch_q6k<2, 1, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi);

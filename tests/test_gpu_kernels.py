@@ -193,11 +193,11 @@ def test_gemm_q4k_split_k_bit_exact(gpu, tile, N, K, M):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
 
 
-@pytest.mark.parametrize("tile", ["2x1n", "1x1n", "2x1s", "1x1s", "2x1x4n", "2x1x4s", "1x1x4s"])
+@pytest.mark.parametrize("tile", ["2x1n", "1x1n", "2x1s", "1x1s", "2x1x4n", "2x1x4s", "1x1x4s", "wn", "ws"])
 @pytest.mark.parametrize("N,K,M", [(1000, 4096, 77), (640, 12288, 40), (300, 2304, 33)])
 def test_gemm_q6k_tiles_and_split_bit_exact(gpu, tile, N, K, M):
-    """Q6_K kernel tiles, with and without split K (scales up to +-127 exercise the
-    exact f16 operand split), against the oracle bit for bit."""
+    """Q6_K kernel tiles (register ring, and "w" the LDS-DMA kernel), with and without split K
+    (scales up to +-127 exercise the exact f16 operand split), against the oracle bit for bit."""
     raw = quant(dfx.TYPE_Q6_K, N, K)
     X = rng.standard_normal((M, K)).astype(np.float32)
     with forced_tile(dfx.TYPE_Q6_K, tile):
