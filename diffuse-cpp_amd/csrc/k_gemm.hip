@@ -1429,7 +1429,8 @@ k_q6k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
 
 // ---------------------------------------------------------------------------
 // Q6_K, LDS-DMA fed: k_q6k's operands, sums and flush inside k_q4k_w's pipeline.  A 64 x 128
-// workgroup tile (TM = 2 row tiles of 32, four waves side by side, 32 weight rows each); one
+// or 96 x 128 workgroup tile (TM = 2 or 3 row tiles of 32, four waves side by side, 32 weight
+// rows each); one
 // K step (128 elements, half a super-block) is requested one step ahead, in this order:
 //   NA = 2 * TM copies global -> LDS of the step's fragment-ordered A (shared by the waves);
 //   even steps: the 16 scale bytes and the d word of the wave's rows (register loads);
@@ -1446,7 +1447,7 @@ k_q6k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
         int n_tiles, int m_tiles, float * __restrict__ ws, dfx_epi epi) {
 #pragma clang fp contract(off)
     constexpr int BM = 32 * TM, NA = 2 * TM;
-    static_assert(TM == 2 && NA <= 4, "64-row tiles");
+    static_assert((TM == 2 || TM == 3) && NA <= 6, "64- or 96-row tiles");
     __shared__ __attribute__((aligned(1024))) half_t As0[BM * 128], As1[BM * 128];
     __shared__ __attribute__((aligned(1024))) uint8_t Ds[4 * 1024];   // [wave][1 KB]: d_a of rows m0..
     auto aslot = [&](auto stage) __attribute__((always_inline)) -> half_t * {
@@ -1476,7 +1477,7 @@ k_q6k_w(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict
 
     // (fixed size: this clang drops the host stub of a kernel template whose lambdas capture a
     // local array sized by a template parameter)
-    uint32_t off_a[4];   // this wave copies A operands NA*wv.. of the step: row tile f/8, operand f%8
+    uint32_t off_a[6];   // this wave copies A operands NA*wv.. of the step: row tile f/8, operand f%8
 #pragma unroll
     for (int f = 0; f < NA; f++) {
         const int ff = NA * wv + f, mt = min(m0 / 32 + (ff >> 3), m_pad / 32 - 1);
@@ -2068,22 +2069,28 @@ static int launch_q6k_w(const void * w, int N, int K, const void * act, int M, c
     return DFX_OK;
 }
 
-// Q6_K: 64x128 workgroup tiles, the LDS-DMA kernel above 48 rows, the register-ring kernel
-// (32 rows, 2-deep weight ring) below; split K when the grid is small.  A forced tile
-// "<TM>x<TN>[x<D>][s|n]" (dfx_gemm_force_tile) picks a register-ring tile, "w" the DMA kernel.
+// Q6_K: above 48 rows the LDS-DMA kernel, with 96-row tiles where they pad M to no more rows
+// than 64-row tiles (ties included), else 64-row tiles; at most 48 rows the register-ring
+// kernel (32 rows, 2-deep weight ring).  Split K when the grid is small.  Measured on MI355X at
+// the LLaDA-8B vocab head (126464 x 4096) and Q6_K down projection (4096 x 12288) and the
+// Dream-7B ones, every variant the same bits: 96-row tiles 10-30 % faster at 74, 162, 181 and
+// 288 rows, 25-50 % slower at 97 and 120 (192 rows of tiles against 128), even at 240 and
+// 2-20 % slower at 256 (288 against 256); the DMA kernel 2-5 % faster than the register ring at
+// 64-row tiles.  A forced tile "<TM>x<TN>[x<D>][s|n]" (dfx_gemm_force_tile) picks a
+// register-ring tile, "w" / "w1" the 64-row and "w3" the 96-row DMA kernel.
 static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                         float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer,
                         dfx_epi epi) {
-    int tm = M > 48 ? 2 : 1, tn = 1;
+    bool dma = M > 48;
+    int tm = !dma ? 1 : (M + 95) / 96 * 96 <= (M + 63) / 64 * 64 ? 3 : 2, tn = 1;
     const int chunks = dot_chunks(K);
     const int64_t tiles = (int64_t)((M + 32 * tm - 1) / (32 * tm)) * ((N + 128 * tn - 1) / (128 * tn));
     bool split = chunks > 1 && tiles * 4 < 1024 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
     int d = 2;
-    bool dma = tm == 2;
     if (const tile_force f = forced_tile(1); f.on) {
         if (f.got >= 2 && ((f.tm == 1 || f.tm == 2) && f.tn == 1)) { tm = f.tm; tn = f.tn; dma = false; }
         if (f.got == 3 && (f.d == 2 || f.d == 4)) d = f.d;
-        if (f.w) { tm = 2; dma = true; }
+        if (f.w) { tm = f.w3 ? 3 : 2; dma = true; }
         if (f.split) split = chunks > 1 && ws && ws_bytes >= (size_t)chunks * M * N * sizeof(float);
         if (f.nosplit) split = false;
     }
@@ -2091,6 +2098,7 @@ static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, c
     const int sb = K / 256, sb_last = sb - (chunks - 1) * (DFX_DOT_CHUNK / 256);
     if (sb_last % 2) d = 2;
     float * wsf = split ? (float *)ws : nullptr;
+    if (dma && tm == 3) return launch_q6k_w<3>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi);
     if (dma) return launch_q6k_w<2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi);
     if (tm == 2)
         return d == 4 ? launch_q6k<2, 1, 4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi)

@@ -124,6 +124,8 @@ def test_swiglu_convert_matches_oracle(gpu):
 GEMM_CASES = [(dfx.TYPE_Q4_K, 4096, 4096, m) for m in (1, 5, 50, 96, 128, 255, 288)] + [
     (dfx.TYPE_Q4_K, 12288, 4096, 288), (dfx.TYPE_Q6_K, 4096, 4096, 64), (dfx.TYPE_Q6_K, 2048, 12288, 100),
     (dfx.TYPE_Q6_K, 1000, 4096, 288), (dfx.TYPE_Q8_0, 4096, 4096, 77), (dfx.TYPE_Q4_K, 4096, 12288, 288),
+    # Q6_K 96-row DMA tiles: split K over 74 rows, whole K over 162
+    (dfx.TYPE_Q6_K, 2048, 12288, 74), (dfx.TYPE_Q6_K, 3000, 4096, 162),
     (dfx.TYPE_Q8_0, 1024, 4096, 300),
     # batched long-context workload: one 512 + 256 sequence's step-0 rows on Q8_0 weights
     (dfx.TYPE_Q8_0, 4096, 4096, 768), (dfx.TYPE_Q8_0, 4096, 12288, 768),
@@ -193,7 +195,7 @@ def test_gemm_q4k_split_k_bit_exact(gpu, tile, N, K, M):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
 
 
-@pytest.mark.parametrize("tile", ["2x1n", "1x1n", "2x1s", "1x1s", "2x1x4n", "2x1x4s", "1x1x4s", "wn", "ws"])
+@pytest.mark.parametrize("tile", ["2x1n", "1x1n", "2x1s", "1x1s", "2x1x4n", "2x1x4s", "1x1x4s", "wn", "ws", "w3n", "w3s"])
 @pytest.mark.parametrize("N,K,M", [(1000, 4096, 77), (640, 12288, 40), (300, 2304, 33)])
 def test_gemm_q6k_tiles_and_split_bit_exact(gpu, tile, N, K, M):
     """Q6_K kernel tiles (register ring, and "w" the LDS-DMA kernel), with and without split K
