@@ -91,6 +91,33 @@ __device__ __forceinline__ void store_q4(uint16_t * dst, const uint16_t o[4]) {
     *(uint64_t *)dst = packed;
 }
 
+// Lane-to-lane moves inside rows of 16 lanes (DPP: no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+#define DPP_QUAD_1032 0xB1   // quad_perm [1, 0, 3, 2]: lane ^ 1
+#define DPP_QUAD_2301 0x4E   // quad_perm [2, 3, 0, 1]: lane ^ 2
+#define DPP_ROW_HALF_MIRROR 0x141
+#define DPP_ROW_MIRROR 0x140
+
+// Maximum over the (fully active) wave of non-negative, non-NaN v: within each row of 16
+// lanes by DPP, then over the four rows' results read out of lanes 0, 16, 32, 48.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    v = fmaxf(v, dpp_f<DPP_QUAD_1032>(v));
+    v = fmaxf(v, dpp_f<DPP_QUAD_2301>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_MIRROR>(v));
+    const int b = __float_as_int(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0)), r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32)), r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 // row m, block b (256 elements) of a [M][K] activation
 __device__ __forceinline__ void convert_block256(const float v[4], int lane, int mode, uint8_t * act,
                                                  const act_layout & Lay, int64_t m, int64_t K, int64_t b) {
@@ -105,24 +132,27 @@ __device__ __forceinline__ void convert_block256(const float v[4], int lane, int
         // GGML quantize_row_q8_K_ref: max = the signed value of the first element
         // with the largest |x|; iscale = -127/max; q = min(127, nearest_int(iscale*x));
         // d = 1/iscale; bsums over 16.  All-zero block -> d = 0, q = 0.
-        // one 64-bit key per element: |x| bits (ordered as |x| for non-negative floats),
-        // then the inverted element index (the first of equal |x| wins), then the sign;
-        // the largest key over the wave names max
-        unsigned long long key = 0;
+        // amax = the largest |x| over the block (a NaN never compares greater, as in the
+        // reference's |x| > amax scan: it counts as 0); max = the element with the lowest
+        // index among those with |x| = amax: the lowest lane holding one (ballot), its lowest j
+        uint32_t ab[4];
+        float a4 = 0.0f;
         for (int j = 0; j < 4; j++) {
-            const uint32_t ab = __float_as_uint(v[j]) & 0x7fffffffu;
-            // a NaN never compares greater, as in the reference's |x| > amax scan
-            const uint64_t kj = ab > 0x7f800000u ? 0ull
-                                                 : ((uint64_t)ab << 32) | ((uint64_t)(0xffffu - (4 * lane + j)) << 1) |
-                                                       (__float_as_uint(v[j]) >> 31);
-            key = kj > key ? kj : key;
+            ab[j] = __float_as_uint(v[j]) & 0x7fffffffu;
+            if (ab[j] > 0x7f800000u) ab[j] = 0u;
+            a4 = fmaxf(a4, __uint_as_float(ab[j]));
         }
-        for (int off = 32; off > 0; off >>= 1) {
-            const unsigned long long o = __shfl_xor(key, off, WAVE);
-            key = o > key ? o : key;
-        }
-        const float amax = __uint_as_float((uint32_t)(key >> 32));
-        const float mx = (key & 1) ? -amax : amax;
+        const float amax = wave_max_nonneg(a4);
+        const uint32_t amax_bits = __float_as_uint(amax);
+        bool has = false;
+        int sign = 0;
+        for (int j = 3; j >= 0; j--)
+            if (ab[j] == amax_bits) {
+                has = true;
+                sign = (int)(__float_as_uint(v[j]) >> 31);
+            }
+        const int first = __builtin_ctzll(__ballot(has));   // amax is some element's |x|: has holds somewhere
+        const float mx = __builtin_amdgcn_readlane(sign, first) ? -amax : amax;
         int qi[4] = {0, 0, 0, 0};
         float d = 0.0f;
         if (amax != 0.0f) {
@@ -154,15 +184,18 @@ __device__ __forceinline__ void convert_block256(const float v[4], int lane, int
             *(uint32_t *)(act + Lay.i8 + m * K + b * 256 + 4 * lane) = w;
         }
         int s = qi[0] + qi[1] + qi[2] + qi[3];
-        s += __shfl_xor(s, 1, WAVE);
-        s += __shfl_xor(s, 2, WAVE);
+        s += dpp_i<DPP_QUAD_1032>(s);
+        s += dpp_i<DPP_QUAD_2301>(s);
         if ((lane & 3) == 0) ((uint16_t *)(act + Lay.bs))[m * (K / 16) + b * 16 + (lane >> 2)] = f2h((float)s);
         if (lane == 0) ((float *)(act + Lay.d))[conv_is_frag(mode) ? b * Lay.mq + m : m * (K / 256) + b] = d;
     } else if (mode == CONV_Q8_0) {
         // GGML quantize_row_q8_0_ref over 32-element blocks (8 lanes each):
         // d = amax/127, q = roundf(x * (1/d)), stored d rounded to f16.
         float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-        for (int off = 4; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, WAVE));
+        // over the block's 8 lanes (a half row of 16): lane ^ 1, lane ^ 2, then the mirrored quad
+        amax = fmaxf(amax, dpp_f<DPP_QUAD_1032>(amax));
+        amax = fmaxf(amax, dpp_f<DPP_QUAD_2301>(amax));
+        amax = fmaxf(amax, dpp_f<DPP_ROW_HALF_MIRROR>(amax));
         const float d = (float)((double)amax / 127.0);
         const float id = d != 0.0f ? (float)(1.0 / (double)d) : 0.0f;
         for (int j = 0; j < 4; j++) o[j] = f2h((float)(int)roundf(v[j] * id));
@@ -174,13 +207,16 @@ __device__ __forceinline__ void convert_block256(const float v[4], int lane, int
     }
 }
 
-// One wave per (row, 256-block).
-__global__ void k_act_convert(int mode, const float * x, int64_t M, int64_t K, uint8_t * act) {
+// One wave per (row, 256-block); a workgroup's eight waves take eight consecutive rows of one
+// block, so that in the matrix-core operand order (rows 16 bytes apart within an operand) the
+// workgroup's stores fill whole 128-byte lines instead of 16 bytes of each.
+#define AC_ROWS 8
+__global__ void __launch_bounds__(64 * AC_ROWS) k_act_convert(int mode, const float * x, int64_t M, int64_t K,
+                                                              uint8_t * act) {
     const int lane = threadIdx.x & 63;
-    const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    const int64_t nb = K >> 8;
-    if (wid >= M * nb) return;
-    const int64_t m = wid / nb, b = wid - m * nb;
+    const int64_t n_rg = (M + AC_ROWS - 1) / AC_ROWS;
+    const int64_t b = blockIdx.x / n_rg, m = AC_ROWS * (blockIdx.x - b * n_rg) + (threadIdx.x >> 6);
+    if (m >= M) return;
     const act_layout Lay = act_layout_of(mode, M, K);
     const float4 t = *(const float4 *)(x + m * K + b * 256 + 4 * lane);
     const float v[4] = {t.x, t.y, t.z, t.w};
@@ -341,8 +377,8 @@ extern "C" int dfx_act_convert(int wtype, const float * x, int64_t M, int64_t K,
         return DFX_ERR_UNSUPPORTED;
     }
     if (M == 0) return DFX_OK;
-    const int64_t waves = M * (K >> 8);
-    hipLaunchKernelGGL(k_act_convert, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
+    const int64_t groups = (K >> 8) * ((M + AC_ROWS - 1) / AC_ROWS);
+    hipLaunchKernelGGL(k_act_convert, dim3((unsigned)groups), dim3(64 * AC_ROWS), 0, (hipStream_t)stream,
                        conv_mode(wtype), x, M, K, (uint8_t *)act);
     DFX_CHECK_LAUNCH("dfx_act_convert");
     return DFX_OK;
