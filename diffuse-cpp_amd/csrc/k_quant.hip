@@ -240,7 +240,11 @@ __global__ void __launch_bounds__(1024) k_rmsnorm_convert(int mode, float * x, c
                                                           int64_t part_stride) {
 #pragma clang fp contract(off)
     __shared__ double red[16];
-    const int64_t m = blockIdx.x;
+    // Rows 64a + 8x .. 64a + 8x + 7 go to workgroups on XCD x (workgroup g runs on XCD g % 8):
+    // the eight rows whose operand-order activations share 128-byte lines are written through
+    // one L2 (a placement only: every row's arithmetic is its own).
+    const int64_t wg = blockIdx.x, m = 64 * (wg >> 6) + 8 * (wg & 7) + ((wg >> 3) & 7);
+    if (m >= M) return;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
     const int nb = (int)(K >> 8);
     const int64_t r = xmap ? xmap[m] : m;
@@ -401,8 +405,8 @@ static int rmsnorm_launch(int wtype, float * x, const int32_t * xmap, const floa
     const dim3 block((unsigned)(64 * ((nb + bpw - 1) / bpw)));
     auto kern = bpw == 1 ? k_rmsnorm_convert<1> : bpw == 2 ? k_rmsnorm_convert<2>
               : bpw == 4 ? k_rmsnorm_convert<4> : k_rmsnorm_convert<8>;
-    hipLaunchKernelGGL(kern, dim3((unsigned)M), block, 0, (hipStream_t)stream, conv_mode(wtype), x, xmap, w, M, K,
-                       eps, (uint8_t *)act, part, n_part, part_stride);
+    hipLaunchKernelGGL(kern, dim3((unsigned)((M + 63) / 64 * 64)), block, 0, (hipStream_t)stream, conv_mode(wtype), x,
+                       xmap, w, M, K, eps, (uint8_t *)act, part, n_part, part_stride);
     DFX_CHECK_LAUNCH("dfx_rmsnorm_convert");
     return DFX_OK;
 }
