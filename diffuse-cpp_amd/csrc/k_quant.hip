@@ -105,19 +105,6 @@ __device__ __forceinline__ int dpp_i(int v) {
 #define DPP_ROW_HALF_MIRROR 0x141
 #define DPP_ROW_MIRROR 0x140
 
-// Maximum over the (fully active) wave of non-negative, non-NaN v: within each row of 16
-// lanes by DPP, then over the four rows' results read out of lanes 0, 16, 32, 48.
-__device__ __forceinline__ float wave_max_nonneg(float v) {
-    v = fmaxf(v, dpp_f<DPP_QUAD_1032>(v));
-    v = fmaxf(v, dpp_f<DPP_QUAD_2301>(v));
-    v = fmaxf(v, dpp_f<DPP_ROW_HALF_MIRROR>(v));
-    v = fmaxf(v, dpp_f<DPP_ROW_MIRROR>(v));
-    const int b = __float_as_int(v);
-    const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0)), r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
-    const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32)), r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
-    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
-}
-
 // row m, block b (256 elements) of a [M][K] activation
 __device__ __forceinline__ void convert_block256(const float v[4], int lane, int mode, uint8_t * act,
                                                  const act_layout & Lay, int64_t m, int64_t K, int64_t b) {
@@ -142,7 +129,7 @@ __device__ __forceinline__ void convert_block256(const float v[4], int lane, int
             if (ab[j] > 0x7f800000u) ab[j] = 0u;
             a4 = fmaxf(a4, __uint_as_float(ab[j]));
         }
-        const float amax = wave_max_nonneg(a4);
+        const float amax = wave_max(a4);
         const uint32_t amax_bits = __float_as_uint(amax);
         bool has = false;
         int sign = 0;
