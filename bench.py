@@ -339,6 +339,54 @@ def config_sampler():
 LLADA_Q4K_SHAPES = (("q|k|v", 12288, 4096), ("o", 4096, 4096), ("gate|up", 24576, 4096), ("down", 4096, 12288))
 
 
+def q6k_tiles(reps=10):
+    """The Q6_K GEMM's tile choice at the Q6_K shapes of the benchmark models (LLaDA-8B vocab head
+    126464 x 4096 and down projection 4096 x 12288, Dream-7B head 152064 x 3584 and down 3584 x
+    18944) over the row counts their steps run: the built-in choice against the 64-row ("w1") and
+    96-row ("w3") LDS-DMA kernels and the 64-row register-ring kernel ("2x1x2"), forced with
+    dfx_gemm_force_tile.  Times from HIP events over `reps` calls after 3 warm-ups, the variants
+    measured in turn twice (the chip's clock drifts over a run); every variant checked to give the
+    built-in choice's bits."""
+    L = dfx.lib
+    rng = np.random.default_rng(5)
+    shapes = (("llada_head", 126464, 4096, (288, 256, 240, 181, 162, 120, 97, 74)),
+              ("llada_down", 4096, 12288, (256, 162, 97, 74)),
+              ("dream_head", 152064, 3584, (128, 64)), ("dream_down", 3584, 18944, (128, 64)))
+    out = []
+    for name, N, K, rows in shapes:
+        raw = dfx.quantize_rows(dfx.TYPE_Q6_K, rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+        w = dfx.Buf.of(dfx.repack(dfx.TYPE_Q6_K, raw, N, K))
+        del raw
+        for M in rows:
+            xb = dfx.Buf.of(rng.standard_normal((M, K), dtype=np.float32))
+            ab = dfx.Buf(L().dfx_act_bytes(dfx.TYPE_Q6_K, M, K))
+            dfx.check(L().dfx_act_convert(dfx.TYPE_Q6_K, xb.ptr, M, K, ab.ptr, None), "convert")
+            yb, ws = dfx.Buf(M * N * 4), dfx.Buf(L().dfx_gemm_ws_bytes(M, N, K))
+            res, ref, same = {}, None, True
+            for v in ("", "w1", "w3", "2x1x2") * 2:
+                dfx.check(L().dfx_gemm_force_tile(dfx.TYPE_Q6_K, v.encode() if v else None), "force")
+
+                def call():
+                    dfx.check(L().dfx_gemm(dfx.TYPE_Q6_K, w.ptr, N, K, ab.ptr, M, None, None, yb.ptr, ws.ptr, None),
+                              "gemm")
+                for _ in range(3):
+                    call()
+                tm, ms = C.c_void_p(), C.c_float()
+                dfx.check(L().dfx_timer_start(C.byref(tm), None), "timer")
+                for _ in range(reps):
+                    call()
+                dfx.check(L().dfx_timer_stop(tm, None, C.byref(ms)), "timer")
+                res.setdefault(v or "default", []).append(round(1000 * ms.value / reps, 2))
+                got = yb.download(np.float32, M * N)
+                if ref is None:
+                    ref = got
+                same = same and bool(np.array_equal(got, ref))
+            dfx.check(L().dfx_gemm_force_tile(dfx.TYPE_Q6_K, None), "force")
+            out.append({"gemm": name, "N": N, "K": K, "M": M, "us": res, "same_bits": same})
+            log(f"q6k tiles {name} M={M}: " + ", ".join(f"{k} {min(v)} us" for k, v in res.items()))
+    return out
+
+
 def sustained_mfma_rate():
     """The dense f16 rate this chip sustains: `mfma-rate` (back-to-back independent
     v_mfma_f32_32x32x16_f16 on one CU, then on every SIMD), run as a child process; None when
@@ -521,12 +569,18 @@ def main():
     ap.add_argument("--cpu-full", action="store_true",
                     help="only time one whole full-depth generation of the headline workload on the CPU oracle "
                          "(minutes of host time), print one JSON line and exit")
+    ap.add_argument("--q6k-tiles", action="store_true",
+                    help="only time the Q6_K GEMM's tile variants at the models' Q6_K shapes, print one JSON line "
+                         "and exit")
     ap.add_argument("--ceiling", action="store_true",
                     help="only measure the GEMM ceiling evidence (sustained MFMA rate, hipBLASLt f16 and the exact "
                          "Q4_K GEMM at the headline's shapes), print one JSON line and exit")
     args = ap.parse_args()
     if args.ceiling:
         print(json.dumps(ceiling()))
+        return
+    if args.q6k_tiles:
+        print(json.dumps({"q6k_tiles": q6k_tiles()}))
         return
     if args.only:
         runs = {"dream": config_dream, "sampler": config_sampler, "ar": config_ar,

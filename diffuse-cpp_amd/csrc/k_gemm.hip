@@ -2073,10 +2073,10 @@ static int launch_q6k_w(const void * w, int N, int K, const void * act, int M, c
 // than 64-row tiles (ties included), else 64-row tiles; at most 48 rows the register-ring
 // kernel (32 rows, 2-deep weight ring).  Split K when the grid is small.  Measured on MI355X at
 // the LLaDA-8B vocab head (126464 x 4096) and Q6_K down projection (4096 x 12288) and the
-// Dream-7B ones, every variant the same bits: 96-row tiles 10-30 % faster at 74, 162, 181 and
-// 288 rows, 25-50 % slower at 97 and 120 (192 rows of tiles against 128), even at 240 and
-// 2-20 % slower at 256 (288 against 256); the DMA kernel 2-5 % faster than the register ring at
-// 64-row tiles.  A forced tile "<TM>x<TN>[x<D>][s|n]" (dfx_gemm_force_tile) picks a
+// Dream-7B ones, every variant the same bits: 96-row tiles 10-33 % faster at 74, 162, 181 and
+// 288 rows, 25-50 % slower at 97, 120 and 128 (192 rows of tiles against 128), even at 240 and
+// 256 at the head, 20 % slower at 256 for the down projection; the DMA kernel 2-6 % faster than
+// the register ring at 64-row tiles.  A forced tile "<TM>x<TN>[x<D>][s|n]" (dfx_gemm_force_tile) picks a
 // register-ring tile, "w" / "w1" the 64-row and "w3" the 96-row DMA kernel.
 static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                         float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer,
