@@ -186,10 +186,12 @@ def cpu_full_generate(path, n_threads, host):
             "rows_per_step": [st.rows_per_step[i] for i in range(st.actual_steps)]}
 
 
-def config_llada_b64(model):
-    """LLaDA-8B Q4_K_M, 32 + 64 masks, low_confidence, no cache, 16 steps (96 rows a step)."""
+def config_llada_b64(model, launch="graphs"):
+    """LLaDA-8B Q4_K_M, 32 + 64 masks, low_confidence, no cache, 16 steps (96 rows a step).
+    launch "direct": the layer stacks launched kernel by kernel (for kernel traces)."""
     prompt = np.random.default_rng(1).integers(0, 126000, 32).astype(np.int32)
     ctx = dfx.Context(model, 96)
+    ctx.set_device_loop(True, graphs=launch == "graphs")
     params = dfx.SamplerParams.make(n_steps=16, remasking=dfx.LOW_CONFIDENCE, use_cache=False, seed=42)
     sec, st = time_generations(ctx, prompt, 64, params, 3, 1)
     ctx.close()
@@ -199,12 +201,14 @@ def config_llada_b64(model):
             "rows_per_step": [st.rows_per_step[i] for i in range(st.actual_steps)]}
 
 
-def config_dream():
-    """Dream-7B Q4_K_M, 64 + 64 masks, entropy_exit + cache, 16 steps."""
+def config_dream(launch="graphs"):
+    """Dream-7B Q4_K_M, 64 + 64 masks, entropy_exit + cache, 16 steps.  launch "direct": the
+    layer stacks launched kernel by kernel (for kernel traces)."""
     path = ensure_model("dream7b", dfx.DREAM_7B, "q4_k_m", 2)
     model = dfx.Model(path)
     prompt = np.random.default_rng(3).integers(0, 151643, 64).astype(np.int32)
     ctx = dfx.Context(model, 128)
+    ctx.set_device_loop(True, graphs=launch == "graphs")
     params = dfx.SamplerParams.make(n_steps=16, remasking=dfx.ENTROPY_EXIT, use_cache=True, seed=42,
                                     entropy_threshold=1.5)
     sec, st = time_generations(ctx, prompt, 64, params, 3, 1)
@@ -583,11 +587,11 @@ def main():
         print(json.dumps({"q6k_tiles": q6k_tiles()}))
         return
     if args.only:
-        runs = {"dream": config_dream, "sampler": config_sampler, "ar": config_ar,
+        runs = {"dream": lambda: config_dream(args.launch), "sampler": config_sampler, "ar": config_ar,
                 "batched_q8_0": lambda: config_batched("q8_0"), "batched_f16": lambda: config_batched("f16")}
         if args.only == "llada_b64":
             model = dfx.Model(ensure_model())
-            res = config_llada_b64(model)
+            res = config_llada_b64(model, args.launch)
             model.close()
         else:
             res = runs[args.only]()

@@ -1751,38 +1751,6 @@ __global__ void k_gemm_reduce(const float * __restrict__ ws, int S, int64_t MN, 
         }
         return;
     }
-    if (epi.kind == DFX_EPI_ROPE) {
-        // one element per thread: its chunk sums and its pair partner's (column n ^ 16)
-        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < MN; i += stride) {
-            const int64_t m = i / N;
-            const int n = (int)(i - m * N), np = n ^ 16;
-            float v = 0.0f, w = 0.0f;
-            for (int s = 0; s < S; s++) {
-                v = v + ws[(int64_t)s * MN + m * N + n];
-                w = w + ws[(int64_t)s * MN + m * N + np];
-            }
-            if (bias) {
-                v = v + bias[n];
-                w = w + bias[np];
-            }
-            const int p = epi.pos[m];
-            const int hd = epi.hd, half = hd >> 1;
-            const int g = n + epi.col0, hh = g / hd, cc = g - hh * hd;
-            if (hh < epi.H + epi.Hkv) {
-                const bool first = (cc & 16) == 0;
-                const int d0 = 16 * (cc >> 5) + (cc & 15), d = first ? d0 : half + d0;
-                const float2 cs = *(const float2 *)(epi.tab + ((int64_t)p * half + d0) * 2);
-                const float x0 = first ? v : w, x1 = first ? w : v;
-                const float y = first ? x0 * cs.x - x1 * cs.y : x0 * cs.y + x1 * cs.x;
-                float * dst = hh < epi.H ? epi.q_out + (m * epi.H + hh) * hd
-                                         : epi.kc + ((int64_t)p * epi.Hkv + (hh - epi.H)) * hd;
-                dst[d] = y;
-            } else {
-                epi.vt[((int64_t)(hh - epi.H - epi.Hkv) * hd + cc) * epi.v_ld + p] = v;
-            }
-        }
-        return;
-    }
     for (int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i0 < MN; i0 += REDUCE_R * stride) {
         int64_t idx[REDUCE_R];
         float v[REDUCE_R];
@@ -1890,10 +1858,72 @@ extern "C" size_t dfx_gemm_ws_bytes(int64_t M, int64_t N, int64_t K) {
 // Split-K epilogue: sums the S partial slices in ws (slice order) plus bias and residual
 // into Y, or, with defer, leaves the slices for the consumer of Y (the next RMSNorm,
 // which then adds them and the residual itself) and reports S.
+// The RoPE epilogue after split K, by tiles of 4 rows x 64 columns (whole NEOX pairs: a column's
+// partner n ^ 16 is in the same tile): each element's chunk sums (slice order) plus bias are read
+// once, along the columns, into LDS, where the partner's sum is taken from; Q and K are rotated
+// and stored along the columns, V along the rows of the transposed value cache.  Each element's
+// arithmetic is the element-wise reduction's.  Against one element (and its partner's sums) per
+// thread: Dream-7B generations 2.4 % faster in a same-box A/B (its Q|K|V at 12-64 rows splits K);
+// 8-, 16- and 32-row tiles gained 1.6, 0.4 and -2 %.
+#define RR_M 4
+#define RR_N 64
+__global__ void __launch_bounds__(256) k_gemm_reduce_rope(const float * __restrict__ ws, int S, int M, int N,
+                                                          const float * bias, dfx_epi epi) {
+#pragma clang fp contract(off)
+    __shared__ float tile[RR_M][RR_N + 1];
+    const int m0 = blockIdx.y * RR_M, n0 = blockIdx.x * RR_N, tid = threadIdx.x;
+    const int64_t MN = (int64_t)M * N;
+    // sums: thread (row r = tid / 64 + 4 i, column c = tid % 64), clamped reads, zero outside
+#pragma unroll
+    for (int i = 0; i < RR_M / 4; i++) {
+        const int r = tid / RR_N + 4 * i, c = tid % RR_N;
+        const int m = min(m0 + r, M - 1), n = min(n0 + c, N - 1);
+        float v = 0.0f;
+        for (int sl = 0; sl < S; sl++) v = v + ws[(int64_t)sl * MN + (int64_t)m * N + n];
+        if (bias) v = v + bias[n];
+        tile[r][c] = v;
+    }
+    __syncthreads();
+    const int hd = epi.hd, half = hd >> 1, qk_cols = (epi.H + epi.Hkv) * hd;
+    // Q and K: along the columns
+#pragma unroll
+    for (int i = 0; i < RR_M / 4; i++) {
+        const int r = tid / RR_N + 4 * i, c = tid % RR_N, m = m0 + r, n = n0 + c;
+        const int g = n + epi.col0;
+        if (m >= M || n >= N || g >= qk_cols) continue;
+        const int hh = g / hd, cc = g - hh * hd;
+        const bool first = (cc & 16) == 0;
+        const int d0 = 16 * (cc >> 5) + (cc & 15), d = first ? d0 : half + d0;
+        const int p = epi.pos[m];
+        const float2 cs = *(const float2 *)(epi.tab + ((int64_t)p * half + d0) * 2);
+        const float v = tile[r][c], w = tile[r][c ^ 16];
+        const float x0 = first ? v : w, x1 = first ? w : v;
+        const float y = first ? x0 * cs.x - x1 * cs.y : x0 * cs.y + x1 * cs.x;
+        float * dst = hh < epi.H ? epi.q_out + ((int64_t)m * epi.H + hh) * hd
+                                 : epi.kc + ((int64_t)p * epi.Hkv + (hh - epi.H)) * hd;
+        dst[d] = y;
+    }
+    // V: along the rows (transposed store)
+#pragma unroll
+    for (int i = 0; i < RR_N * RR_M / 256; i++) {
+        const int r = tid % RR_M, c = tid / RR_M + (256 / RR_M) * i, m = m0 + r, n = n0 + c;
+        const int g = n + epi.col0;
+        if (m >= M || n >= N || g < qk_cols) continue;
+        const int hh = g / hd, cc = g - hh * hd;
+        epi.vt[((int64_t)(hh - epi.H - epi.Hkv) * hd + cc) * epi.v_ld + epi.pos[m]] = tile[r][c];
+    }
+}
+
 static int reduce_or_defer(const void * ws, int S, int M, int N, const float * bias, const float * res, float * y,
                            int64_t ldy, const int32_t * ymap, hipStream_t st, int * defer, dfx_epi epi) {
     if (defer) {
         *defer = S;
+        return DFX_OK;
+    }
+    if (epi.kind == DFX_EPI_ROPE) {
+        const dim3 grid((unsigned)((N + RR_N - 1) / RR_N), (unsigned)((M + RR_M - 1) / RR_M));
+        hipLaunchKernelGGL(k_gemm_reduce_rope, grid, dim3(256), 0, st, (const float *)ws, S, M, N, bias, epi);
+        DFX_CHECK_LAUNCH("dfx_gemm reduce (RoPE)");
         return DFX_OK;
     }
     const int64_t MN = (int64_t)M * N;
