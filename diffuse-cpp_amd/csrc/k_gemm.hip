@@ -1855,9 +1855,6 @@ extern "C" size_t dfx_gemm_ws_bytes(int64_t M, int64_t N, int64_t K) {
     return (size_t)slices * M * N * sizeof(float);
 }
 
-// Split-K epilogue: sums the S partial slices in ws (slice order) plus bias and residual
-// into Y, or, with defer, leaves the slices for the consumer of Y (the next RMSNorm,
-// which then adds them and the residual itself) and reports S.
 // The RoPE epilogue after split K, by tiles of 4 rows x 64 columns (whole NEOX pairs: a column's
 // partner n ^ 16 is in the same tile): each element's chunk sums (slice order) plus bias are read
 // once, along the columns, into LDS, where the partner's sum is taken from; Q and K are rotated
@@ -1914,6 +1911,9 @@ __global__ void __launch_bounds__(256) k_gemm_reduce_rope(const float * __restri
     }
 }
 
+// Split-K epilogue: sums the S partial slices in ws (slice order) plus bias and residual
+// into Y, or, with defer, leaves the slices for the consumer of Y (the next RMSNorm,
+// which then adds them and the residual itself) and reports S.
 static int reduce_or_defer(const void * ws, int S, int M, int N, const float * bias, const float * res, float * y,
                            int64_t ldy, const int32_t * ymap, hipStream_t st, int * defer, dfx_epi epi) {
     if (defer) {
