@@ -347,7 +347,7 @@ def q6k_tiles(reps=10):
     """The Q6_K GEMM's tile choice at the Q6_K shapes of the benchmark models (LLaDA-8B vocab head
     126464 x 4096 and down projection 4096 x 12288, Dream-7B head 152064 x 3584 and down 3584 x
     18944) over the row counts their steps run: the built-in choice against the 64-row ("w1") and
-    96-row ("w3") LDS-DMA kernels and the 64-row register-ring kernel ("2x1x2"), forced with
+    96-row ("w3") LDS-DMA kernels and the 64- and 32-row register-ring kernels ("2x1x2", "1x1x2"), forced with
     dfx_gemm_force_tile.  Times from HIP events over `reps` calls after 3 warm-ups, the variants
     measured in turn twice (the chip's clock drifts over a run); every variant checked to give the
     built-in choice's bits."""
@@ -355,7 +355,8 @@ def q6k_tiles(reps=10):
     rng = np.random.default_rng(5)
     shapes = (("llada_head", 126464, 4096, (288, 256, 240, 181, 162, 120, 97, 74)),
               ("llada_down", 4096, 12288, (256, 162, 97, 74)),
-              ("dream_head", 152064, 3584, (128, 64)), ("dream_down", 3584, 18944, (128, 64)))
+              ("dream_head", 152064, 3584, (128, 64, 48, 40, 34, 24, 12)),
+              ("dream_down", 3584, 18944, (128, 64, 48, 34, 24)))
     out = []
     for name, N, K, rows in shapes:
         raw = dfx.quantize_rows(dfx.TYPE_Q6_K, rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
@@ -367,7 +368,7 @@ def q6k_tiles(reps=10):
             dfx.check(L().dfx_act_convert(dfx.TYPE_Q6_K, xb.ptr, M, K, ab.ptr, None), "convert")
             yb, ws = dfx.Buf(M * N * 4), dfx.Buf(L().dfx_gemm_ws_bytes(M, N, K))
             res, ref, same = {}, None, True
-            for v in ("", "w1", "w3", "2x1x2") * 2:
+            for v in ("", "w1", "w3", "2x1x2", "1x1x2") * 2:
                 dfx.check(L().dfx_gemm_force_tile(dfx.TYPE_Q6_K, v.encode() if v else None), "force")
 
                 def call():

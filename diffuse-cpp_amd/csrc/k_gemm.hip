@@ -2099,19 +2099,20 @@ static int launch_q6k_w(const void * w, int N, int K, const void * act, int M, c
     return DFX_OK;
 }
 
-// Q6_K: above 48 rows the LDS-DMA kernel, with 96-row tiles where they pad M to no more rows
-// than 64-row tiles (ties included), else 64-row tiles; at most 48 rows the register-ring
+// Q6_K: above 32 rows the LDS-DMA kernel, with 96-row tiles where they pad M to no more rows
+// than 64-row tiles (ties included), else 64-row tiles; at most 32 rows the register-ring
 // kernel (32 rows, 2-deep weight ring).  Split K when the grid is small.  Measured on MI355X at
 // the LLaDA-8B vocab head (126464 x 4096) and Q6_K down projection (4096 x 12288) and the
 // Dream-7B ones, every variant the same bits: 96-row tiles 10-33 % faster at 74, 162, 181 and
 // 288 rows, 25-50 % slower at 97, 120 and 128 (192 rows of tiles against 128), even at 240 and
 // 256 at the head, 20 % slower at 256 for the down projection; the DMA kernel 2-6 % faster than
-// the register ring at 64-row tiles.  A forced tile "<TM>x<TN>[x<D>][s|n]" (dfx_gemm_force_tile) picks a
+// the register ring at 64-row tiles; at 34-48 rows its 64-row tiles 10-30 % faster than two
+// 32-row tiles of the register ring (each weight dequantised once), at 12-24 rows 20 % slower.  A forced tile "<TM>x<TN>[x<D>][s|n]" (dfx_gemm_force_tile) picks a
 // register-ring tile, "w" / "w1" the 64-row and "w3" the 96-row DMA kernel.
 static int dispatch_q6k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                         float * y, int64_t ldy, const int32_t * ymap, void * ws, size_t ws_bytes, hipStream_t st, int * defer,
                         dfx_epi epi) {
-    bool dma = M > 48;
+    bool dma = M > 32;
     int tm = !dma ? 1 : (M + 95) / 96 * 96 <= (M + 63) / 64 * 64 ? 3 : 2, tn = 1;
     const int chunks = dot_chunks(K);
     const int64_t tiles = (int64_t)((M + 32 * tm - 1) / (32 * tm)) * ((N + 128 * tn - 1) / (128 * tn));
