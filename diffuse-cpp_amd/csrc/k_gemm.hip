@@ -595,15 +595,20 @@ __device__ __forceinline__ half8 mins_half8(uint32_t m4) {
     return __builtin_bit_cast(half8, r);
 }
 
-template <int TM, int TN, int D>
-__global__ void __launch_bounds__(256, TM * TN >= 4 ? 1 : 2)
+// NWV waves side by side (4: 128 weight rows per workgroup; 1 or 2 give narrow GEMMs over few
+// rows more workgroups than CUs would otherwise get); the second bound is waves per SIMD,
+// so the register budget does not depend on NWV.
+template <int TM, int TN, int D, int NWV = 4>
+__global__ void __launch_bounds__(64 * NWV, TM * TN >= 4 ? 1 : 2)
 k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__ act, int M,
       const float * __restrict__ bias, const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
       int n_tiles, int m_tiles, float * __restrict__ ws, dfx_epi epi) {
 #pragma clang fp contract(off)
-    constexpr int BM = TM * 32, BN = 4 * TN * 32;
+    constexpr int NT = 64 * NWV;             // threads per workgroup
+    constexpr int BM = TM * 32, BN = NWV * TN * 32;
     constexpr int BST = 24;                  // LDS halves per row of 16 block sums
-    constexpr int A_PER_T = BM * 16 / 256;   // 16-byte chunks of the A tile per thread
+    constexpr int A_PER_T = BM * 16 / NT;    // 16-byte chunks of the A tile per thread
+    static_assert(A_PER_T >= 1 && A_PER_T * NT == BM * 16 && NT >= 2 * BM, "A tile split over the threads");
     // A tile of one K step in fragment order: operand kk of row tile i at half (8i + kk) * 512
     __shared__ __attribute__((aligned(16))) half_t As[2][BM * 128];
     __shared__ __attribute__((aligned(16))) float Ad[2][BM];
@@ -639,7 +644,7 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
 #pragma unroll
     for (int i = 0; i < A_PER_T; i++) {
         // chunk c of the step: row tile c / 512 (clamped to the padded rows), 16 bytes c % 512
-        const int c = tid + 256 * i, mt = min(m0 / 32 + (c >> 9), m_pad / 32 - 1);
+        const int c = tid + NT * i, mt = min(m0 / 32 + (c >> 9), m_pad / 32 - 1);
         off_a[i] = (uint32_t)mt * (uint32_t)(K / 128) * 8192u + (uint32_t)(c & 511) * 16u;
     }
 #pragma unroll
@@ -706,7 +711,7 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
         // activation stage -> LDS
 #pragma unroll
         for (int i = 0; i < A_PER_T; i++) {
-            *(u32x4 *)(&As[buf][(tid + 256 * i) * 8]) = a_st[buf][i];
+            *(u32x4 *)(&As[buf][(tid + NT * i) * 8]) = a_st[buf][i];
         }
         if (h == 0) {
             // every thread stores (threads of the same row store the same value), so
@@ -1798,13 +1803,15 @@ __global__ void k_gemm_reduce(const float * __restrict__ ws, int S, int64_t MN, 
 // Forced tile of the Q4_K / Q6_K kernels, for tuning and tests:
 // "<TM>x<TN>[x<D>]" picks a register tile, "s" splits K when possible, "n" never
 // splits, "w" / "w1" / "w3" pick the LDS-DMA Q4_K kernel (64 x 64 / 64 x 32 / 96 x 32
-// per wave).
+// per wave), "v1" / "v2" run a Q4_K 32 x 32 register tile with one or two waves per
+// workgroup instead of four.
 // Set with dfx_gemm_force_tile; DFX_Q4K_TILE / DFX_Q6K_TILE are read once, at the
 // first GEMM launch or setter call.  Parsed once, not per launch.
 struct tile_force {
     bool on = false;
     int got = 0, tm = 0, tn = 0, d = 0;
     bool split = false, nosplit = false, w = false, w1 = false, w3 = false, halves = false;
+    int nwv = 4;   // "v<n>": waves per workgroup of a register-ring tile (1, 2 or 4)
 };
 static std::mutex g_force_mu;
 static tile_force g_force[2];   // [0] Q4_K, [1] Q6_K
@@ -1821,6 +1828,7 @@ static tile_force parse_force(const char * f) {
     t.w1 = strstr(f, "w1") != nullptr;
     t.w3 = strstr(f, "w3") != nullptr;
     t.halves = strchr(f, 'f') != nullptr;
+    if (const char * v = strchr(f, 'v')) t.nwv = atoi(v + 1);
     return t;
 }
 
@@ -1985,11 +1993,11 @@ static int launch_mmq(const void * w, int N, int K, const void * act, int M, con
     return DFX_OK;
 }
 
-template <int TM, int TN, int D>
+template <int TM, int TN, int D, int NWV = 4>
 static int launch_q4k(const void * w, int N, int K, const void * act, int M, const float * bias, const float * res,
                       float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st, int * defer,
                       dfx_epi epi) {
-    constexpr int BM = TM * 32, BN = 4 * TN * 32;
+    constexpr int BM = TM * 32, BN = NWV * TN * 32;
     const int n_tiles = (N + BN - 1) / BN, m_tiles = (M + BM - 1) / BM;
     const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
     const int chunks = dot_chunks(K), passes = ws ? chunks : 1;
@@ -2001,7 +2009,7 @@ static int launch_q4k(const void * w, int N, int K, const void * act, int M, con
         dfx_set_error("dfx_gemm q4_k: K=%d does not fit the pipeline depth %d", K, D);
         return DFX_ERR_ARG;
     }
-    hipLaunchKernelGGL((k_q4k<TM, TN, D>), dim3((unsigned)(per_pass * passes)), dim3(256), 0, st,
+    hipLaunchKernelGGL((k_q4k<TM, TN, D, NWV>), dim3((unsigned)(per_pass * passes)), dim3(64 * NWV), 0, st,
                        (const uint8_t *)w, N, K, (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles, ws, epi);
     DFX_CHECK_LAUNCH("dfx_gemm q4_k");
     if (ws) return reduce_or_defer(ws, chunks, M, N, bias, res, y, ldy, ymap, st, defer, epi);
@@ -2203,10 +2211,29 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
     } else {
         split = can_split && (chunks > 2 || (int64_t)n_col * ((M + 63) / 64) < 160);
     }
-    // A forced tile "<TM>x<TN>[x<D>][s|n]" (dfx_gemm_force_tile) overrides the choice:
-    // s = split K when possible, n = never split.
+    // Narrow GEMMs over at most 64 rows: 32 x 32 register tiles in workgroups of one or two
+    // waves where four-wave workgroups would leave CUs idle or fill a second round only in
+    // part (LLaDA-8B and Dream-7B O, Q|K|V and down at 12-64 rows: 3-13 % faster; slower where
+    // the four-wave grid fills the chip once, as LLaDA-8B's down projection does):
+    //   at most two chunks, when twice the four-wave split grid fits one workgroup per CU:
+    //     two waves, 2-deep ring, split K;
+    //   more chunks, with 256 to 512 workgroups of one 32- or 64-row tile per column tile and
+    //     chunk: one wave up to 32 rows, two above, 2-deep ring, split K.
+    int nwv = 4;
+    if (narrow && M <= 64 && can_split) {
+        const int64_t g4 = (int64_t)n_col * ((M + 31) / 32) * chunks, g1 = (int64_t)n_col * chunks;
+        if (chunks <= 2 ? 2 * g4 <= 256 : g1 > 256 && g1 < 512) {
+            nwv = chunks > 2 && M <= 32 ? 1 : 2;
+            dma = false;
+            pick = C_1x1x2;
+            split = true;
+        }
+    }
+    // A forced tile "<TM>x<TN>[x<D>][s|n][v1|v2]" (dfx_gemm_force_tile) overrides the choice:
+    // s = split K when possible, n = never split, v = waves per workgroup.
     const tile_force f = forced_tile(0);
     if (f.on) {
+        nwv = f.nwv;
         if (f.got >= 2) {
             dma = false;
             for (int c = n_cand - 1; c >= 0; c--)
@@ -2271,6 +2298,13 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
         for (int c = 0; c < n_cand; c++)
             if (cands[c].tm == cands[pick].tm && cands[c].tn == cands[pick].tn && cands[c].d == 2) { pick = c; break; }
     float * wsf = split ? (float *)ws : nullptr;
+    if ((nwv == 1 || nwv == 2) && cands[pick].tm == 1 && cands[pick].tn == 1) {
+        if (nwv == 1)
+            return cands[pick].d == 4 ? launch_q4k<1, 1, 4, 1>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi)
+                                      : launch_q4k<1, 1, 2, 1>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi);
+        return cands[pick].d == 4 ? launch_q4k<1, 1, 4, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi)
+                                  : launch_q4k<1, 1, 2, 2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi);
+    }
 #define Q4K_CASE(c, TM_, TN_, D_) \
     case c: return launch_q4k<TM_, TN_, D_>(w, N, K, act, M, bias, res, y, ldy, ymap, wsf, st, defer, epi);
     switch (pick) {

@@ -135,7 +135,11 @@ GEMM_CASES = [(dfx.TYPE_Q4_K, 4096, 4096, m) for m in (1, 5, 50, 96, 128, 255, 2
     (dfx.TYPE_Q4_K, 24576, 4096, 288), (dfx.TYPE_Q6_K, 126464, 4096, 288),
     # Dream-7B: fused Q|K|V, gate|up, down, vocab head (steps of 128 and 64 rows)
     (dfx.TYPE_Q4_K, 4608, 3584, 128), (dfx.TYPE_Q4_K, 37888, 3584, 64), (dfx.TYPE_Q4_K, 3584, 18944, 128),
-    (dfx.TYPE_Q6_K, 152064, 3584, 64)]
+    (dfx.TYPE_Q6_K, 152064, 3584, 64),
+    # narrow GEMMs over few rows: one-wave (down at 24 rows) and two-wave workgroups (down at
+    # 48 rows, O at 40, Q|K|V at 20)
+    (dfx.TYPE_Q4_K, 3584, 18944, 24), (dfx.TYPE_Q4_K, 3584, 18944, 48), (dfx.TYPE_Q4_K, 3584, 3584, 40),
+    (dfx.TYPE_Q4_K, 4608, 3584, 20)]
 
 
 @contextlib.contextmanager
@@ -168,7 +172,8 @@ def test_gemm_quantized_bit_exact(gpu, typ, N, K, M):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
 
 
-@pytest.mark.parametrize("tile", ["2x2x2", "4x1x2", "2x1x2", "1x1x4", "1x1x2", "2x1x4", "2x2x4", "w", "w1", "w3"])
+@pytest.mark.parametrize("tile", ["2x2x2", "4x1x2", "2x1x2", "1x1x4", "1x1x2", "2x1x4", "2x2x4", "w", "w1", "w3",
+                                  "1x1x4v1", "1x1x2v1", "1x1x4v2", "1x1x2v2"])
 @pytest.mark.parametrize("N,K,M", [(1000, 2048, 77), (4096, 4096, 288)])
 def test_gemm_q4k_every_tile_bit_exact(gpu, tile, N, K, M):
     """Every register tile of the Q4_K kernel (forced with dfx_gemm_force_tile), with ragged
@@ -181,7 +186,7 @@ def test_gemm_q4k_every_tile_bit_exact(gpu, tile, N, K, M):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
 
 
-@pytest.mark.parametrize("tile", ["1x1x4s", "2x1x2s", "2x1x4s", "ws", "w1s", "w3s"])
+@pytest.mark.parametrize("tile", ["1x1x4s", "2x1x2s", "2x1x4s", "ws", "w1s", "w3s", "1x1x4v1s", "1x1x2v2s"])
 @pytest.mark.parametrize("N,K,M", [(512, 12288, 70), (1000, 3584, 33), (640, 2304, 40), (4096, 4096, 256)])
 def test_gemm_q4k_split_k_bit_exact(gpu, tile, N, K, M):
     """Split K (one workgroup per 2048-element chunk, chunk sums added in order by the
