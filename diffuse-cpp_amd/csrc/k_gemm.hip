@@ -820,23 +820,25 @@ k_q4k(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__
 // ---------------------------------------------------------------------------
 // Q4_K over few rows, super-blocks side by side.  Over 12-96 rows the K loop of k_q4k is a
 // chain of K steps, each waiting on a barrier and on its MFMAs, with few waves to hide
-// either.  Here a workgroup of eight waves computes one 32 x 32 output tile, one chunk of
-// 2048 at a time (or one chunk only, z, with ws): wave w takes super-block w of the chunk,
-// forms its integer sums with the same 16 + 1 MFMAs as k_q4k and
-// x = fma(-dmin_w, msum, d_w * isum), and leaves x and the rows' d_a in LDS; wave 0 then adds
-// the chunk's super-blocks in order, S = fma(d_a, x, S), and T = T + S.  The operations and
-// their order are k_q4k's, so the bits are the same; a chunk costs the latency of one
-// super-block instead of eight.  Activation fragments are read straight from the
-// operand-order buffer (every 64-lane read is one contiguous KB).
-__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
+// either.  Here a workgroup of eight waves computes TN 32 x 32 output tiles side by side, one
+// chunk of 2048 at a time (or one chunk only, z, with ws): wave w takes super-block w of the
+// chunk, loads its activation fragments once (straight from the operand-order buffer, one
+// contiguous KB per 64-lane load) for all TN tiles, forms each tile's integer sums with the
+// same 16 + 1 MFMAs as k_q4k and x = fma(-dmin_w, msum, d_w * isum), and leaves x and the rows'
+// d_a in LDS; wave t then adds tile t's super-blocks in chunk order, S = fma(d_a, x, S), and
+// T = T + S.  The operations and their order are k_q4k's, so the bits are the same; a chunk
+// costs the latency of one super-block instead of eight.  TN = 1: two workgroups per CU;
+// TN = 2 / 4 read the activations half / a quarter as often, one workgroup per CU.
+template <int TN>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(TN == 1 ? 4 : 2)))
 k_q4k_sb(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restrict__ act, int M,
          const float * __restrict__ bias, const float * res, float * Y, int64_t ldy, const int32_t * __restrict__ ymap,
          int n_tiles, int m_tiles, float * __restrict__ ws, dfx_epi epi) {
 #pragma clang fp contract(off)
     constexpr int NW = 8, SBC = DFX_DOT_CHUNK / 256;
     static_assert(SBC == NW, "one wave per super-block of a chunk");
-    __shared__ __attribute__((aligned(16))) float4 X[NW][4][64];   // x of super-block w: registers 4q..4q+3 of a lane
-    __shared__ __attribute__((aligned(16))) float Dl[NW][32];      // d_a of super-block w, rows m0..m0+31
+    extern __shared__ __attribute__((aligned(16))) float4 X[];   // [NW][TN][4][64]: x of super-block w, tile t
+    float * Dl = (float *)(X + NW * TN * 4 * 64);                 // [NW][32]: d_a of super-block w, rows m0..
 
     // tile order as k_q4k: column tile x on XCD x % 8, its row tiles and chunks there too
     const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
@@ -845,7 +847,7 @@ k_q4k_sb(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restric
     if (tx >= n_tiles) return;
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, hl = lane >> 5, l32 = lane & 31;
-    const int n0 = tx * 32, m0 = ty * 32;
+    const int n0 = tx * 32 * TN, m0 = ty * 32;
     const int n_sb_all = K >> 8, n_chunks = (n_sb_all + SBC - 1) / SBC;
     const uint32_t row_bytes = (uint32_t)n_sb_all * SB_Q4_K;
     const act_layout Lay = act_layout_of(CONV_Q8_K_P4, M, K);
@@ -853,7 +855,6 @@ k_q4k_sb(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restric
     const uint8_t * Aq = act + Lay.q + (size_t)(m0 / 32) * (size_t)(K / 128) * 8192 + (size_t)lane * 16;
     const float * Adg = (const float *)(act + Lay.d);
     const uint8_t * Absg = act + Lay.bs;
-    const uint8_t * wrow = W + (size_t)min(n0 + l32, N - 1) * row_bytes;
     const int m_bs = min(m0 + l32, M - 1);
     const uint32_t MASK_LO = opaque(0x000F000Fu), MASK_HI = opaque(0x00F000F0u), MAGIC = opaque(0x64006400u);
     const float16v zero16 = {};
@@ -865,13 +866,16 @@ k_q4k_sb(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restric
         if (wv < nsb) {
             const int sb = sb0 + wv;
             // every load of the super-block issued before the first use
-            const uint8_t * wb = wrow + (size_t)sb * SB_Q4_K;
-            const u32x4 hdr = *(const u32x4 *)wb;
-            u32x4 q[2][2];
+            u32x4 hdr[TN], q[TN][2][2];
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                q[h][0] = *(const u32x4 *)(wb + 16 + 32 * (2 * h + hl));
-                q[h][1] = *(const u32x4 *)(wb + 32 + 32 * (2 * h + hl));
+            for (int t = 0; t < TN; t++) {
+                const uint8_t * wb = W + (size_t)min(n0 + 32 * t + l32, N - 1) * row_bytes + (size_t)sb * SB_Q4_K;
+                hdr[t] = *(const u32x4 *)wb;
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    q[t][h][0] = *(const u32x4 *)(wb + 16 + 32 * (2 * h + hl));
+                    q[t][h][1] = *(const u32x4 *)(wb + 32 + 32 * (2 * h + hl));
+                }
             }
             half8 a[2][8];
 #pragma unroll
@@ -881,40 +885,46 @@ k_q4k_sb(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restric
             const half8 bsa = *(const half8 *)(Absg + ((size_t)m_bs * (size_t)(K / 16) + (size_t)sb * 16 + 8 * hl) * 2);
             const float dav = Adg[(size_t)sb * m_pad + m_bs];
 
-            const q4k_sm sm = q4k_unpack(hdr);
-            float16v P = zero16;
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const q4k_consts kc = q4k_group_consts(h == 0 ? sm.sc_lo : sm.sc_hi, 16 * hl);
+            for (int t = 0; t < TN; t++) {
+                const q4k_sm sm = q4k_unpack(hdr[t]);
+                float16v P = zero16;
 #pragma unroll
-                for (int kk = 0; kk < 8; kk++) {
-                    const half8 b = q4k_word(q[h][kk >> 2][kk & 3], kc, MASK_LO, MASK_HI, MAGIC);
-                    P = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[h][kk], b, (h == 0 && kk == 0) ? zero16 : P, 0, 0, 0);
+                for (int h = 0; h < 2; h++) {
+                    const q4k_consts kc = q4k_group_consts(h == 0 ? sm.sc_lo : sm.sc_hi, 16 * hl);
+#pragma unroll
+                    for (int kk = 0; kk < 8; kk++) {
+                        const half8 b = q4k_word(q[t][h][kk >> 2][kk & 3], kc, MASK_LO, MASK_HI, MAGIC);
+                        P = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[h][kk], b, (h == 0 && kk == 0) ? zero16 : P, 0, 0,
+                                                                   0);
+                    }
                 }
+                const float16v Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(bsa, mins_half8(hl ? sm.mn_hi : sm.mn_lo),
+                                                                          zero16, 0, 0, 0);
+                const float dw = h2f((uint16_t)(hdr[t].x & 0xFFFFu)), dmw = h2f((uint16_t)(hdr[t].x >> 16));
+                float x[16];
+#pragma unroll
+                for (int r = 0; r < 16; r++) x[r] = dw * P[r];
+                pass_barrier(x);
+#pragma unroll
+                for (int r = 0; r < 16; r++) x[r] = fmaf(-dmw, Q[r], x[r]);
+#pragma unroll
+                for (int q4 = 0; q4 < 4; q4++)
+                    X[((wv * TN + t) * 4 + q4) * 64 + lane] = make_float4(x[4 * q4], x[4 * q4 + 1], x[4 * q4 + 2],
+                                                                          x[4 * q4 + 3]);
             }
-            const float16v Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(bsa, mins_half8(hl ? sm.mn_hi : sm.mn_lo),
-                                                                      zero16, 0, 0, 0);
-            const float dw = h2f((uint16_t)(hdr.x & 0xFFFFu)), dmw = h2f((uint16_t)(hdr.x >> 16));
-            float x[16];
-#pragma unroll
-            for (int r = 0; r < 16; r++) x[r] = dw * P[r];
-            pass_barrier(x);
-#pragma unroll
-            for (int r = 0; r < 16; r++) x[r] = fmaf(-dmw, Q[r], x[r]);
-#pragma unroll
-            for (int q4 = 0; q4 < 4; q4++) X[wv][q4][lane] = make_float4(x[4 * q4], x[4 * q4 + 1], x[4 * q4 + 2], x[4 * q4 + 3]);
-            if (hl == 0) Dl[wv][l32] = dav;
+            if (hl == 0) Dl[wv * 32 + l32] = dav;
         }
         __syncthreads();
-        if (wv == 0) {
-            // the chunk's super-blocks in order: S = fma(d_a, x, S), then T = T + S
+        if (wv < TN) {
+            // tile wv: the chunk's super-blocks in order, S = fma(d_a, x, S), then T = T + S
             float16v S = zero16;
             for (int w = 0; w < nsb; w++) {
                 float da[16], xv[16];
 #pragma unroll
                 for (int q4 = 0; q4 < 4; q4++) {
-                    const float4 d4 = *(const float4 *)(&Dl[w][8 * q4 + 4 * hl]);
-                    const float4 x4 = X[w][q4][lane];
+                    const float4 d4 = *(const float4 *)(&Dl[w * 32 + 8 * q4 + 4 * hl]);
+                    const float4 x4 = X[((w * TN + wv) * 4 + q4) * 64 + lane];
                     da[4 * q4] = d4.x; da[4 * q4 + 1] = d4.y; da[4 * q4 + 2] = d4.z; da[4 * q4 + 3] = d4.w;
                     xv[4 * q4] = x4.x; xv[4 * q4 + 1] = x4.y; xv[4 * q4 + 2] = x4.z; xv[4 * q4 + 3] = x4.w;
                 }
@@ -925,7 +935,7 @@ k_q4k_sb(const uint8_t * __restrict__ W, int N, int K, const uint8_t * __restric
         }
         if (c + 1 < c_end) __syncthreads();   // X and Dl are refilled by the next chunk
     }
-    if (wv == 0) epilogue_tile(T, m0, n0 + l32, M, N, bias, res, Y, ldy, ymap, ws, z, lane, epi);
+    if (wv < TN) epilogue_tile(T, m0, n0 + 32 * wv + l32, M, N, bias, res, Y, ldy, ymap, ws, z, lane, epi);
 }
 
 // ---------------------------------------------------------------------------
@@ -1922,6 +1932,7 @@ struct tile_force {
     bool on = false;
     int got = 0, tm = 0, tn = 0, d = 0;
     bool split = false, nosplit = false, w = false, w1 = false, w3 = false, halves = false, sbp = false;
+    int sbtn = 1;   // "k<n>": column tiles per workgroup of the super-block-parallel kernel (1, 2 or 4)
     int nwv = 4;   // "v<n>": waves per workgroup of a register-ring tile (1, 2 or 4)
 };
 static std::mutex g_force_mu;
@@ -1939,7 +1950,11 @@ static tile_force parse_force(const char * f) {
     t.w1 = strstr(f, "w1") != nullptr;
     t.w3 = strstr(f, "w3") != nullptr;
     t.halves = strchr(f, 'f') != nullptr;
-    t.sbp = strchr(f, 'k') != nullptr;
+    if (const char * k = strchr(f, 'k')) {
+        t.sbp = true;
+        const int v = atoi(k + 1);
+        t.sbtn = v == 2 || v == 4 ? v : 1;
+    }
     if (const char * v = strchr(f, 'v')) t.nwv = atoi(v + 1);
     return t;
 }
@@ -2128,16 +2143,27 @@ static int launch_q4k(const void * w, int N, int K, const void * act, int M, con
     return DFX_OK;
 }
 
-// Super-block-parallel Q4_K (k_q4k_sb): eight waves per 32 x 32 tile; with ws, one
+// Super-block-parallel Q4_K (k_q4k_sb): eight waves per 32 x (32 TN) tile; with ws, one
 // workgroup per chunk and the chunk sums added by the reduction (or by the caller).
+template <int TN>
 static int launch_q4k_sb(const void * w, int N, int K, const void * act, int M, const float * bias,
                          const float * res, float * y, int64_t ldy, const int32_t * ymap, float * ws, hipStream_t st,
                          int * defer, dfx_epi epi) {
-    const int n_tiles = (N + 31) / 32, m_tiles = (M + 31) / 32;
+    const int n_tiles = (N + 32 * TN - 1) / (32 * TN), m_tiles = (M + 31) / 32;
     const int per_pass = 8 * ((n_tiles + 7) / 8) * m_tiles;
     const int chunks = dot_chunks(K);
     if (chunks == 1) ws = nullptr;
-    hipLaunchKernelGGL(k_q4k_sb, dim3((unsigned)(per_pass * (ws ? chunks : 1))), dim3(512), 0, st,
+    const size_t lds = (size_t)8 * TN * 4 * 64 * 16 + 8 * 32 * 4;
+    static std::once_flag once;
+    static hipError_t attr = hipSuccess;
+    std::call_once(once, [lds] {
+        attr = hipFuncSetAttribute((const void *)k_q4k_sb<TN>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    });
+    if (attr != hipSuccess) {
+        dfx_set_error("dfx_gemm q4_k: %zu bytes of LDS refused: %s", lds, hipGetErrorString(attr));
+        return DFX_ERR_HIP;
+    }
+    hipLaunchKernelGGL(k_q4k_sb<TN>, dim3((unsigned)(per_pass * (ws ? chunks : 1))), dim3(512), lds, st,
                        (const uint8_t *)w, N, K, (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles,
                        ws, epi);
     DFX_CHECK_LAUNCH("dfx_gemm q4_k");
@@ -2379,17 +2405,20 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
     // 64 + 64 generation 4.2 % faster; slower over many chunks or many column tiles, where
     // every tile re-reads the activations.
     if (!f.on && chunks <= 2 && M <= 96 && (int64_t)((N + 31) / 32) * ((M + 31) / 32) <= 432)
-        return launch_q4k_sb(w, N, K, act, M, bias, res, y, ldy, ymap, defer && can_split ? (float *)ws : nullptr,
-                             st, defer, epi);
+        return launch_q4k_sb<1>(w, N, K, act, M, bias, res, y, ldy, ymap, defer && can_split ? (float *)ws : nullptr,
+                                st, defer, epi);
     // a 4-deep ring needs a multiple of 4 K steps in every workgroup
     const int sb = K / 256, sb_last = sb - (chunks - 1) * (DFX_DOT_CHUNK / 256);
     // whole and half tiles in one launch (k_q4k_w): two chunks, tile counters, and room in ws
     // for both halves' chunk totals
     const bool halves_ok = epi.tile_cnt && chunks == 2 && N % 128 == 0 && ws &&
                            ws_bytes >= (size_t)2 * M * N * sizeof(float);
-    if (f.on && f.sbp)
-        return launch_q4k_sb(w, N, K, act, M, bias, res, y, ldy, ymap, f.split && can_split ? (float *)ws : nullptr,
-                             st, defer, epi);
+    if (f.on && f.sbp) {
+        float * wsk = f.split && can_split ? (float *)ws : nullptr;
+        if (f.sbtn == 4) return launch_q4k_sb<4>(w, N, K, act, M, bias, res, y, ldy, ymap, wsk, st, defer, epi);
+        if (f.sbtn == 2) return launch_q4k_sb<2>(w, N, K, act, M, bias, res, y, ldy, ymap, wsk, st, defer, epi);
+        return launch_q4k_sb<1>(w, N, K, act, M, bias, res, y, ldy, ymap, wsk, st, defer, epi);
+    }
     if (f.on && f.w) {
         // "w": 64 x 64 per wave; "w1": 64 x 32 per wave, two workgroups per CU
         float * wsw = split ? (float *)ws : nullptr;

@@ -173,7 +173,7 @@ def test_gemm_quantized_bit_exact(gpu, typ, N, K, M):
 
 
 @pytest.mark.parametrize("tile", ["2x2x2", "4x1x2", "2x1x2", "1x1x4", "1x1x2", "2x1x4", "2x2x4", "w", "w1", "w3",
-                                  "1x1x4v1", "1x1x2v1", "1x1x4v2", "1x1x2v2", "k", "ks"])
+                                  "1x1x4v1", "1x1x2v1", "1x1x4v2", "1x1x2v2", "k", "ks", "k2", "k4"])
 @pytest.mark.parametrize("N,K,M", [(1000, 2048, 77), (4096, 4096, 288)])
 def test_gemm_q4k_every_tile_bit_exact(gpu, tile, N, K, M):
     """Every register tile of the Q4_K kernel (forced with dfx_gemm_force_tile), with ragged
@@ -186,7 +186,7 @@ def test_gemm_q4k_every_tile_bit_exact(gpu, tile, N, K, M):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rel_l2(got, ref)
 
 
-@pytest.mark.parametrize("tile", ["1x1x4s", "2x1x2s", "2x1x4s", "ws", "w1s", "w3s", "1x1x4v1s", "1x1x2v2s", "ks"])
+@pytest.mark.parametrize("tile", ["1x1x4s", "2x1x2s", "2x1x4s", "ws", "w1s", "w3s", "1x1x4v1s", "1x1x2v2s", "ks", "k4s"])
 @pytest.mark.parametrize("N,K,M", [(512, 12288, 70), (1000, 3584, 33), (640, 2304, 40), (4096, 4096, 256)])
 def test_gemm_q4k_split_k_bit_exact(gpu, tile, N, K, M):
     """Split K (one workgroup per 2048-element chunk, chunk sums added in order by the
@@ -316,7 +316,7 @@ def oracle_swiglu(g, u):
     (dfx.TYPE_Q4_K, 1024, 4096, 130, "w"), (dfx.TYPE_Q4_K, 1024, 4096, 130, "ws"),
     (dfx.TYPE_Q4_K, 1024, 3584, 150, "w3"), (dfx.TYPE_Q4_K, 512, 12288, 5, "1x1x4s"),
     (dfx.TYPE_Q4_K, 2048, 4096, 1, None), (dfx.TYPE_Q4_K, 1024, 4096, 4, None), (dfx.TYPE_Q6_K, 512, 4096, 2, None),
-    (dfx.TYPE_Q6_K, 512, 12288, 40, "2x1s"), (dfx.TYPE_Q4_K, 512, 12288, 40, "ks"), (dfx.TYPE_Q4_K, 512, 3584, 70, "k"),
+    (dfx.TYPE_Q6_K, 512, 12288, 40, "2x1s"), (dfx.TYPE_Q4_K, 512, 12288, 40, "ks"), (dfx.TYPE_Q4_K, 512, 3584, 70, "k"), (dfx.TYPE_Q4_K, 768, 4096, 50, "k4"),
     (dfx.TYPE_Q6_K, 512, 4096, 66, "2x1n"), (dfx.TYPE_Q8_0, 512, 4096, 33, None),
     (dfx.TYPE_F16, 512, 4096, 33, None), (dfx.TYPE_F32, 256, 512, 20, None)])
 def test_gemm_swiglu_epilogue_bit_exact(gpu, typ, F, K, M, tile):
@@ -375,7 +375,7 @@ def rope_row_order(H, Hkv, hd):
     (dfx.TYPE_Q4_K, 4, 4, 128, 4096, 150, "w3", False), (dfx.TYPE_Q4_K, 6, 2, 64, 4096, 40, "2x1x2s", True),
     (dfx.TYPE_Q4_K, 4, 2, 128, 4096, 200, "ws", False), (dfx.TYPE_Q4_K, 8, 8, 128, 4096, 3, None, False),
     (dfx.TYPE_Q4_K, 4, 2, 128, 3584, 1, None, True), (dfx.TYPE_Q6_K, 4, 4, 64, 4096, 2, None, False),
-    (dfx.TYPE_Q4_K, 4, 2, 128, 3584, 50, "ks", True), (dfx.TYPE_Q4_K, 6, 2, 64, 4096, 40, "k", True),
+    (dfx.TYPE_Q4_K, 4, 2, 128, 3584, 50, "ks", True), (dfx.TYPE_Q4_K, 6, 2, 64, 4096, 40, "k", True), (dfx.TYPE_Q4_K, 4, 2, 128, 4096, 74, "k2s", True),
     (dfx.TYPE_Q6_K, 4, 2, 128, 4096, 66, "2x1s", True), (dfx.TYPE_Q6_K, 4, 4, 64, 2048, 100, "2x1n", False),
     (dfx.TYPE_Q8_0, 4, 2, 128, 2048, 33, None, True), (dfx.TYPE_F16, 4, 1, 128, 2048, 45, None, True),
     (dfx.TYPE_F32, 2, 1, 64, 512, 20, None, False)])
