@@ -173,8 +173,9 @@ int dfx_gemm_rope(int wtype, const void * w, int64_t N, int64_t K, const void * 
  * process (tuning and tests; every choice gives the same bits): "<TM>x<TN>[x<D>]" picks a
  * register tile, "s" splits K where possible, "n" never splits, "w" / "w1" / "w3" pick the
  * Q4_K LDS-DMA kernel (w3: 96 rows per tile), "v1" / "v2" a Q4_K 32-row register tile in
- * workgroups of one or two waves, "k" the Q4_K super-block-parallel kernel ("ks": K split at
- * chunk borders); NULL or "" restores the built-in choice.
+ * workgroups of one or two waves, "k" / "k2" / "k4" the Q4_K super-block-parallel kernel over
+ * 1, 2 or 4 column tiles per workgroup ("ks": K split at chunk borders); NULL or "" restores
+ * the built-in choice.
  * DFX_Q4K_TILE and DFX_Q6K_TILE in the environment are read once, before the first call.
  * No counterpart in the reference (GGML has no tile choice). */
 int dfx_gemm_force_tile(int wtype, const char * spec);
