@@ -228,6 +228,27 @@ k_attn_mfma(const float * __restrict__ q, const float * __restrict__ kc, const f
     }
     __syncthreads();
 
+    // The first value steps of phase 3 are loaded here, so that their latency passes under the
+    // softmax.  Value column of this lane for column tile ct: 16*wv + 16*NW*ct + li; keys
+    // 16s+4g..+3.
+    const float * vb = vt + ((int64_t)kvh * HD + 16 * wv + li) * v_ld + 4 * lg;
+    auto load_v = [&](float4 (&vf)[CT], int s) {
+        const int n = 16 * s + 4 * lg;                 // first of this lane's 4 keys
+#pragma unroll
+        for (int ct = 0; ct < CT; ct++) {
+            const float * p = vb + (int64_t)16 * NW * ct * v_ld + 16 * min(s, ntiles - 1);
+            // v_ld and n are multiples of 4 and n_keys <= v_ld: the load stays in the row;
+            // keys past the end of the sequence count as 0
+            const f32x4 v = *(const f32x4 *)p;
+            vf[ct] = make_float4(n < n_keys ? v.x : 0.0f, n + 1 < n_keys ? v.y : 0.0f, n + 2 < n_keys ? v.z : 0.0f,
+                                 n + 3 < n_keys ? v.w : 0.0f);
+        }
+    };
+    constexpr int PV = 4;                           // value steps in flight
+    float4 vq[PV][CT];
+#pragma unroll
+    for (int u = 0; u < PV; u++) load_v(vq[u], u);
+
     // ---- phase 2: the wave's RPW rows (wv, wv + NW, ..) together, four keys per lane and
     // row at a time, so that RPW * 4 exponentials and the rows' reductions are in flight at
     // once.  Each lane sums its keys lane, lane + 64, .. in increasing order and the lanes
@@ -294,24 +315,6 @@ k_attn_mfma(const float * __restrict__ q, const float * __restrict__ kc, const f
     double4v o[CT][2];                              // chains: column tile x MFMA parity
 #pragma unroll
     for (int ct = 0; ct < CT; ct++) o[ct][0] = o[ct][1] = 0.0;
-    // value column of this lane for column tile ct: 16*wv + 16*NW*ct + li; keys 16s+4g..+3
-    const float * vb = vt + ((int64_t)kvh * HD + 16 * wv + li) * v_ld + 4 * lg;
-    auto load_v = [&](float4 (&vf)[CT], int s) {
-        const int n = 16 * s + 4 * lg;                 // first of this lane's 4 keys
-#pragma unroll
-        for (int ct = 0; ct < CT; ct++) {
-            const float * p = vb + (int64_t)16 * NW * ct * v_ld + 16 * min(s, ntiles - 1);
-            // v_ld and n are multiples of 4 and n_keys <= v_ld: the load stays in the row;
-            // keys past the end of the sequence count as 0
-            const f32x4 v = *(const f32x4 *)p;
-            vf[ct] = make_float4(n < n_keys ? v.x : 0.0f, n + 1 < n_keys ? v.y : 0.0f, n + 2 < n_keys ? v.z : 0.0f,
-                                 n + 3 < n_keys ? v.w : 0.0f);
-        }
-    };
-    constexpr int PV = 4;                           // value steps in flight
-    float4 vq[PV][CT];
-#pragma unroll
-    for (int u = 0; u < PV; u++) load_v(vq[u], u);
     for (int s0 = 0; s0 < ntiles; s0 += PV) {
 #pragma unroll
         for (int u = 0; u < PV; u++) {
