@@ -149,23 +149,27 @@ __device__ __forceinline__ double4v mfma_f64(double a, double b, double4v c) {
 // Every output element's sums are the same for every NW: the wave count only decides which
 // wave computes them.  With eight waves (and at most 128 VGPRs) two workgroups share a CU
 // at four waves per SIMD, and each workgroup finishes in about half the time of four waves.
-// Workgroups are numbered so that all query tiles of head h run on XCD h % 8.
+// Workgroups are numbered so that all query tiles of head h run on XCD h % 8.  With vs = 2
+// (grids that leave CUs idle) each query tile runs as two workgroups that both form the scores
+// and probabilities and take half of the value columns each (phase 3 on half the waves): the
+// same operations for every output element, so the same bits.
 template <int HD, int KR, int NW>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 4 : 1)))
 k_attn_mfma(const float * __restrict__ q, const float * __restrict__ kc, const float * __restrict__ vt, int64_t v_ld,
             int M, int n_keys, int H, int Hkv, int sstride, int q_tiles, int q_pos0, int window,
-            float * __restrict__ out) {
+            float * __restrict__ out, int vs) {
 #pragma clang fp contract(off)
     extern __shared__ float S[];       // [16][sstride] scores, then probabilities
     constexpr int SS = HD / 16;        // reduction steps of 16 head dims
     constexpr int CT = HD / (16 * NW); // phase-3 column tiles per wave
     static_assert(CT >= 1 && CT * 16 * NW == HD, "head dims split evenly over the waves");
-    const int L = blockIdx.x, xcd = L & 7, j = L >> 3;
-    const int h = 8 * (j / q_tiles) + xcd, qt = j % q_tiles;
+    const int L = blockIdx.x, xcd = L & 7, j = L >> 3, slots = q_tiles * vs;
+    const int h = 8 * (j / slots) + xcd, qt = (j % slots) / vs, part = (j % slots) % vs;
     if (h >= H) return;
     const int kvh = h / (H / Hkv);
     const int q0 = qt * 16;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const bool pv = (wv * vs) / NW == part;   // this wave's value columns are this workgroup's
     const int li = lane & 15, lg = lane >> 4;
     const int64_t kvstride = (int64_t)Hkv * HD;
     const float scale = 1.0f / sqrtf((float)HD);
@@ -246,8 +250,9 @@ k_attn_mfma(const float * __restrict__ q, const float * __restrict__ kc, const f
     };
     constexpr int PV = 4;                           // value steps in flight
     float4 vq[PV][CT];
+    if (pv)
 #pragma unroll
-    for (int u = 0; u < PV; u++) load_v(vq[u], u);
+        for (int u = 0; u < PV; u++) load_v(vq[u], u);
 
     // ---- phase 2: the wave's RPW rows (wv, wv + NW, ..) together, four keys per lane and
     // row at a time, so that RPW * 4 exponentials and the rows' reductions are in flight at
@@ -312,6 +317,7 @@ k_attn_mfma(const float * __restrict__ q, const float * __restrict__ kc, const f
     __syncthreads();
 
     // ---- phase 3
+    if (!pv) return;
     double4v o[CT][2];                              // chains: column tile x MFMA parity
 #pragma unroll
     for (int ct = 0; ct < CT; ct++) o[ct][0] = o[ct][1] = 0.0;
@@ -913,6 +919,19 @@ extern "C" int dfx_rope_store(const float * qkv, const int32_t * pos, int64_t M,
     return DFX_OK;
 }
 
+// Compute units of the current device, read once per device.
+static int attn_cu_count() {
+    static std::atomic<int> cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int v = cached[dev].load(std::memory_order_relaxed);
+    if (!v) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cached[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
 // LDS a workgroup may use on the current device (160 KB on gfx950), read once per device
 // (contexts on several host threads may ask at once).
 static size_t attn_lds_limit() {
@@ -961,18 +980,23 @@ static int attn_exact(const float * q, const float * kc, const float * vt, int64
     const size_t lds = (size_t)16 * sstride * sizeof(float);
     const int q_tiles = (M + 15) / 16;
     const dim3 grid((unsigned)(8 * ((H + 7) / 8) * q_tiles));
+    // value columns split over two workgroups per query tile where twice the grid still gives
+    // each CU at most one workgroup (LLaDA-8B at 50 rows, Dream-7B at 12-64 rows: 11-12 % less
+    // attention time; slower on larger grids, where the second workgroup shares a CU)
+    const int vs = 2 * (int)grid.x <= attn_cu_count() ? 2 : 1;
+    const dim3 grid_vs((unsigned)(8 * ((H + 7) / 8) * q_tiles * vs));
     if (lds <= attn_lds_limit()) {
         // 128 dims: eight waves, a one-slot key ring (at most 128 VGPRs: four waves per SIMD);
         // 64 dims: four waves, three slots
         if (hd == 128 && ATTN_NW == 8)
-            hipLaunchKernelGGL((k_attn_mfma<128, 1, 8>), grid, dim3(512), lds, st, q, kc, vt, v_ld, M, n_keys, H, Hkv,
-                               sstride, q_tiles, q_pos0, window, out);
+            hipLaunchKernelGGL((k_attn_mfma<128, 1, 8>), grid_vs, dim3(512), lds, st, q, kc, vt, v_ld, M, n_keys, H, Hkv,
+                               sstride, q_tiles, q_pos0, window, out, vs);
         else if (hd == 128)
-            hipLaunchKernelGGL((k_attn_mfma<128, 2, 4>), grid, dim3(256), lds, st, q, kc, vt, v_ld, M, n_keys, H, Hkv,
-                               sstride, q_tiles, q_pos0, window, out);
+            hipLaunchKernelGGL((k_attn_mfma<128, 2, 4>), grid_vs, dim3(256), lds, st, q, kc, vt, v_ld, M, n_keys, H, Hkv,
+                               sstride, q_tiles, q_pos0, window, out, vs);
         else
-            hipLaunchKernelGGL((k_attn_mfma<64, 3, 4>), grid, dim3(256), lds, st, q, kc, vt, v_ld, M, n_keys, H, Hkv,
-                               sstride, q_tiles, q_pos0, window, out);
+            hipLaunchKernelGGL((k_attn_mfma<64, 3, 4>), grid_vs, dim3(256), lds, st, q, kc, vt, v_ld, M, n_keys, H, Hkv,
+                               sstride, q_tiles, q_pos0, window, out, vs);
     } else if (hd == 128) {   // score rows longer than the LDS holds: recomputed in three passes
         hipLaunchKernelGGL((k_attn_long<128>), grid, dim3(256), 0, st, q, kc, vt, v_ld, M, n_keys, H, Hkv, q_tiles,
                            q_pos0, window, out);
