@@ -2384,6 +2384,14 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
             split = true;
         }
     }
+    // Wide GEMMs over at most 32 rows (gate|up): two waves per workgroup, 2-deep ring, K split
+    // where the workspace allows (Dream-7B's gate|up at 12-32 rows 29.2-29.4 -> 25.8-29.1 us,
+    // LLaDA-8B's 23.5-24.1 -> 21.9-22.2 us).
+    if (!narrow && M <= 32 && !dma) {
+        nwv = 2;
+        pick = C_1x1x2;
+        split = can_split;
+    }
     // A forced tile "<TM>x<TN>[x<D>][s|n][v1|v2]" (dfx_gemm_force_tile) overrides the choice:
     // s = split K when possible, n = never split, v = waves per workgroup.
     const tile_force f = forced_tile(0);
