@@ -2154,14 +2154,18 @@ static int launch_q4k_sb(const void * w, int N, int K, const void * act, int M, 
     const int chunks = dot_chunks(K);
     if (chunks == 1) ws = nullptr;
     const size_t lds = (size_t)8 * TN * 4 * 64 * 16 + 8 * 32 * 4;
-    static std::once_flag once;
-    static hipError_t attr = hipSuccess;
-    std::call_once(once, [lds] {
-        attr = hipFuncSetAttribute((const void *)k_q4k_sb<TN>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    });
-    if (attr != hipSuccess) {
-        dfx_set_error("dfx_gemm q4_k: %zu bytes of LDS refused: %s", lds, hipGetErrorString(attr));
-        return DFX_ERR_HIP;
+    if (lds > 64 * 1024) {
+        // above the default limit of dynamic LDS (TN >= 2: the forced tuning forms only)
+        static std::once_flag once;
+        static hipError_t attr = hipSuccess;
+        std::call_once(once, [lds] {
+            attr = hipFuncSetAttribute((const void *)k_q4k_sb<TN>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+        });
+        if (attr != hipSuccess) {
+            dfx_set_error("dfx_gemm q4_k: %zu bytes of LDS refused: %s", lds, hipGetErrorString(attr));
+            return DFX_ERR_HIP;
+        }
     }
     hipLaunchKernelGGL(k_q4k_sb<TN>, dim3((unsigned)(per_pass * (ws ? chunks : 1))), dim3(512), lds, st,
                        (const uint8_t *)w, N, K, (const uint8_t *)act, M, bias, res, y, ldy, ymap, n_tiles, m_tiles,
