@@ -392,6 +392,58 @@ def q6k_tiles(reps=10):
     return out
 
 
+def q4k_small_tiles(reps=10):
+    """The Q4_K GEMM's forms over 12-96 rows at the Q4_K shapes of the benchmark models (Dream-7B
+    Q|K|V 4608 x 3584, O 3584 x 3584, gate|up 37888 x 3584, down 3584 x 18944; LLaDA-8B Q|K|V
+    12288 x 4096, O 4096 x 4096, gate|up 24576 x 4096, down 4096 x 12288): the built-in choice
+    against the four-wave 32-row register ring ("1x1x4"), its two- and one-wave forms with split K
+    ("1x1x2v2s", "1x1x2v1s"), the super-block-parallel kernel whole-K and split ("k", "ks") and the
+    64-row LDS-DMA tile ("w1"), forced with dfx_gemm_force_tile.  dfx_gemm with a workspace (a
+    split's reduction is launched and timed; the engine defers the O and down projections'
+    reductions into the next RMSNorm).  Times from HIP events over `reps` calls after 3 warm-ups,
+    the variants measured in turn twice; every variant checked to give the built-in choice's bits."""
+    L = dfx.lib
+    rng = np.random.default_rng(5)
+    shapes = (("dream_qkv", 4608, 3584), ("dream_o", 3584, 3584), ("dream_gateup", 37888, 3584),
+              ("dream_down", 3584, 18944), ("llada_qkv", 12288, 4096), ("llada_o", 4096, 4096),
+              ("llada_gateup", 24576, 4096), ("llada_down", 4096, 12288))
+    variants = ("", "1x1x4", "1x1x2v2s", "1x1x2v1s", "k", "ks", "w1")
+    out = []
+    for name, N, K in shapes:
+        raw = dfx.quantize_rows(dfx.TYPE_Q4_K, rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+        w = dfx.Buf.of(dfx.repack(dfx.TYPE_Q4_K, raw, N, K))
+        del raw
+        for M in (12, 32, 48, 64, 96):
+            xb = dfx.Buf.of(rng.standard_normal((M, K), dtype=np.float32))
+            ab = dfx.Buf(L().dfx_act_bytes(dfx.TYPE_Q4_K, M, K))
+            dfx.check(L().dfx_act_convert(dfx.TYPE_Q4_K, xb.ptr, M, K, ab.ptr, None), "convert")
+            yb, ws = dfx.Buf(M * N * 4), dfx.Buf(L().dfx_gemm_ws_bytes(M, N, K))
+            res, ref, same = {}, None, True
+            for v in variants * 2:
+                dfx.check(L().dfx_gemm_force_tile(dfx.TYPE_Q4_K, v.encode() if v else None), "force")
+
+                def call():
+                    dfx.check(L().dfx_gemm(dfx.TYPE_Q4_K, w.ptr, N, K, ab.ptr, M, None, None, yb.ptr, ws.ptr, None),
+                              "gemm")
+                for _ in range(3):
+                    call()
+                tm, ms = C.c_void_p(), C.c_float()
+                dfx.check(L().dfx_timer_start(C.byref(tm), None), "timer")
+                for _ in range(reps):
+                    call()
+                dfx.check(L().dfx_timer_stop(tm, None, C.byref(ms)), "timer")
+                res.setdefault(v or "default", []).append(round(1000 * ms.value / reps, 2))
+                got = yb.download(np.float32, M * N)
+                if ref is None:
+                    ref = got
+                same = same and bool(np.array_equal(got, ref))
+            dfx.check(L().dfx_gemm_force_tile(dfx.TYPE_Q4_K, None), "force")
+            out.append({"gemm": name, "N": N, "K": K, "M": M, "us": res, "same_bits": same,
+                        "weight_gbs_default": round(N * K * 144 / 256 / (min(res["default"]) * 1e-6) / 1e9, 1)})
+            log(f"q4k small tiles {name} M={M}: " + ", ".join(f"{k} {min(v)} us" for k, v in res.items()))
+    return out
+
+
 def sustained_mfma_rate():
     """The dense f16 rate this chip sustains: `mfma-rate` (back-to-back independent
     v_mfma_f32_32x32x16_f16 on one CU, then on every SIMD), run as a child process; None when
@@ -577,6 +629,9 @@ def main():
     ap.add_argument("--q6k-tiles", action="store_true",
                     help="only time the Q6_K GEMM's tile variants at the models' Q6_K shapes, print one JSON line "
                          "and exit")
+    ap.add_argument("--q4k-small-tiles", action="store_true",
+                    help="only time the Q4_K GEMM's forms over 12-96 rows at the models' Q4_K shapes, print one "
+                         "JSON line and exit")
     ap.add_argument("--ceiling", action="store_true",
                     help="only measure the GEMM ceiling evidence (sustained MFMA rate, hipBLASLt f16 and the exact "
                          "Q4_K GEMM at the headline's shapes), print one JSON line and exit")
@@ -586,6 +641,9 @@ def main():
         return
     if args.q6k_tiles:
         print(json.dumps({"q6k_tiles": q6k_tiles()}))
+        return
+    if args.q4k_small_tiles:
+        print(json.dumps({"q4k_small_tiles": q4k_small_tiles()}))
         return
     if args.only:
         runs = {"dream": lambda: config_dream(args.launch), "sampler": config_sampler, "ar": config_ar,
