@@ -2333,10 +2333,10 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
     //   M <= 48 (outside the sweep, weight-bandwidth-bound): 32x128, 4-deep ring, split
     //     K while the grid leaves the SIMDs short of a wave each.
     // The choice only changes speed: every variant gives the same bits.
-    //   32 < M <= 48, wide (at least 160 column tiles) or over more than two chunks: the
-    //     64-row DMA tile (every weight dequantised once for all rows), K split only over
-    //     many chunks (Dream-7B gate|up and down at 34-48 rows: 15-18 % faster than 32-row
-    //     tiles);
+    //   32 < M <= 48, not narrow or over more than two chunks: the 64-row DMA tile (every
+    //     weight dequantised once for all rows), K split over many chunks or on grids under
+    //     160 column tiles (Dream-7B gate|up and down at 34-48 rows: 15-18 % faster than 32-row
+    //     tiles; LLaDA-8B Q|K|V at 48 rows 23.3 -> 19.5 us);
     //   64 < M <= 96, unless narrow over at most two chunks: one 96-row tile (k_q4k_w<3, 1, 2>),
     //     K split over many chunks or on grids under 160 workgroups (LLaDA-8B Q|K|V, gate|up
     //     and down at 74 and 96 rows: 2-15 % faster than 64-row tiles).
@@ -2349,8 +2349,8 @@ static int dispatch_q4k(const void * w, int N, int K, const void * act, int M, c
     int pick = C_2x1x2;   // register-ring 64x128 (when the DMA kernel is not used)
     bool dma = true, split = false, rows96 = false;
     if (M <= 48) {
-        if (M > 32 && (n_col >= 160 || chunks > 2)) {
-            split = can_split && chunks > 2;
+        if (M > 32 && (!narrow || chunks > 2)) {
+            split = can_split && (chunks > 2 || n_col < 160);
         } else {
             dma = false;
             pick = C_1x1x4;
