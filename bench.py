@@ -254,19 +254,22 @@ def config_ar(reps=3):
             "decode_weight_gbs": round(gbs, 1), "decode_frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4)}
 
 
-def config_batched(scheme="q8_0"):
+def config_batched(scheme="q8_0", launch="graphs"):
     """The batched long-context workload: 8 independent sequences of a 512-token prompt + B=256
     masks on LLaDA-8B (Q8_0 or F16 weights, seed 5), 16 steps, low_confidence with the
     inter-step cache (the header's default policy).  The sequences run at the same time, one
     context each (own stream) on one shared model, from 8 host threads; tok/s = 8 x 256 / the
     wall time of the whole batch.  One warm-up batch, then one timed batch; a single sequence
-    alone is timed beside it."""
+    alone is timed beside it.  launch "direct": the layer stacks launched kernel by kernel (for
+    kernel traces)."""
     import threading
     path = ensure_model("llada8b", dfx.LLADA_8B, scheme, 5)
     model = dfx.Model(path)
     S, P, Bm = 8, 512, 256
     prompts = [np.random.default_rng(50 + i).integers(0, 126000, P).astype(np.int32) for i in range(S)]
     ctxs = [dfx.Context(model, P + Bm) for _ in range(S)]
+    for c in ctxs:
+        c.set_device_loop(True, graphs=launch == "graphs")
     params = dfx.SamplerParams.make(n_steps=16, remasking=dfx.LOW_CONFIDENCE, use_cache=True, seed=42)
     stats = [dfx.GenStats() for _ in range(S)]
 
@@ -647,7 +650,8 @@ def main():
         return
     if args.only:
         runs = {"dream": lambda: config_dream(args.launch), "sampler": config_sampler, "ar": config_ar,
-                "batched_q8_0": lambda: config_batched("q8_0"), "batched_f16": lambda: config_batched("f16")}
+                "batched_q8_0": lambda: config_batched("q8_0", args.launch),
+                "batched_f16": lambda: config_batched("f16", args.launch)}
         if args.only == "llada_b64":
             model = dfx.Model(ensure_model())
             res = config_llada_b64(model, args.launch)
