@@ -139,7 +139,10 @@ GEMM_CASES = [(dfx.TYPE_Q4_K, 4096, 4096, m) for m in (1, 5, 50, 96, 128, 255, 2
     # narrow GEMMs over few rows: one-wave (down at 24 rows) and two-wave workgroups (down at
     # 48 rows, O at 40, Q|K|V at 20)
     (dfx.TYPE_Q4_K, 3584, 18944, 24), (dfx.TYPE_Q4_K, 3584, 18944, 48), (dfx.TYPE_Q4_K, 3584, 3584, 40),
-    (dfx.TYPE_Q4_K, 4608, 3584, 20)]
+    (dfx.TYPE_Q4_K, 4608, 3584, 20),
+    # wide GEMMs over few rows: two-wave register tiles with split K (24 rows), 64-row DMA tiles with
+    # split K on a mid-width grid (40 rows)
+    (dfx.TYPE_Q4_K, 37888, 3584, 24), (dfx.TYPE_Q4_K, 12288, 4096, 40)]
 
 
 @contextlib.contextmanager
