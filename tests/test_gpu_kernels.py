@@ -319,6 +319,7 @@ def oracle_swiglu(g, u):
     (dfx.TYPE_Q4_K, 1024, 4096, 130, "w"), (dfx.TYPE_Q4_K, 1024, 4096, 130, "ws"),
     (dfx.TYPE_Q4_K, 1024, 3584, 150, "w3"), (dfx.TYPE_Q4_K, 512, 12288, 5, "1x1x4s"),
     (dfx.TYPE_Q4_K, 2048, 4096, 1, None), (dfx.TYPE_Q4_K, 1024, 4096, 4, None), (dfx.TYPE_Q6_K, 512, 4096, 2, None),
+    (dfx.TYPE_Q4_K, 2688, 3584, 24, None),   # wide, few rows: two-wave tiles, split K, SwiGLU in the reduction
     (dfx.TYPE_Q6_K, 512, 12288, 40, "2x1s"), (dfx.TYPE_Q4_K, 512, 12288, 40, "ks"), (dfx.TYPE_Q4_K, 512, 3584, 70, "k"), (dfx.TYPE_Q4_K, 768, 4096, 50, "k4"),
     (dfx.TYPE_Q6_K, 512, 4096, 66, "2x1n"), (dfx.TYPE_Q8_0, 512, 4096, 33, None),
     (dfx.TYPE_F16, 512, 4096, 33, None), (dfx.TYPE_F32, 256, 512, 20, None)])
